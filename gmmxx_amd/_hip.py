@@ -1,0 +1,308 @@
+"""ctypes boundary to libgmmxx_hip.so (the HIP/gfx950 EM engine).
+
+Role of the reference's ``gmmxx/_cuda.py`` (:1-1416) for the ``"hip"``
+backend: validate tensors, pass raw device pointers and the current HIP stream
+across the C ABI declared in ``include/gmmxx_hip.h``, and turn status codes
+into Python exceptions.  There is no fallback path: if the library is missing
+or a call fails, the caller gets an exception (``HipBackendUnavailable`` /
+``HipRuntimeError``), never a silent CPU or PyTorch result.
+
+Workspace and output tensors are allocated here through PyTorch's caching
+allocator and handed to the library, which itself never allocates.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Tuple
+
+import torch
+
+_LIB_NAME = "libgmmxx_hip.so"
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
+ABI_VERSION = 1
+
+COV_CODES = {"spherical": 0, "diag": 1, "tied": 2, "full": 3}
+_DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1}
+
+
+class HipBackendUnavailable(RuntimeError):
+    """The HIP library is not built/loadable, or no GPU is visible
+    (role of CudaBackendUnavailable, gmmxx/_cuda.py:35-36)."""
+
+
+class HipRuntimeError(RuntimeError):
+    """A library call returned a nonzero status (the message comes from
+    gmmxx_hip_last_error).  Role of CudaRuntimeFallback (gmmxx/_cuda.py:39-41),
+    except that nothing falls back: the error propagates to the caller."""
+
+
+class _Problem(ctypes.Structure):
+    _fields_ = [("covariance_type", ctypes.c_int32), ("x_dtype", ctypes.c_int32),
+                ("B", ctypes.c_int64), ("N", ctypes.c_int64), ("D", ctypes.c_int64),
+                ("K", ctypes.c_int64)]
+
+
+_lib = None
+_load_error: Optional[BaseException] = None
+
+
+def _declare(lib):
+    P = ctypes.POINTER(_Problem)
+    vp, i64, f64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_double, ctypes.c_int32
+    sig = {
+        "gmmxx_hip_abi_version": (ctypes.c_int, []),
+        "gmmxx_hip_last_error": (ctypes.c_char_p, []),
+        "gmmxx_hip_canary": (ctypes.c_int, [vp, vp, i64, i32, vp]),
+        "gmmxx_hip_supported": (ctypes.c_int, [P]),
+        "gmmxx_hip_workspace_bytes": (i64, [P]),
+        "gmmxx_hip_em_step": (ctypes.c_int, [P, vp, vp, vp, vp, vp, f64, f64, vp, vp, i64, vp]),
+        "gmmxx_hip_estep_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, vp, i64, vp]),
+        "gmmxx_hip_score": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
+        "gmmxx_hip_predict_proba": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, i64, vp]),
+        "gmmxx_hip_gram": (ctypes.c_int, [P, vp, vp, vp, i64, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def exported_symbols() -> Tuple[str, ...]:
+    return ("gmmxx_hip_abi_version", "gmmxx_hip_last_error", "gmmxx_hip_canary",
+            "gmmxx_hip_supported", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step",
+            "gmmxx_hip_estep_stats", "gmmxx_hip_score", "gmmxx_hip_predict_proba",
+            "gmmxx_hip_gram")
+
+
+def load_library(path: Optional[str] = None):
+    """Loads (once) and returns the ctypes handle; raises HipBackendUnavailable."""
+    global _lib, _load_error
+    if _lib is not None and path is None:
+        return _lib
+    p = path or os.environ.get("GMMXX_HIP_LIBRARY", _LIB_PATH)
+    try:
+        lib = _declare(ctypes.CDLL(p, mode=ctypes.RTLD_LOCAL))
+    except OSError as exc:
+        _load_error = exc
+        raise HipBackendUnavailable(
+            f"cannot load {p}: {exc}. Build it with `python -m gmmxx_amd.build`.") from exc
+    ver = lib.gmmxx_hip_abi_version()
+    if ver != ABI_VERSION:
+        raise HipBackendUnavailable(f"{p} has ABI version {ver}, expected {ABI_VERSION}")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def library_loaded() -> bool:
+    return _lib is not None
+
+
+def has_hip() -> bool:
+    """True iff the library loads and a GPU is visible (role of has_cuda, gmmxx/_cuda.py:44-46)."""
+    if not torch.cuda.is_available():
+        return False
+    try:
+        load_library()
+    except HipBackendUnavailable:
+        return False
+    return True
+
+
+def require_hip() -> None:
+    """Raises HipBackendUnavailable unless the engine can run (gmmxx/_cuda.py:57-64)."""
+    load_library()
+    if not torch.cuda.is_available():
+        raise HipBackendUnavailable("no ROCm GPU is visible to PyTorch")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = _lib.gmmxx_hip_last_error().decode(errors="replace")
+        raise HipRuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def problem(covariance_type: str, x_dtype: torch.dtype, B: int, N: int, D: int, K: int) -> _Problem:
+    if covariance_type not in COV_CODES:
+        raise ValueError(f"unknown covariance_type {covariance_type!r}")
+    if x_dtype not in _DTYPE_CODES:
+        raise ValueError(f"x dtype must be float32 or bfloat16, got {x_dtype}")
+    return _Problem(COV_CODES[covariance_type], _DTYPE_CODES[x_dtype], int(B), int(N), int(D), int(K))
+
+
+def supported(covariance_type: str, x_dtype: torch.dtype, B: int, N: int, D: int, K: int) -> bool:
+    """Shape/dtype gate of the engine, answered by the library itself."""
+    if x_dtype not in _DTYPE_CODES or covariance_type not in COV_CODES:
+        return False
+    lib = load_library()
+    return bool(lib.gmmxx_hip_supported(ctypes.byref(problem(covariance_type, x_dtype, B, N, D, K))))
+
+
+def _device_tensor(t: torch.Tensor, name: str, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    if not torch.is_tensor(t):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name}: must be on a GPU device, got {t.device}")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name}: dtype must be {dtype}, got {t.dtype}")
+    return t.contiguous()
+
+
+class Workspace:
+    """Device scratch for one problem shape, sized by the library (256-byte aligned)."""
+
+    def __init__(self, prob: _Problem, device: torch.device):
+        lib = load_library()
+        nbytes = int(lib.gmmxx_hip_workspace_bytes(ctypes.byref(prob)))
+        if nbytes < 0:
+            raise HipRuntimeError("problem not supported by the HIP engine: "
+                                  + lib.gmmxx_hip_last_error().decode(errors="replace"))
+        self._buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+        base = self._buf.data_ptr()
+        self.ptr = ctypes.c_void_p(base + (-base) % 256)
+        self.nbytes = nbytes
+
+
+def _shape(x: torch.Tensor, means: torch.Tensor) -> Tuple[int, int, int, int]:
+    if x.ndim != 3:
+        raise ValueError("x must have shape (B, N, D)")
+    if means.ndim != 3 or means.shape[0] != x.shape[0] or means.shape[2] != x.shape[2]:
+        raise ValueError("means must have shape (B, K, D) matching x")
+    return int(x.shape[0]), int(x.shape[1]), int(x.shape[2]), int(means.shape[1])
+
+
+def _cov_shape(cov: str, B: int, K: int, D: int) -> Tuple[int, ...]:
+    return {"spherical": (B, K), "diag": (B, K, D), "tied": (B, D, D), "full": (B, K, D, D)}[cov]
+
+
+def _check_params(cov, means, covs, weights, B, K, D):
+    if tuple(covs.shape) != _cov_shape(cov, B, K, D):
+        raise ValueError(f"{cov} covariances must have shape {_cov_shape(cov, B, K, D)}, got {tuple(covs.shape)}")
+    if tuple(weights.shape) != (B, K):
+        raise ValueError(f"weights must have shape {(B, K)}, got {tuple(weights.shape)}")
+
+
+# ---------------------------------------------------------------------------
+# Operations
+# ---------------------------------------------------------------------------
+
+def canary_add_offset(inp: torch.Tensor, offset: int) -> torch.Tensor:
+    """out = inp + offset on the GPU (role of gmmxx/_cuda.py canary_add_offset)."""
+    require_hip()
+    inp = _device_tensor(inp, "input", torch.int32)
+    out = torch.empty_like(inp)
+    _check(_lib.gmmxx_hip_canary(_ptr(inp), _ptr(out), inp.numel(), int(offset), _stream(inp.device)),
+           "gmmxx_hip_canary")
+    return out
+
+
+def gram(x: torch.Tensor, ws: Optional[Workspace] = None) -> torch.Tensor:
+    """XᵀX per batch, (B, D, D) fp32."""
+    require_hip()
+    x = _device_tensor(x, "x", torch.float32)
+    B, N, D = x.shape
+    prob = problem("tied", x.dtype, B, N, D, 1)
+    ws = ws or Workspace(prob, x.device)
+    out = torch.empty((B, D, D), dtype=torch.float32, device=x.device)
+    _check(_lib.gmmxx_hip_gram(ctypes.byref(prob), _ptr(x), _ptr(out), ws.ptr, ws.nbytes, _stream(x.device)),
+           "gmmxx_hip_gram")
+    return out
+
+
+def em_step(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+            weights: torch.Tensor, lower_bound_out: torch.Tensor, *, reg_covar: float = 1e-6,
+            min_weight: float = 1e-8, gram_xx: Optional[torch.Tensor] = None,
+            ws: Optional[Workspace] = None) -> None:
+    """One in-place soft-EM iteration on (means, covs, weights); fp32 contiguous
+    device tensors.  ``lower_bound_out`` (1 float, device) receives the mean
+    log-likelihood under the entry parameters."""
+    require_hip()
+    x = _device_tensor(x, "x")
+    B, N, D, K = _shape(x, means)
+    for t, nm in ((means, "means"), (covs, "covariances"), (weights, "weights"), (lower_bound_out, "lower_bound")):
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise ValueError(f"{nm} must be a contiguous float32 GPU tensor")
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    ws = ws or Workspace(prob, x.device)
+    if covariance_type == "tied" and gram_xx is None:
+        raise ValueError("tied EM needs gram_xx = XᵀX")
+    _check(_lib.gmmxx_hip_em_step(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
+                                  _ptr(gram_xx), float(reg_covar), float(min_weight), _ptr(lower_bound_out),
+                                  ws.ptr, ws.nbytes, _stream(x.device)), "gmmxx_hip_em_step")
+
+
+def estep_stats(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+                weights: torch.Tensor, *, reg_covar: float = 1e-6, min_weight: float = 1e-8,
+                ws: Optional[Workspace] = None):
+    """Sufficient statistics of one E-step: (nk, sum_x, sum_q, ll_sum)."""
+    require_hip()
+    x = _device_tensor(x, "x")
+    means = _device_tensor(means, "means", torch.float32)
+    covs = _device_tensor(covs, "covariances", torch.float32)
+    weights = _device_tensor(weights, "weights", torch.float32)
+    B, N, D, K = _shape(x, means)
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    ws = ws or Workspace(prob, x.device)
+    dev = x.device
+    nk = torch.empty((B, K), dtype=torch.float32, device=dev)
+    sum_x = torch.empty((B, K, D), dtype=torch.float32, device=dev)
+    q_shape = {"spherical": (B, K), "diag": (B, K, D), "full": (B, K, D, D)}.get(covariance_type)
+    sum_q = torch.empty(q_shape, dtype=torch.float32, device=dev) if q_shape else None
+    ll = torch.empty((1,), dtype=torch.float32, device=dev)
+    _check(_lib.gmmxx_hip_estep_stats(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
+                                      float(reg_covar), float(min_weight), _ptr(nk), _ptr(sum_x), _ptr(sum_q),
+                                      _ptr(ll), ws.ptr, ws.nbytes, _stream(dev)), "gmmxx_hip_estep_stats")
+    return nk, sum_x, sum_q, ll
+
+
+def score(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+          weights: torch.Tensor, *, want_scores: bool = True, want_labels: bool = True,
+          ws: Optional[Workspace] = None):
+    """Per-sample log-likelihood (B, N) fp32 and/or first-max labels (B, N) int64."""
+    require_hip()
+    x = _device_tensor(x, "x")
+    means = _device_tensor(means, "means", torch.float32)
+    covs = _device_tensor(covs, "covariances", torch.float32)
+    weights = _device_tensor(weights, "weights", torch.float32)
+    B, N, D, K = _shape(x, means)
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    ws = ws or Workspace(prob, x.device)
+    scores = torch.empty((B, N), dtype=torch.float32, device=x.device) if want_scores else None
+    labels = torch.empty((B, N), dtype=torch.int64, device=x.device) if want_labels else None
+    _check(_lib.gmmxx_hip_score(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
+                                _ptr(scores), _ptr(labels), ws.ptr, ws.nbytes, _stream(x.device)),
+           "gmmxx_hip_score")
+    return scores, labels
+
+
+def predict_proba(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+                  weights: torch.Tensor, *, ws: Optional[Workspace] = None) -> torch.Tensor:
+    """Responsibilities (B, N, K) fp32."""
+    require_hip()
+    x = _device_tensor(x, "x")
+    means = _device_tensor(means, "means", torch.float32)
+    covs = _device_tensor(covs, "covariances", torch.float32)
+    weights = _device_tensor(weights, "weights", torch.float32)
+    B, N, D, K = _shape(x, means)
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    ws = ws or Workspace(prob, x.device)
+    out = torch.empty((B, N, K), dtype=torch.float32, device=x.device)
+    _check(_lib.gmmxx_hip_predict_proba(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
+                                        _ptr(out), ws.ptr, ws.nbytes, _stream(x.device)),
+           "gmmxx_hip_predict_proba")
+    return out

@@ -1,0 +1,366 @@
+// C-ABI entry points of libgmmxx_hip.so (declared in include/gmmxx_hip.h).
+//
+// Each call plans the launch geometry for the problem, carves the caller's
+// workspace, and enqueues the kernels of one operation on the caller's stream.
+// Nothing is allocated and nothing synchronises.
+
+#include <stdint.h>
+
+#include <algorithm>
+#include <string>
+
+#include "common.hpp"
+#include "engine.hpp"
+#include "gmmxx_hip.h"
+#include "params.hpp"
+
+namespace {
+
+using namespace gx;
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+struct Plan {
+  int cov = 0, bf = 0, B = 0, D = 0, K = 0;
+  int64_t N = 0;
+  int DP = 0, EP = 0, JP = 0, nk_col = 0, CW = 0, nw = 0, ktiles = 0, slices = 0, cblocks = 0;
+  int64_t rows_per_slice = 0;
+  int gram_slices = 0;
+  int64_t gram_rows = 0;
+  int chol_m = 0;
+  size_t o_whi = 0, o_wlo = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
+  size_t o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_prec = 0, o_logdet = 0, o_gram = 0, total = 0;
+};
+
+constexpr int kTargetBlocks = 512;  // ~2 workgroups per CU on 256 CUs
+
+int dp_for(int64_t d) {
+  const int dps[] = {16, 32, 64, 128};
+  for (int v : dps)
+    if (d <= v) return v;
+  return -1;
+}
+
+int plan_problem(const gmmxx_problem* p, Plan* pl) {
+  if (!p) return fail(GMMXX_ERR_INVALID_ARGUMENT, "problem descriptor is NULL");
+  if (p->covariance_type < 0 || p->covariance_type > 3)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "covariance_type must be 0..3");
+  if (p->x_dtype != GMMXX_F32 && p->x_dtype != GMMXX_BF16)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "x_dtype must be GMMXX_F32 or GMMXX_BF16");
+  if (p->B < 1 || p->N < 1 || p->D < 1 || p->K < 1)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "B, N, D and K must be positive");
+  if (p->B > 65535) return fail(GMMXX_ERR_UNSUPPORTED, "B > 65535");
+  if (p->K > 65536) return fail(GMMXX_ERR_UNSUPPORTED, "K > 65536");
+  if (p->N > (int64_t)1 << 40) return fail(GMMXX_ERR_UNSUPPORTED, "N too large");
+  Plan& q = *pl;
+  q.cov = p->covariance_type;
+  q.bf = p->x_dtype == GMMXX_BF16;
+  q.B = (int)p->B;
+  q.N = p->N;
+  q.D = (int)p->D;
+  q.K = (int)p->K;
+  if (q.bf && q.cov != SPH) return fail(GMMXX_ERR_UNSUPPORTED, "bf16 input is supported for spherical only");
+  const int dmax = (q.cov == FULL) ? 16 : (q.cov == TIED ? 64 : 128);
+  if (p->D > dmax) return fail(GMMXX_ERR_UNSUPPORTED, "D exceeds the supported maximum for this covariance type");
+  q.DP = dp_for(q.D);
+  const int S = q.DP * (q.DP + 1) / 2;
+  const int E = (q.cov == SPH || q.cov == TIED) ? q.DP : (q.cov == DIAG ? 2 * q.DP : S + q.DP);
+  const int J = (q.cov == SPH) ? q.DP + 3 : (q.cov == DIAG ? 2 * q.DP + 1 : (q.cov == TIED ? q.DP + 1 : q.DP + S + 1));
+  q.EP = round_up(E, q.bf ? 32 : 16);
+  q.JP = round_up(J, 16);
+  q.nk_col = (q.cov == SPH) ? q.DP : (q.cov == DIAG ? 2 * q.DP : (q.cov == TIED ? q.DP : q.DP + S));
+  q.CW = tile_cw(q.cov, q.DP, q.bf);
+  q.nw = std::min(8, (q.K + q.CW - 1) / q.CW);
+  q.ktiles = (q.K + q.nw * q.CW - 1) / (q.nw * q.CW);
+  const int64_t row_blocks = (q.N + kBN - 1) / kBN;
+  int64_t slices = std::max<int64_t>(1, (kTargetBlocks + (int64_t)q.ktiles * q.B - 1) / ((int64_t)q.ktiles * q.B));
+  slices = std::min(slices, row_blocks);
+  q.rows_per_slice = ((q.N + slices - 1) / slices + kBN - 1) / kBN * kBN;
+  q.slices = (int)((q.N + q.rows_per_slice - 1) / q.rows_per_slice);
+  q.cblocks = combine_blocks(q.N);
+  int64_t gs = std::min<int64_t>(64, row_blocks);
+  q.gram_rows = ((q.N + gs - 1) / gs + kBN - 1) / kBN * kBN;
+  q.gram_slices = (int)((q.N + q.gram_rows - 1) / q.gram_rows);
+  q.chol_m = (q.cov == TIED) ? q.B : (q.cov == FULL ? q.B * q.K : 0);
+
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  const size_t BK = (size_t)q.B * q.K, BN = (size_t)q.B * q.N;
+  q.o_whi = take(BK * q.EP * (q.bf ? 2 : 4));
+  q.o_wlo = take(q.bf ? BK * q.EP * 2 : 0);
+  q.o_cconst = take(BK * 16);
+  q.o_covs_used = take(q.cov == SPH ? BK * 4 : (q.cov == DIAG ? BK * q.D * 4 : 0));
+  q.o_rowq = take(q.cov == TIED ? BN * 4 : 0);
+  q.o_lse2 = take(BN * 4);
+  q.o_pms = take((size_t)q.ktiles * BN * 8);
+  q.o_pidx = take((size_t)q.ktiles * BN * 4);
+  q.o_pstats = take((size_t)q.slices * BK * q.JP * 4);
+  q.o_stats = take(BK * q.JP * 4);
+  q.o_ll = take((size_t)q.B * q.cblocks * 8);
+  q.o_first = take((size_t)q.chol_m * 4);
+  q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
+  q.o_logdet = take((size_t)q.chol_m * 4);
+  q.o_gram = take(q.cov == TIED ? (size_t)q.gram_slices * q.B * q.D * q.D * 4 : 0);
+  q.total = off;
+  return GMMXX_OK;
+}
+
+template <typename T>
+T* at(void* ws, size_t off) { return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off); }
+
+int check_ws(const Plan& pl, void* ws, int64_t bytes) {
+  if (!ws) return fail(GMMXX_ERR_WORKSPACE, "workspace is NULL");
+  if (bytes < 0 || (uint64_t)bytes < pl.total)
+    return fail(GMMXX_ERR_WORKSPACE, "workspace too small: need " + std::to_string(pl.total) + " bytes");
+  if ((uintptr_t)ws % 256 != 0) return fail(GMMXX_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return GMMXX_OK;
+}
+
+int check_hip(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(GMMXX_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+  return GMMXX_OK;
+}
+
+TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
+  TileArgs a{};
+  a.x = x;
+  a.vec_ok = (pl.D == pl.DP) && ((uintptr_t)x % 16 == 0);
+  a.N = pl.N;
+  a.D = pl.D;
+  a.K = pl.K;
+  a.B = pl.B;
+  a.ktiles = pl.ktiles;
+  a.rows_per_slice = pl.rows_per_slice;
+  a.w_hi = at<void>(ws, pl.o_whi);
+  a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
+  a.cconst = at<float4>(ws, pl.o_cconst);
+  a.rowq = pl.cov == TIED ? at<float>(ws, pl.o_rowq) : nullptr;
+  a.lse2 = at<float>(ws, pl.o_lse2);
+  a.part_ms = at<float>(ws, pl.o_pms);
+  a.part_idx = at<int>(ws, pl.o_pidx);
+  a.part_stats = at<float>(ws, pl.o_pstats);
+  a.proba = nullptr;
+  return a;
+}
+
+// Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
+int prepare(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights,
+            double reg, double minw, int prelude, void* ws, hipStream_t s) {
+  float* prec = nullptr;
+  float* logdet = nullptr;
+  if (pl.cov == TIED || pl.cov == FULL) {
+    prec = at<float>(ws, pl.o_prec);
+    logdet = at<float>(ws, pl.o_logdet);
+    launch_chol(covs, pl.D, pl.chol_m, at<int>(ws, pl.o_first), prec, logdet, s);
+  }
+  PrepArgs a{};
+  a.cov = pl.cov;
+  a.bf = pl.bf;
+  a.prelude = prelude;
+  a.B = pl.B;
+  a.K = pl.K;
+  a.D = pl.D;
+  a.DP = pl.DP;
+  a.EP = pl.EP;
+  a.reg_covar = (float)reg;
+  a.min_weight = (float)minw;
+  a.means = means;
+  a.covs = covs;
+  a.weights = weights;
+  a.prec = prec;
+  a.logdet = logdet;
+  a.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
+  a.w_hi = at<void>(ws, pl.o_whi);
+  a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
+  a.cconst = at<float4>(ws, pl.o_cconst);
+  launch_prep(a, s);
+  if (pl.cov == TIED)
+    launch_rowquad(reinterpret_cast<const float*>(x), pl.B, pl.N, pl.D, prec, at<float>(ws, pl.o_rowq), s);
+  return check_hip("parameter preparation");
+}
+
+// Log-normaliser pass: per-k-tile partials, then the per-row combine.
+int lse_pass(const Plan& pl, const void* x, void* ws, float* scores, int64_t* labels, bool with_ll,
+             hipStream_t s) {
+  const TileArgs t = tile_args(pl, x, ws);
+  const dim3 grid(pl.slices * pl.ktiles, pl.B);
+  if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_LSE, t, grid, pl.nw, s) != 0)
+    return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+  CombineArgs c{};
+  c.B = pl.B;
+  c.ktiles = pl.ktiles;
+  c.N = pl.N;
+  c.part_ms = t.part_ms;
+  c.part_idx = t.part_idx;
+  c.lse2 = at<float>(ws, pl.o_lse2);
+  c.scores = scores;
+  c.labels = labels;
+  c.ll_part = with_ll ? at<double>(ws, pl.o_ll) : nullptr;
+  launch_combine(c, s);
+  return check_hip("log-normaliser pass");
+}
+
+int stats_pass(const Plan& pl, const void* x, void* ws, hipStream_t s) {
+  const TileArgs t = tile_args(pl, x, ws);
+  const dim3 grid(pl.slices * pl.ktiles, pl.B);
+  if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_STATS, t, grid, pl.nw, s) != 0)
+    return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+  launch_reduce_slices(t.part_stats, pl.slices, (int64_t)pl.B * pl.K * pl.JP, at<float>(ws, pl.o_stats), s);
+  return check_hip("statistics pass");
+}
+
+int begin(const gmmxx_problem* p, Plan* pl, const void* x, void* ws, int64_t ws_bytes) {
+  int rc = plan_problem(p, pl);
+  if (rc) return rc;
+  if (!x) return fail(GMMXX_ERR_INVALID_ARGUMENT, "x is NULL");
+  return check_ws(*pl, ws, ws_bytes);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gmmxx_hip_abi_version(void) { return GMMXX_HIP_ABI_VERSION; }
+
+const char* gmmxx_hip_last_error(void) { return g_last_error.c_str(); }
+
+int gmmxx_hip_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, void* stream) {
+  if (n < 0) return fail(GMMXX_ERR_INVALID_ARGUMENT, "n must be non-negative");
+  if (n == 0) return GMMXX_OK;
+  if (!in || !out) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  launch_canary(in, out, n, offset, (hipStream_t)stream);
+  return check_hip("canary");
+}
+
+int gmmxx_hip_supported(const gmmxx_problem* p) {
+  Plan pl;
+  const std::string saved = g_last_error;
+  const int rc = plan_problem(p, &pl);
+  g_last_error = saved;
+  return rc == GMMXX_OK ? 1 : 0;
+}
+
+int64_t gmmxx_hip_workspace_bytes(const gmmxx_problem* p) {
+  Plan pl;
+  if (plan_problem(p, &pl) != GMMXX_OK) return -1;
+  return (int64_t)pl.total;
+}
+
+int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float* covs, float* weights,
+                      const float* gram, double reg_covar, double min_weight, float* lower_bound,
+                      void* ws, int64_t ws_bytes, void* stream) {
+  Plan pl;
+  int rc = begin(p, &pl, x, ws, ws_bytes);
+  if (rc) return rc;
+  if (!means || !covs || !weights || !lower_bound) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL parameter buffer");
+  if (pl.cov == TIED && !gram) return fail(GMMXX_ERR_INVALID_ARGUMENT, "tied EM needs the XᵀX buffer");
+  if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
+  const hipStream_t s = (hipStream_t)stream;
+  if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
+  if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, true, s))) return rc;
+  launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
+  if ((rc = stats_pass(pl, x, ws, s))) return rc;
+  FinalizeArgs f{};
+  f.cov = pl.cov;
+  f.B = pl.B;
+  f.K = pl.K;
+  f.D = pl.D;
+  f.DP = pl.DP;
+  f.JP = pl.JP;
+  f.nk_col = pl.nk_col;
+  f.N = pl.N;
+  f.reg_covar = (float)reg_covar;
+  f.min_weight = (float)min_weight;
+  f.stats = at<float>(ws, pl.o_stats);
+  f.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
+  f.gram = gram;
+  f.means = means;
+  f.covs = covs;
+  f.weights = weights;
+  launch_finalize(f, s);
+  return check_hip("finalize");
+}
+
+int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
+                          const float* weights, double reg_covar, double min_weight, float* nk, float* sum_x,
+                          float* sum_q, float* ll_sum, void* ws, int64_t ws_bytes, void* stream) {
+  Plan pl;
+  int rc = begin(p, &pl, x, ws, ws_bytes);
+  if (rc) return rc;
+  if (!means || !covs || !weights || !nk || !sum_x || !ll_sum)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  if (pl.cov != TIED && !sum_q) return fail(GMMXX_ERR_INVALID_ARGUMENT, "sum_q is required for this covariance type");
+  if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
+  const hipStream_t s = (hipStream_t)stream;
+  if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
+  if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, true, s))) return rc;
+  launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0, ll_sum, s);
+  if ((rc = stats_pass(pl, x, ws, s))) return rc;
+  UnpackArgs u{};
+  u.cov = pl.cov;
+  u.K = pl.K;
+  u.D = pl.D;
+  u.DP = pl.DP;
+  u.JP = pl.JP;
+  u.nk_col = pl.nk_col;
+  u.stats = at<float>(ws, pl.o_stats);
+  u.nk = nk;
+  u.sum_x = sum_x;
+  u.sum_q = pl.cov == TIED ? nullptr : sum_q;
+  launch_unpack(u, pl.B, s);
+  return check_hip("statistics unpack");
+}
+
+int gmmxx_hip_score(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
+                    const float* weights, float* scores, int64_t* labels, void* ws, int64_t ws_bytes,
+                    void* stream) {
+  Plan pl;
+  int rc = begin(p, &pl, x, ws, ws_bytes);
+  if (rc) return rc;
+  if (!means || !covs || !weights) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL parameter buffer");
+  const hipStream_t s = (hipStream_t)stream;
+  if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
+  return lse_pass(pl, x, ws, scores, labels, false, s);
+}
+
+int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
+                            const float* weights, float* proba, void* ws, int64_t ws_bytes, void* stream) {
+  Plan pl;
+  int rc = begin(p, &pl, x, ws, ws_bytes);
+  if (rc) return rc;
+  if (!means || !covs || !weights || !proba) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  const hipStream_t s = (hipStream_t)stream;
+  if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
+  if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, false, s))) return rc;
+  TileArgs t = tile_args(pl, x, ws);
+  t.proba = proba;
+  const dim3 grid(pl.slices * pl.ktiles, pl.B);
+  if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_PROBA, t, grid, pl.nw, s) != 0)
+    return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+  return check_hip("predict_proba");
+}
+
+int gmmxx_hip_gram(const gmmxx_problem* p, const void* x, float* out, void* ws, int64_t ws_bytes, void* stream) {
+  Plan pl;
+  int rc = begin(p, &pl, x, ws, ws_bytes);
+  if (rc) return rc;
+  if (pl.cov != TIED) return fail(GMMXX_ERR_INVALID_ARGUMENT, "gram is defined for the tied problem");
+  if (!out) return fail(GMMXX_ERR_INVALID_ARGUMENT, "out is NULL");
+  const hipStream_t s = (hipStream_t)stream;
+  float* part = at<float>(ws, pl.o_gram);
+  launch_gram(reinterpret_cast<const float*>(x), pl.B, pl.N, pl.D, pl.gram_slices, pl.gram_rows, part, s);
+  launch_reduce_slices(part, pl.gram_slices, (int64_t)pl.B * pl.D * pl.D, out, s);
+  return check_hip("gram");
+}
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+// Internal launch interface between the C-ABI layer and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gx {
+
+struct TileArgs {
+  const void* x;               // [B][N][D], fp32 or bf16
+  int vec_ok;                  // x rows are 16-byte aligned and D == DP
+  int64_t N;
+  int D, K, B;
+  int ktiles;                  // component tiles per batch
+  int64_t rows_per_slice;      // multiple of 32
+  const void* w_hi;            // [B][K][EP] E-step operand (bf16 hi or fp32)
+  const void* w_lo;            // [B][K][EP] bf16 lo part (bf16 path only)
+  const float4* cconst;        // [B][K] (colq, a, b, 0): l2 = a*max(sc*S + rowq + colq, 0) + b
+  const float* rowq;           // [B][N] tied: xᵀPx
+  const float* lse2;           // [B][N] log2-domain log-normaliser (STATS / PROBA)
+  float* part_ms;              // [ktiles][B][N][2] (max, scaled sum)   (LSE)
+  int* part_idx;               // [ktiles][B][N] first argmax           (LSE)
+  float* part_stats;           // [slices][B][K][JP]                    (STATS)
+  float* proba;                // [B][N][K]                             (PROBA)
+};
+
+int tile_cw(int cov, int dp, int bf);
+int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s);
+
+}  // namespace gx

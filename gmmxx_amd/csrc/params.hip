@@ -1,0 +1,518 @@
+// Component-side kernels of one EM iteration: the iteration prelude and E-step
+// operand packing, batched Cholesky with the batch-global jitter ladder,
+// per-row combine of k-tile partials, ordered reductions and the M-step
+// finalize for the four covariance types.  All of them touch K- or N-sized
+// data only; the (N x K) work lives in em_tile.hip.
+
+#include <math.h>
+
+#include "common.hpp"
+#include "params.hpp"
+
+namespace gx {
+
+// ---------------------------------------------------------------------------
+// Block helpers
+// ---------------------------------------------------------------------------
+
+template <typename T>
+__device__ T block_sum(T v, T* scratch) {
+  // scratch: >= 32 elements of shared memory
+  for (int off = 32; off >= 1; off /= 2) v += __shfl_xor(v, off);
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  __syncthreads();
+  if (l == 0) scratch[w] = v;
+  __syncthreads();
+  T t = 0;
+  const int nw = (blockDim.x + 63) / 64;
+  for (int i = 0; i < nw; ++i) t += scratch[i];  // fixed order: deterministic
+  return t;
+}
+
+// Σ_k max(w_k, floor) over one batch row, identical in every block.
+__device__ float weight_total(const float* w, int K, float floor_v, float* scratch) {
+  float s = 0.f;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) s += fmaxf(w[k], floor_v);
+  return block_sum(s, scratch);
+}
+
+// ---------------------------------------------------------------------------
+// Prelude + E-step operand packing (one thread per component)
+// ---------------------------------------------------------------------------
+
+__global__ void prep_kernel(PrepArgs a) {
+  __shared__ float scratch[32];
+  const int b = blockIdx.y;
+  const int K = a.K, D = a.D, DP = a.DP, EP = a.EP;
+  const float* wrow = a.weights + (size_t)b * K;
+  // Iteration prelude (torch_fallback.py:2061-2066): w <- max(w, min_weight) / Σ.
+  // Inference uses the weights as given (log w only).
+  const float floor_v = a.prelude ? a.min_weight : -INFINITY;
+  const float total = a.prelude ? weight_total(wrow, K, floor_v, scratch) : 1.f;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= K) return;
+  const size_t bk = (size_t)b * K + k;
+  const float wk = a.prelude ? fmaxf(wrow[k], floor_v) / total : wrow[k];
+  const float lw = logf(wk);
+  const float* mu = a.means + bk * D;
+  float colq, ca, cb;
+  const float log2pi_d = (float)(kLog2Pi * (double)D);
+
+  auto put_f32 = [&](int e, float v) {
+    reinterpret_cast<float*>(a.w_hi)[bk * EP + e] = v;
+  };
+  auto put_bf = [&](int e, float v) {
+    const __bf16 hi = (__bf16)v;
+    reinterpret_cast<__bf16*>(a.w_hi)[bk * EP + e] = hi;
+    reinterpret_cast<__bf16*>(a.w_lo)[bk * EP + e] = (__bf16)(v - (float)hi);
+  };
+  auto put = [&](int e, float v) { if (a.bf) put_bf(e, v); else put_f32(e, v); };
+
+  if (a.cov == SPH) {
+    float var = a.covs[bk];
+    if (a.prelude) var = fmaxf(var, a.reg_covar);
+    a.covs_used[bk] = var;
+    float msq = 0.f;
+    for (int d = 0; d < D; ++d) msq = fmaf(mu[d], mu[d], msq);
+    for (int e = 0; e < EP; ++e) put(e, e < D ? mu[e] : 0.f);
+    const float lognorm = (float)D * ((float)kLog2Pi + logf(var));
+    colq = msq;
+    ca = -0.5f * kLog2e / var;
+    cb = (lw - 0.5f * lognorm) * kLog2e;
+  } else if (a.cov == DIAG) {
+    // torch_fallback.py:2491-2494
+    const float* vr = a.covs + bk * D;
+    float* vu = a.covs_used + bk * D;
+    float logdet = 0.f, mpm = 0.f;
+    for (int d = 0; d < D; ++d) {
+      float v = vr[d];
+      if (a.prelude) v = fmaxf(v, a.reg_covar);
+      vu[d] = v;
+      const float vc = fmaxf(v, 1e-30f);
+      const float p = 1.f / vc;
+      const float wm = mu[d] * p;
+      logdet += logf(vc);
+      mpm = fmaf(mu[d], wm, mpm);
+      put_f32(d, p);
+      put_f32(DP + d, -2.f * wm);
+    }
+    for (int d = D; d < DP; ++d) { put_f32(d, 0.f); put_f32(DP + d, 0.f); }
+    for (int e = 2 * DP; e < EP; ++e) put_f32(e, 0.f);
+    colq = mpm;
+    ca = -0.5f * kLog2e;
+    cb = (lw - 0.5f * (log2pi_d + logdet)) * kLog2e;
+  } else if (a.cov == TIED) {
+    // Pμ_k (torch_fallback.py:2873), μᵀPμ (:2874)
+    const float* P = a.prec + (size_t)b * D * D;
+    float mpm = 0.f;
+    for (int d = 0; d < D; ++d) {
+      float pm = 0.f;
+      for (int e = 0; e < D; ++e) pm = fmaf(mu[e], P[d * D + e], pm);
+      mpm = fmaf(mu[d], pm, mpm);
+      put_f32(d, pm);
+    }
+    for (int e = D; e < EP; ++e) put_f32(e, 0.f);
+    colq = mpm;
+    ca = -0.5f * kLog2e;
+    cb = (lw - 0.5f * (log2pi_d + a.logdet[b])) * kLog2e;
+  } else {
+    // FULL: W_k = [packed P_k with doubled off-diagonal | -2 P_k μ_k]  (torch_fallback.py:418-432)
+    const float* P = a.prec + bk * D * D;
+    const int S = DP * (DP + 1) / 2;
+    for (int e = 0; e < EP; ++e) put_f32(e, 0.f);
+    float mpm = 0.f;
+    for (int d = 0; d < D; ++d) {
+      float pm = 0.f;
+      for (int e = 0; e < D; ++e) pm = fmaf(P[d * D + e], mu[e], pm);
+      mpm = fmaf(mu[d], pm, mpm);
+      put_f32(S + d, -2.f * pm);
+      for (int e = d; e < D; ++e)
+        put_f32(sym_index(d, e, DP), d == e ? P[d * D + d] : P[d * D + e] + P[e * D + d]);
+    }
+    colq = mpm;
+    ca = -0.5f * kLog2e;
+    cb = (lw - 0.5f * (log2pi_d + a.logdet[bk])) * kLog2e;
+  }
+  a.cconst[bk] = make_float4(colq, ca, cb, 0.f);
+}
+
+// ---------------------------------------------------------------------------
+// Batched Cholesky, precision and log-determinant (torch_fallback.py:316-334)
+//
+// chol_try:    per matrix, the first jitter level that factorises
+//              (level 0 = no jitter, level i = 1e-6 * 10^(i-1), i = 1..6; 7 = none)
+// chol_finish: the batch-global level is the largest first level (all
+//              matrices factorise there); refactorise at it and form
+//              P = L^-T L^-1 and log det = 2 Σ log L_jj.
+// One workgroup of 64 threads per matrix, one thread per row, D <= 64.
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxCholD = 64;
+constexpr int kCS = kMaxCholD + 1;
+
+// The ladder is built in double and cast once, like the reference's Python float.
+__device__ float jitter_of(int level) {
+  double j = 0.0;
+  if (level >= 1) { j = 1e-6; for (int i = 1; i < level; ++i) j *= 10.0; }
+  return (float)j;
+}
+
+// Factorises sym(C) + jitter·I into Ls (lower triangle).  Returns success.
+__device__ bool chol_factor(const float* C, int D, float jitter, float* Ls) {
+  const int i = threadIdx.x;
+  if (i < D) {
+    for (int j = 0; j < D; ++j) {
+      const float s = 0.5f * (C[i * D + j] + C[j * D + i]);
+      Ls[i * kCS + j] = (i == j) ? s + jitter : s;
+    }
+  }
+  __syncthreads();
+  bool ok = true;
+  for (int j = 0; j < D; ++j) {
+    const float djj = Ls[j * kCS + j];
+    if (!(djj > 0.f)) { ok = false; break; }     // uniform across the block
+    const float ljj = sqrtf(djj);
+    __syncthreads();
+    if (i == j) Ls[j * kCS + j] = ljj;
+    if (i > j && i < D) Ls[i * kCS + j] = Ls[i * kCS + j] / ljj;
+    __syncthreads();
+    if (i > j && i < D) {
+      const float lij = Ls[i * kCS + j];
+      for (int c = j + 1; c <= i; ++c) Ls[i * kCS + c] -= lij * Ls[c * kCS + j];
+    }
+    __syncthreads();
+  }
+  __syncthreads();
+  return ok;
+}
+
+__global__ void chol_try_kernel(const float* cov, int D, int* first_ok) {
+  __shared__ float Ls[kMaxCholD * kCS];
+  const int m = blockIdx.x;
+  const float* C = cov + (size_t)m * D * D;
+  int level = 7;
+  for (int l = 0; l < 7; ++l) {
+    if (chol_factor(C, D, jitter_of(l), Ls)) { level = l; break; }
+  }
+  if (threadIdx.x == 0) first_ok[m] = level;
+}
+
+__global__ void chol_finish_kernel(const float* cov, int D, int M, const int* first_ok,
+                                   float* prec, float* logdet) {
+  __shared__ float Ls[kMaxCholD * kCS];
+  __shared__ float Xs[kMaxCholD * kCS];
+  __shared__ int lvl_s;
+  const int m = blockIdx.x;
+  const int i = threadIdx.x;
+  if (i == 0) {
+    int lv = 0;
+    for (int t = 0; t < M; ++t) lv = first_ok[t] > lv ? first_ok[t] : lv;
+    lvl_s = lv > 6 ? 6 : lv;
+  }
+  __syncthreads();
+  chol_factor(cov + (size_t)m * D * D, D, jitter_of(lvl_s), Ls);
+  // X = L^-1 (lower triangular), thread i computes column i by forward substitution.
+  if (i < D) {
+    for (int r = 0; r < D; ++r) Xs[r * kCS + i] = 0.f;
+    Xs[i * kCS + i] = 1.f / Ls[i * kCS + i];
+    for (int r = i + 1; r < D; ++r) {
+      float s = 0.f;
+      for (int c = i; c < r; ++c) s = fmaf(Ls[r * kCS + c], Xs[c * kCS + i], s);
+      Xs[r * kCS + i] = -s / Ls[r * kCS + r];
+    }
+  }
+  __syncthreads();
+  // P = Xᵀ X: P[i][j] = Σ_{r >= max(i,j)} X[r][i] X[r][j]; symmetric by construction.
+  if (i < D) {
+    float* Pm = prec + (size_t)m * D * D;
+    for (int j = 0; j < D; ++j) {
+      float s = 0.f;
+      for (int r = (i > j ? i : j); r < D; ++r) s = fmaf(Xs[r * kCS + i], Xs[r * kCS + j], s);
+      Pm[i * D + j] = s;
+    }
+  }
+  if (i == 0) {
+    float s = 0.f;
+    for (int j = 0; j < D; ++j) s += logf(Ls[j * kCS + j]);
+    logdet[m] = 2.f * s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tied: per-row quadratic form xᵀ P x (torch_fallback.py:451)
+// ---------------------------------------------------------------------------
+
+__global__ void rowquad_kernel(const float* x, int64_t N, int D, const float* prec, float* rowq) {
+  __shared__ float Ps[kMaxCholD * kMaxCholD];
+  const int b = blockIdx.y;
+  const float* P = prec + (size_t)b * D * D;
+  for (int i = threadIdx.x; i < D * D; i += blockDim.x) Ps[i] = P[i];
+  __syncthreads();
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const float* xr = x + ((size_t)b * N + n) * D;
+  float xv[kMaxCholD];
+  for (int d = 0; d < D; ++d) xv[d] = xr[d];
+  float q = 0.f;
+  for (int d = 0; d < D; ++d) {
+    float t = 0.f;
+    for (int e = 0; e < D; ++e) t = fmaf(Ps[d * D + e], xv[e], t);
+    q = fmaf(xv[d], t, q);
+  }
+  rowq[(size_t)b * N + n] = q;
+}
+
+// ---------------------------------------------------------------------------
+// Per-row combine of k-tile partials: log-normaliser, first argmax, Σ lse
+// ---------------------------------------------------------------------------
+
+__global__ void combine_kernel(CombineArgs a) {
+  __shared__ double scratch[32];
+  const int b = blockIdx.y;
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  double contrib = 0.0;
+  if (n < a.N) {
+    float m = -INFINITY, s = 0.f;
+    int idx = 0x7fffffff;
+    for (int t = 0; t < a.ktiles; ++t) {
+      const size_t o = ((size_t)t * a.B + b) * a.N + n;
+      lse_merge(m, s, idx, a.part_ms[2 * o], a.part_ms[2 * o + 1], a.part_idx[o]);
+    }
+    const float lse2 = m + __log2f(s);
+    const size_t o = (size_t)b * a.N + n;
+    if (a.lse2) a.lse2[o] = lse2;
+    const float lse = lse2 * kLn2;
+    if (a.scores) a.scores[o] = lse;
+    if (a.labels) a.labels[o] = (int64_t)idx;
+    contrib = (double)lse;
+  }
+  const double t = block_sum(contrib, scratch);
+  if (threadIdx.x == 0 && a.ll_part) a.ll_part[(size_t)b * gridDim.x + blockIdx.x] = t;
+}
+
+// Mean log-likelihood over all B*N rows (lower bound of the iteration).
+__global__ void ll_reduce_kernel(const double* ll_part, int count, double inv_total, float* out) {
+  __shared__ double scratch[32];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < count; i += blockDim.x) s += ll_part[i];
+  s = block_sum(s, scratch);
+  if (threadIdx.x == 0) out[0] = (float)(s * inv_total);
+}
+
+// out[i] = Σ_s part[s * M + i], fixed slice order (deterministic).
+__global__ void reduce_slices_kernel(const float* part, int slices, int64_t M, float* out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= M) return;
+  float s = 0.f;
+  for (int t = 0; t < slices; ++t) s += part[(size_t)t * M + i];
+  out[i] = s;
+}
+
+// ---------------------------------------------------------------------------
+// M-step finalize (one thread per component; weights renormalised per batch)
+// spherical torch_fallback.py:2293-2305, diag :2654-2666, tied/full means :3143-3146
+// ---------------------------------------------------------------------------
+
+__global__ void finalize_kernel(FinalizeArgs a) {
+  __shared__ float scratch[32];
+  const int b = blockIdx.y;
+  const int K = a.K, D = a.D, JP = a.JP;
+  const float* st = a.stats + (size_t)b * K * JP;
+  // w_new = max(nk / N, min_weight) / Σ  (torch_fallback.py:2303-2305)
+  float part = 0.f;
+  for (int k = threadIdx.x; k < K; k += blockDim.x)
+    part += fmaxf(st[(size_t)k * JP + a.nk_col] / (float)a.N, a.min_weight);
+  const float total = block_sum(part, scratch);
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= K) return;
+  const size_t bk = (size_t)b * K + k;
+  const float* sk = st + (size_t)k * JP;
+  const float nk = sk[a.nk_col];
+  const bool active = nk > a.min_weight;
+  const float nk_safe = fmaxf(nk, a.min_weight);
+  float* mu = a.means + bk * D;
+  float msq = 0.f;
+  for (int d = 0; d < D; ++d) {
+    const float m = active ? sk[d] / nk_safe : mu[d];
+    mu[d] = m;
+    msq = fmaf(m, m, msq);
+  }
+  if (a.cov == SPH) {
+    const float sq = sk[a.nk_col + 1] + sk[a.nk_col + 2];
+    float v = fmaxf(sq - nk * msq, 0.f) / (nk_safe * (float)D);
+    v = fmaxf(v, a.reg_covar);
+    a.covs[bk] = active ? v : a.covs_used[bk];
+  } else if (a.cov == DIAG) {
+    for (int d = 0; d < D; ++d) {
+      const float second = sk[a.DP + d] / nk_safe;
+      const float v = fmaxf(second - mu[d] * mu[d], a.reg_covar);
+      a.covs[bk * D + d] = active ? v : a.covs_used[bk * D + d];
+    }
+  }
+  a.weights[bk] = fmaxf(nk / (float)a.N, a.min_weight) / total;
+}
+
+// Tied: Σ = sym((XᵀX − Σ_k n_k μ_k μ_kᵀ) / N) + reg·I   (torch_fallback.py:3159-3162)
+__global__ void finalize_tied_kernel(FinalizeArgs a) {
+  const int b = blockIdx.y;
+  const int K = a.K, D = a.D, JP = a.JP;
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= D * D) return;
+  const int d = t / D, e = t % D;
+  const float* st = a.stats + (size_t)b * K * JP;
+  const float* mu = a.means + (size_t)b * K * D;
+  float sde = 0.f, sed = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const float nk = st[(size_t)k * JP + a.nk_col];
+    sde += nk * (mu[k * D + d] * mu[k * D + e]);
+    sed += nk * (mu[k * D + e] * mu[k * D + d]);
+  }
+  const float* G = a.gram + (size_t)b * D * D;
+  const float ade = (G[d * D + e] - sde) / (float)a.N;
+  const float aed = (G[e * D + d] - sed) / (float)a.N;
+  a.covs[(size_t)b * D * D + t] = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
+}
+
+// Full: Σ_k = sym((Σ r xxᵀ − n_k μμᵀ) / max(n_k, floor)) + reg·I, kept if inactive (:3150-3158)
+__global__ void finalize_full_kernel(FinalizeArgs a) {
+  const int b = blockIdx.y, k = blockIdx.x;
+  const int K = a.K, D = a.D, JP = a.JP, DP = a.DP;
+  const int t = threadIdx.x;
+  if (t >= D * D) return;
+  const int d = t / D, e = t % D;
+  const size_t bk = (size_t)b * K + k;
+  const float* sk = a.stats + bk * JP;
+  const float nk = sk[a.nk_col];
+  const bool active = nk > a.min_weight;
+  const float nk_safe = fmaxf(nk, a.min_weight);
+  const float* mu = a.means + bk * D;
+  const float sxx = sk[DP + sym_index(d < e ? d : e, d < e ? e : d, DP)];
+  const float ade = (sxx - nk * (mu[d] * mu[e])) / nk_safe;
+  const float aed = (sxx - nk * (mu[e] * mu[d])) / nk_safe;
+  float* C = a.covs + bk * D * D;
+  const float v = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
+  if (active) C[t] = v;  // inactive components keep their previous covariance
+}
+
+// Unpacks the statistics rows into (N_k, Σ r x, Σ r q(x)) for callers and tests.
+__global__ void unpack_stats_kernel(UnpackArgs a) {
+  const int b = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= a.K) return;
+  const size_t bk = (size_t)b * a.K + k;
+  const float* sk = a.stats + bk * a.JP;
+  const int D = a.D, DP = a.DP;
+  a.nk[bk] = sk[a.nk_col];
+  for (int d = 0; d < D; ++d) a.sum_x[bk * D + d] = sk[d];
+  if (!a.sum_q) return;
+  if (a.cov == SPH) {
+    a.sum_q[bk] = sk[a.nk_col + 1] + sk[a.nk_col + 2];
+  } else if (a.cov == DIAG) {
+    for (int d = 0; d < D; ++d) a.sum_q[bk * D + d] = sk[DP + d];
+  } else if (a.cov == FULL) {
+    for (int d = 0; d < D; ++d)
+      for (int e = 0; e < D; ++e)
+        a.sum_q[(bk * D + d) * D + e] = sk[DP + sym_index(d < e ? d : e, d < e ? e : d, DP)];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// XᵀX per batch (tied, once per fit; torch_fallback.py:2856-2862)
+// ---------------------------------------------------------------------------
+
+__global__ void gram_partial_kernel(const float* x, int64_t N, int D, int64_t rows_per_slice, float* part) {
+  __shared__ float xs[32 * (kMaxCholD + 1)];
+  const int b = blockIdx.y, slice = blockIdx.x;
+  const int64_t r0 = (int64_t)slice * rows_per_slice;
+  const int64_t r1 = (r0 + rows_per_slice < N) ? r0 + rows_per_slice : N;
+  const float* xb = x + (size_t)b * N * D;
+  constexpr int kPer = (kMaxCholD * kMaxCholD + 255) / 256;
+  float acc[kPer];
+  for (int i = 0; i < kPer; ++i) acc[i] = 0.f;
+  for (int64_t n0 = r0; n0 < r1; n0 += 32) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < 32 * D; i += blockDim.x) {
+      const int r = i / D, c = i % D;
+      xs[r * (kMaxCholD + 1) + c] = (n0 + r < r1) ? xb[(size_t)(n0 + r) * D + c] : 0.f;
+    }
+    __syncthreads();
+    for (int i = 0; i < kPer; ++i) {
+      const int t = threadIdx.x + i * blockDim.x;
+      if (t < D * D) {
+        const int d = t / D, e = t % D;
+        float s = acc[i];
+        for (int r = 0; r < 32; ++r) s = fmaf(xs[r * (kMaxCholD + 1) + d], xs[r * (kMaxCholD + 1) + e], s);
+        acc[i] = s;
+      }
+    }
+  }
+  for (int i = 0; i < kPer; ++i) {
+    const int t = threadIdx.x + i * blockDim.x;
+    if (t < D * D) part[((size_t)slice * gridDim.y + b) * D * D + t] = acc[i];
+  }
+}
+
+__global__ void canary_kernel(const int32_t* in, int32_t* out, int64_t n, int32_t offset) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = in[i] + offset;
+}
+
+}  // namespace gx
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+
+namespace gx {
+
+void launch_prep(const PrepArgs& a, hipStream_t s) {
+  dim3 grid((a.K + 255) / 256, a.B);
+  prep_kernel<<<grid, 256, 0, s>>>(a);
+}
+
+void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, float* logdet, hipStream_t s) {
+  chol_try_kernel<<<M, 64, 0, s>>>(cov, D, first_ok);
+  chol_finish_kernel<<<M, 64, 0, s>>>(cov, D, M, first_ok, prec, logdet);
+}
+
+void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s) {
+  dim3 grid((unsigned)((N + 255) / 256), B);
+  rowquad_kernel<<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
+}
+
+int combine_blocks(int64_t N) { return (int)((N + 255) / 256); }
+
+int launch_combine(const CombineArgs& a, hipStream_t s) {
+  const int nb = combine_blocks(a.N);
+  combine_kernel<<<dim3(nb, a.B), 256, 0, s>>>(a);
+  return nb;
+}
+
+void launch_ll_reduce(const double* ll_part, int count, double inv_total, float* out, hipStream_t s) {
+  ll_reduce_kernel<<<1, 1024, 0, s>>>(ll_part, count, inv_total, out);
+}
+
+void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s) {
+  reduce_slices_kernel<<<(unsigned)((M + 255) / 256), 256, 0, s>>>(part, slices, M, out);
+}
+
+void launch_finalize(const FinalizeArgs& a, hipStream_t s) {
+  finalize_kernel<<<dim3((a.K + 255) / 256, a.B), 256, 0, s>>>(a);
+  if (a.cov == TIED) finalize_tied_kernel<<<dim3((a.D * a.D + 255) / 256, a.B), 256, 0, s>>>(a);
+  if (a.cov == FULL) finalize_full_kernel<<<dim3(a.K, a.B), 256, 0, s>>>(a);
+}
+
+void launch_unpack(const UnpackArgs& a, int B, hipStream_t s) {
+  unpack_stats_kernel<<<dim3((a.K + 255) / 256, B), 256, 0, s>>>(a);
+}
+
+void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
+                 hipStream_t s) {
+  gram_partial_kernel<<<dim3(slices, B), 256, 0, s>>>(x, N, D, rows_per_slice, part);
+}
+
+void launch_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, hipStream_t s) {
+  canary_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(in, out, n, offset);
+}
+
+}  // namespace gx

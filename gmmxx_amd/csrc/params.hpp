@@ -1,0 +1,68 @@
+// Component-side kernels: argument blocks and host launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gx {
+
+struct PrepArgs {
+  int cov, bf, prelude;
+  int B, K, D, DP, EP;
+  float reg_covar, min_weight;
+  const float* means;      // [B][K][D]
+  const float* covs;       // spherical [B][K], diag [B][K][D]
+  const float* weights;    // [B][K]
+  const float* prec;       // tied [B][D][D], full [B][K][D][D]
+  const float* logdet;     // tied [B], full [B][K]
+  float* covs_used;        // spherical/diag: the (clamped) variances this iteration used
+  void* w_hi;              // [B][K][EP]
+  void* w_lo;              // [B][K][EP] (bf16 path)
+  float4* cconst;          // [B][K]
+};
+
+struct CombineArgs {
+  int B, ktiles;
+  int64_t N;
+  const float* part_ms;
+  const int* part_idx;
+  float* lse2;             // [B][N] or null
+  float* scores;           // [B][N] natural-log scores or null
+  int64_t* labels;         // [B][N] or null
+  double* ll_part;         // [B][gridDim.x] or null
+};
+
+struct FinalizeArgs {
+  int cov, B, K, D, DP, JP, nk_col;
+  int64_t N;
+  float reg_covar, min_weight;
+  const float* stats;      // [B][K][JP]
+  const float* covs_used;  // spherical/diag old (clamped) variances
+  const float* gram;       // tied XᵀX [B][D][D]
+  float* means;
+  float* covs;
+  float* weights;
+};
+
+struct UnpackArgs {
+  int cov, K, D, DP, JP, nk_col;
+  const float* stats;
+  float* nk;
+  float* sum_x;
+  float* sum_q;
+};
+
+void launch_prep(const PrepArgs& a, hipStream_t s);
+void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, float* logdet, hipStream_t s);
+void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s);
+int launch_combine(const CombineArgs& a, hipStream_t s);  // returns the per-batch block count
+int combine_blocks(int64_t N);
+void launch_ll_reduce(const double* ll_part, int count, double inv_total, float* out, hipStream_t s);
+void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s);
+void launch_finalize(const FinalizeArgs& a, hipStream_t s);
+void launch_unpack(const UnpackArgs& a, int B, hipStream_t s);
+void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
+                 hipStream_t s);
+void launch_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, hipStream_t s);
+
+}  // namespace gx

@@ -1,0 +1,235 @@
+"""Host-side EM loops of the HIP backend.
+
+Function-level API mirroring the reference's ``batch_gmm_*_torch_native``
+(gmmxx/torch_fallback.py:1897-3336): same positional/keyword arguments, same
+return tuple ``(labels, means, covariances, weights, info)``.  Every EM
+iteration is one call of ``gmmxx_hip_em_step`` on the current stream; with
+``tol == 0`` and ``verbose=False`` nothing synchronises until the loop ends.
+
+Semantics follow the reference's soft EM on fp32 data: bf16 input (spherical
+only) is kept in bf16 in HBM and computed with fp32 accumulation, i.e. it
+equals the fp32 algorithm on the bf16-rounded values.  Parameters are fp32.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _hip
+
+_COVS = ("spherical", "diag", "tied", "full")
+
+
+def _as_device_input(x: torch.Tensor, covariance_type: str) -> torch.Tensor:
+    if not torch.is_tensor(x):
+        raise TypeError("x must be a torch.Tensor")
+    if x.ndim != 3:
+        raise ValueError("x must have shape (B, N, D)")
+    if not x.is_cuda:
+        raise ValueError(f"x must be on a GPU device for the hip backend, got {x.device}")
+    if x.dtype == torch.bfloat16 and covariance_type == "spherical":
+        return x.contiguous()
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16, torch.float64):
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    return x.to(torch.float32).contiguous()
+
+
+def _f32(t: torch.Tensor, device) -> torch.Tensor:
+    return t.detach().to(device=device, dtype=torch.float32).contiguous().clone()
+
+
+def _sym(m: torch.Tensor) -> torch.Tensor:
+    return 0.5 * (m + m.transpose(-1, -2))
+
+
+# --- default-variance initialisers (torch_fallback.py:1348-1381), on device ---
+
+def global_spherical_variance(x: torch.Tensor, k: int, reg_covar: float) -> torch.Tensor:
+    d = x.shape[-1]
+    xf = x.to(torch.float32)
+    mean = xf.mean(dim=1)
+    second = xf.square().sum(dim=-1).mean(dim=1)
+    gv = (second - mean.square().sum(dim=-1)).clamp_min(0.0) / float(d)
+    return gv.clamp_min(reg_covar).unsqueeze(-1).expand(-1, k).contiguous()
+
+
+def global_diag_variance(x: torch.Tensor, k: int, reg_covar: float) -> torch.Tensor:
+    xf = x.to(torch.float32)
+    gv = (xf - xf.mean(dim=1, keepdim=True)).square().mean(dim=1).clamp_min(reg_covar)
+    return gv.unsqueeze(1).expand(-1, k, -1).contiguous()
+
+
+def global_tied_covariance(x: torch.Tensor, reg_covar: float) -> torch.Tensor:
+    n, d = x.shape[1], x.shape[2]
+    xf = x.to(torch.float32)
+    c = xf - xf.mean(dim=1, keepdim=True)
+    cov = torch.bmm(c.transpose(1, 2), c) / float(n)
+    return (_sym(cov) + reg_covar * torch.eye(d, device=x.device)).contiguous()
+
+
+def _init_weights(init_weights, bsz, k, device):
+    w = (torch.full((bsz, k), 1.0 / float(k), device=device) if init_weights is None
+         else _f32(init_weights, device))
+    if tuple(w.shape) != (bsz, k):
+        raise ValueError("init_weights must have shape (B, K)")
+    w = w.clamp_min(1e-8)
+    return (w / w.sum(dim=-1, keepdim=True)).contiguous()
+
+
+def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init_means=None,
+               init_covs=None, init_weights=None, reg_covar: float = 1e-6,
+               init_params: str = "kmeans", generator: Optional[torch.Generator] = None):
+    """Initial (means, covariances, weights, source), fp32 on x's device.
+
+    Explicit parameters get the reference's entry clamps
+    (torch_fallback.py:1661-1682, :1731-1742, :1791-1802, :1851-1862).  Without
+    ``init_means`` the reference's ``kmeans``/``random`` initialisers reduce to
+    random data rows plus the global variance when flash-kmeans is absent
+    (:1580-1582, :1706-1714); rows are drawn on the device.
+    """
+    bsz, n, d = x.shape
+    dev = x.device
+    if init_means is not None:
+        means = _f32(init_means, dev)
+        if means.ndim != 3 or means.shape[0] != bsz or means.shape[2] != d:
+            raise ValueError("init_means must have shape (B, K, D) matching x")
+        k = means.shape[1]
+        source = "user"
+    else:
+        if init_params not in {"kmeans", "random"}:
+            raise ValueError("init_params must be 'kmeans' or 'random'")
+        k = int(n_components)
+        idx = torch.randint(0, n, (bsz, k), device=dev, generator=generator)
+        means = torch.gather(x, 1, idx[..., None].expand(-1, -1, d)).to(torch.float32).contiguous()
+        source = "random"
+        init_covs, init_weights = None, None
+    if covariance_type == "spherical":
+        covs = _f32(init_covs, dev) if init_covs is not None else global_spherical_variance(x, k, reg_covar)
+        if tuple(covs.shape) != (bsz, k):
+            raise ValueError("init_variances must have shape (B, K)")
+        covs = covs.clamp_min(reg_covar)
+    elif covariance_type == "diag":
+        covs = _f32(init_covs, dev) if init_covs is not None else global_diag_variance(x, k, reg_covar)
+        if tuple(covs.shape) != (bsz, k, d):
+            raise ValueError("init_variances must have shape (B, K, D) for diag covariance")
+        covs = covs.clamp_min(reg_covar)
+    elif covariance_type == "tied":
+        covs = _f32(init_covs, dev) if init_covs is not None else global_tied_covariance(x, reg_covar)
+        if tuple(covs.shape) != (bsz, d, d):
+            raise ValueError("init_variances must have shape (B, D, D) for tied covariance")
+        covs = _sym(covs)
+    else:
+        covs = (_f32(init_covs, dev) if init_covs is not None
+                else global_tied_covariance(x, reg_covar).unsqueeze(1).expand(-1, k, -1, -1))
+        if tuple(covs.shape) != (bsz, k, d, d):
+            raise ValueError("init_variances must have shape (B, K, D, D) for full covariance")
+        covs = _sym(covs)
+    weights = _init_weights(init_weights, bsz, k, dev)
+    return means.contiguous(), covs.contiguous(), weights, source
+
+
+@torch.no_grad()
+def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: int = 100,
+        tol: float = 1e-4, init_means=None, init_covs=None, init_weights=None, verbose: bool = False,
+        init_params: str = "kmeans", reg_covar: float = 1e-6, min_weight: float = 1e-8,
+        compute_labels: bool = True, generator: Optional[torch.Generator] = None,
+        ) -> Tuple[Optional[torch.Tensor], torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, object]]:
+    """Soft EM on the HIP engine; see the module docstring."""
+    if covariance_type not in _COVS:
+        raise ValueError("covariance_type must be 'spherical', 'diag', 'tied' or 'full'")
+    if n_components <= 0:
+        raise ValueError("n_components must be positive")
+    if max_iters <= 0:
+        raise ValueError("max_iters must be positive")
+    if min_weight <= 0.0:
+        raise ValueError("min_weight must be positive")
+    _hip.require_hip()
+    x = _as_device_input(x, covariance_type)
+    bsz, n, d = x.shape
+    if n == 0:
+        raise ValueError("x must contain at least one sample")
+    means, covs, weights, source = initialize(
+        x, covariance_type, n_components, init_means=init_means, init_covs=init_covs,
+        init_weights=init_weights, reg_covar=reg_covar, init_params=init_params, generator=generator)
+    k = means.shape[1]
+    if not _hip.supported(covariance_type, x.dtype, bsz, n, d, k):
+        raise _hip.HipRuntimeError(
+            f"shape not supported by the hip backend: {covariance_type} B={bsz} N={n} D={d} K={k} {x.dtype}")
+    prob = _hip.problem(covariance_type, x.dtype, bsz, n, d, k)
+    ws = _hip.Workspace(prob, x.device)
+    gram = _hip.gram(x, ws) if covariance_type == "tied" else None
+    lb = torch.zeros((max_iters,), dtype=torch.float32, device=x.device)
+    spherical = covariance_type == "spherical"
+    sync_each = bool(verbose or tol > 0.0)
+    prev = None
+    n_iter = 0
+    for it in range(max_iters):
+        _hip.em_step(covariance_type, x, means, covs, weights, lb[it:it + 1], reg_covar=reg_covar,
+                     min_weight=min_weight, gram_xx=gram, ws=ws)
+        n_iter = it + 1
+        if not sync_each:
+            continue
+        value = float(lb[it].item())
+        if verbose:
+            print(f"Iter {it}, lower_bound: {value:.6f}")
+        # Convergence rules: spherical torch_fallback.py:2322-2330, others :2695-2698.
+        last = it + 1 == max_iters
+        if spherical:
+            if not last and prev is not None and abs(value - prev) < tol:
+                break
+            if not last:
+                prev = value
+        else:
+            if tol > 0.0 and prev is not None and abs(value - prev) < tol:
+                break
+            if tol > 0.0:
+                prev = value
+    history = [float(v) for v in lb[:n_iter].tolist()]
+    labels = None
+    if compute_labels:
+        _, labels = _hip.score(covariance_type, x, means, covs, weights, want_scores=False, ws=ws)
+    info: Dict[str, object] = {
+        "n_iter": n_iter,
+        "lower_bound": history[-1],
+        "lower_bound_history": history,
+        "init_source": source,
+        "hip_enabled": True,
+        "triton_estep_enabled": False,
+        "triton_fused_update_enabled": False,
+        "triton_streaming_update_enabled": False,
+        "triton_labels_enabled": False,
+        "approximate_em_enabled": False,
+        "approx_top_k": None,
+        "backend_breakdown": {"hip": n_iter},
+    }
+    return labels, means, covs, weights, info
+
+
+def _api(covariance_type):
+    def run(x, n_components, max_iters=100, tol=1e-4, init_means=None, init_variances=None,
+            init_weights=None, verbose=False, *, init_params="kmeans", reg_covar=1e-6,
+            min_weight=1e-8, compute_labels=True, generator=None, **unused):
+        for key in unused:
+            if key not in {"chunk_size_N", "chunk_size_K", "kmeans_init_iters", "kmeans_init_tol",
+                           "kmeans_use_triton", "gmm_use_triton", "gmm_use_triton_estep",
+                           "gmm_use_triton_streaming_update", "approx_top_k"}:
+                raise TypeError(f"unexpected keyword argument {key!r}")
+        if unused.get("approx_top_k") is not None:
+            raise NotImplementedError("approximate top-k EM is not part of the hip backend")
+        return fit(x, n_components, covariance_type, max_iters=max_iters, tol=tol, init_means=init_means,
+                   init_covs=init_variances, init_weights=init_weights, verbose=verbose,
+                   init_params=init_params, reg_covar=reg_covar, min_weight=min_weight,
+                   compute_labels=compute_labels, generator=generator)
+    run.__name__ = f"batch_gmm_{covariance_type.capitalize()}_hip"
+    run.__doc__ = (f"{covariance_type} soft EM on the HIP engine; signature and return value of "
+                   f"the reference's batch_gmm_*_torch_native (chunk/Triton knobs are accepted and ignored).")
+    return run
+
+
+batch_gmm_Spherical_hip = _api("spherical")
+batch_gmm_Diagonal_hip = _api("diag")
+batch_gmm_Tied_hip = _api("tied")
+batch_gmm_Full_hip = _api("full")

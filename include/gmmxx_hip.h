@@ -1,0 +1,119 @@
+/*
+ * gmmxx_hip.h — C ABI of the MI355X (gfx950) GMM EM engine.
+ *
+ * The library replaces the reference's native extension `gmmxx._C`
+ * (gmmxx/csrc/bindings.cpp:16-191, loaded by gmmxx/_cuda.py:25-32) and the
+ * Triton E/M-step modules for the EM iteration hot path.  All entry points:
+ *   - take plain device pointers, sizes and a hipStream_t passed as void*;
+ *   - allocate nothing: scratch memory comes from the caller's workspace
+ *     (size from gmmxx_hip_workspace_bytes), outputs are caller-owned;
+ *   - are asynchronous on the given stream and never synchronise;
+ *   - return GMMXX_OK (0) or a nonzero status; the message for the calling
+ *     thread is available from gmmxx_hip_last_error().
+ * Data layout: x is row-major (B, N, D) fp32 or bf16; every parameter array is
+ * fp32 row-major in the reference's batched shapes: means (B, K, D), weights
+ * (B, K), covariances spherical (B, K), diag (B, K, D), tied (B, D, D),
+ * full (B, K, D, D).
+ */
+#ifndef GMMXX_HIP_H_
+#define GMMXX_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GMMXX_HIP_ABI_VERSION 1
+
+enum gmmxx_status {
+  GMMXX_OK = 0,
+  GMMXX_ERR_INVALID_ARGUMENT = 1,
+  GMMXX_ERR_UNSUPPORTED = 2,
+  GMMXX_ERR_WORKSPACE = 3,
+  GMMXX_ERR_HIP = 4
+};
+
+enum gmmxx_covariance { GMMXX_SPHERICAL = 0, GMMXX_DIAG = 1, GMMXX_TIED = 2, GMMXX_FULL = 3 };
+enum gmmxx_dtype { GMMXX_F32 = 0, GMMXX_BF16 = 1 };
+
+typedef struct gmmxx_problem {
+  int32_t covariance_type; /* enum gmmxx_covariance */
+  int32_t x_dtype;         /* enum gmmxx_dtype */
+  int64_t B, N, D, K;
+} gmmxx_problem;
+
+/* ABI version of the loaded library (GMMXX_HIP_ABI_VERSION). */
+int gmmxx_hip_abi_version(void);
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* gmmxx_hip_last_error(void);
+
+/* Smoke test: out[i] = in[i] + offset.
+ * Replaces `canary_add_offset` (gmmxx/csrc/canary/canary.cu:21-48, gmmxx/_cuda.py:67-95). */
+int gmmxx_hip_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, void* stream);
+
+/* 1 if the engine supports the problem shape/dtype, else 0.
+ * Replaces the shape gates cuda_{spherical,diag,tied,full}_supported
+ * (gmmxx/_runtime.py:31-191). */
+int gmmxx_hip_supported(const gmmxx_problem* p);
+
+/* Bytes of device workspace every entry point below needs for this problem
+ * (the same size serves all of them); -1 if unsupported. */
+int64_t gmmxx_hip_workspace_bytes(const gmmxx_problem* p);
+
+/* One full soft-EM iteration, in place: the iteration prelude (variance clamp
+ * to reg_covar for spherical/diag, weight floor min_weight and
+ * renormalisation), the E-step log-normaliser and responsibilities, the M-step
+ * sufficient statistics and the finalize.  `lower_bound` (device, 1 float)
+ * receives the mean per-sample log-likelihood under the parameters on entry.
+ * `gram` is XᵀX per batch (B, D, D) for tied (gmmxx_hip_gram), NULL otherwise.
+ * Replaces one loop iteration of batch_gmm_{Spherical,Diagonal}_torch_native
+ * and _batch_gmm_matrix_torch_native (gmmxx/torch_fallback.py:2060-2330,
+ * :2484-2698, :2864-3199) and the CUDA loops _train_{spherical,diag,tied,full}_cuda
+ * (gmmxx/interface.py:666-1275) with their _C calls spherical_fused,
+ * blocked_update_*, finalize_* (gmmxx/csrc/bindings.cpp:60-170). */
+int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float* covariances,
+                      float* weights, const float* gram, double reg_covar, double min_weight,
+                      float* lower_bound, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* E-step + M-step sufficient statistics only (no finalize, parameters untouched;
+ * the iteration prelude is applied to the values used).  Outputs (device):
+ *   nk (B, K); sum_x (B, K, D); sum_q: spherical Σ r‖x‖² (B, K), diag Σ r x² (B, K, D),
+ *   full Σ r xxᵀ (B, K, D, D), tied: pass NULL; ll_sum (1 float): Σ over all rows of
+ *   log Σ_k w_k N(x | k).
+ * Replaces the statistics kernels blocked_update_* / spherical_fused / the
+ * Triton fused_single_tile_update_* (gmmxx/csrc/bindings.cpp:104-170,
+ * gmmxx/fused_update_triton.py:449-659). */
+int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* means,
+                          const float* covariances, const float* weights, double reg_covar,
+                          double min_weight, float* nk, float* sum_x, float* sum_q, float* ll_sum,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Inference under fixed parameters (no prelude): per-sample log-likelihood
+ * `scores` (B, N) and/or first-maximum labels (B, N) int64; either may be NULL.
+ * Replaces spherical/diag/full assign + logsumexp (gmmxx/csrc/bindings.cpp:19-58,
+ * :140-190; gmmxx/_cuda.py:1246-1314) and the torch inference functions
+ * *_assign_torch_native_chunked / *_score_samples_torch_native_chunked
+ * (gmmxx/torch_fallback.py:780-1130). */
+int gmmxx_hip_score(const gmmxx_problem* p, const void* x, const float* means,
+                    const float* covariances, const float* weights, float* scores, int64_t* labels,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Responsibilities (B, N, K) fp32 under fixed parameters.
+ * Replaces *_resp (gmmxx/csrc/bindings.cpp:40-58) and
+ * *_predict_proba_torch_native_chunked (gmmxx/torch_fallback.py:1133-1345). */
+int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* means,
+                            const float* covariances, const float* weights, float* proba,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/* XᵀX per batch (B, D, D) fp32, the fit-constant of the tied M-step
+ * (gmmxx/torch_fallback.py:2856-2862). */
+int gmmxx_hip_gram(const gmmxx_problem* p, const void* x, float* out, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GMMXX_HIP_H_ */

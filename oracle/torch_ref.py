@@ -370,6 +370,78 @@ def _spherical_chunk_n(n, d, k, chunk_size_N):
 
 
 
+def _accumulate(x, x_sq_all, mdl, covariance_type, chunk_n, chunk_size_K, collect=True):
+    """E-step + M-step sufficient statistics of one iteration (the chunk loops of
+    torch_fallback.py:2097-2291, :2500-2652, :2911-3141)."""
+    bsz, n, d = x.shape
+    k = mdl.k
+    spherical = covariance_type == "spherical"
+    nk = torch.zeros((bsz, k), dtype=torch.float32)
+    sum_x = torch.zeros((bsz, k, d), dtype=torch.float32)
+    if spherical:
+        sum_q = torch.zeros((bsz, k), dtype=torch.float32)
+    elif covariance_type == "diag":
+        sum_q = torch.zeros((bsz, k, d), dtype=torch.float32)
+    elif covariance_type == "full":
+        sum_q = torch.zeros((bsz, k, d, d), dtype=torch.float32)
+    else:
+        sum_q = None
+    total_ll = torch.zeros((), dtype=torch.float32)
+    for n0 in range(0, n, chunk_n):
+        n1 = min(n0 + chunk_n, n)
+        xc = x[:, n0:n1, :]
+        xcf = xc.to(torch.float32)
+        xs = x_sq_all[:, n0:n1] if spherical else None
+        if not spherical and k <= chunk_size_K:
+            # Single-K-tile branch (:2602-2620, :3054-3090).
+            logits = mdl.logits(xc, xs, 0, k)
+            lse = torch.logsumexp(logits, dim=-1)
+            if collect:
+                total_ll = total_ll + lse.sum()
+            resp = logits.sub(lse.unsqueeze(-1)).exp_()
+            nk += resp.sum(dim=1)
+            sum_x += torch.bmm(resp.transpose(1, 2), xcf)
+            if covariance_type == "diag":
+                sum_q += torch.bmm(resp.transpose(1, 2), xcf.square())
+            elif covariance_type == "full":
+                sum_q += torch.einsum("bnk,bnd,bne->bkde", resp, xcf, xcf)
+            continue
+        # Streaming branch (:2210-2291, :2622-2652, :3092-3141).
+        lse = mdl.stream_lse(xc, xs, chunk_size_K)
+        if collect:
+            total_ll = total_ll + lse.sum()
+        for k0 in range(0, k, chunk_size_K):
+            k1 = min(k0 + chunk_size_K, k)
+            resp = torch.exp(mdl.logits(xc, xs, k0, k1) - lse.unsqueeze(-1))
+            nk[:, k0:k1] += resp.sum(dim=1)
+            sum_x[:, k0:k1, :] += torch.bmm(resp.transpose(1, 2), xcf)
+            if spherical:
+                sum_q[:, k0:k1] += (resp * xs.unsqueeze(-1)).sum(dim=1)
+            elif covariance_type == "diag":
+                sum_q[:, k0:k1, :] += torch.bmm(resp.transpose(1, 2), xcf.square())
+            elif covariance_type == "full":
+                sum_q[:, k0:k1, :, :] += torch.einsum("bnk,bnd,bne->bkde", resp, xcf, xcf)
+    return nk, sum_x, sum_q, total_ll
+
+
+@torch.no_grad()
+def estep_stats(x, covariance_type, means, covs, weights, *, reg_covar=1e-6, min_weight=1e-8,
+                chunk_size_N=DEFAULT_CHUNK_N, chunk_size_K=DEFAULT_CHUNK_K):
+    """Sufficient statistics (nk, Σr·x, Σr·q(x), Σ lse) of one iteration from
+    the given parameters, after the iteration prelude (:2061-2066, :2486-2490,
+    :2866-2868)."""
+    spherical = covariance_type == "spherical"
+    if covariance_type in ("spherical", "diag"):
+        covs = covs.clamp_min(reg_covar)
+    weights = weights.clamp_min(min_weight)
+    weights = weights / weights.sum(dim=-1, keepdim=True)
+    mdl = _Model(covariance_type, means, covs, weights)
+    x_sq_all = (x.to(torch.float32) ** 2).sum(dim=-1) if spherical else None
+    n, d, k = x.shape[1], x.shape[2], means.shape[1]
+    chunk_n = _spherical_chunk_n(n, d, k, chunk_size_N) if spherical else chunk_size_N
+    return _accumulate(x, x_sq_all, mdl, covariance_type, chunk_n, chunk_size_K)
+
+
 def finalize(covariance_type, nk, sum_x, sum_q, means, covs, *, n, reg_covar=1e-6,
              min_weight=1e-8, total_xx=None, x_dtype=torch.float32):
     """M-step parameter update from sufficient statistics.
@@ -464,52 +536,8 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         weights = weights / weights.sum(dim=-1, keepdim=True)
         mdl = _Model(covariance_type, means, covs, weights)
 
-        nk = torch.zeros((bsz, k), dtype=torch.float32)
-        sum_x = torch.zeros((bsz, k, d), dtype=torch.float32)
-        if spherical:
-            sum_q = torch.zeros((bsz, k), dtype=torch.float32)
-        elif covariance_type == "diag":
-            sum_q = torch.zeros((bsz, k, d), dtype=torch.float32)
-        elif covariance_type == "full":
-            sum_q = torch.zeros((bsz, k, d, d), dtype=torch.float32)
-        else:
-            sum_q = None
-        total_ll = torch.zeros((), dtype=torch.float32)
-
-        for n0 in range(0, n, chunk_n):
-            n1 = min(n0 + chunk_n, n)
-            xc = x[:, n0:n1, :]
-            xcf = xc.to(torch.float32)
-            xs = x_sq_all[:, n0:n1] if spherical else None
-            if not spherical and k <= chunk_size_K:
-                # Single-K-tile branch (:2602-2620, :3054-3090).
-                logits = mdl.logits(xc, xs, 0, k)
-                lse = torch.logsumexp(logits, dim=-1)
-                if collect:
-                    total_ll = total_ll + lse.sum()
-                resp = logits.sub(lse.unsqueeze(-1)).exp_()
-                nk += resp.sum(dim=1)
-                sum_x += torch.bmm(resp.transpose(1, 2), xcf)
-                if covariance_type == "diag":
-                    sum_q += torch.bmm(resp.transpose(1, 2), xcf.square())
-                elif covariance_type == "full":
-                    sum_q += torch.einsum("bnk,bnd,bne->bkde", resp, xcf, xcf)
-                continue
-            # Streaming branch (:2210-2291, :2622-2652, :3092-3141).
-            lse = mdl.stream_lse(xc, xs, chunk_size_K)
-            if collect:
-                total_ll = total_ll + lse.sum()
-            for k0 in range(0, k, chunk_size_K):
-                k1 = min(k0 + chunk_size_K, k)
-                resp = torch.exp(mdl.logits(xc, xs, k0, k1) - lse.unsqueeze(-1))
-                nk[:, k0:k1] += resp.sum(dim=1)
-                sum_x[:, k0:k1, :] += torch.bmm(resp.transpose(1, 2), xcf)
-                if spherical:
-                    sum_q[:, k0:k1] += (resp * xs.unsqueeze(-1)).sum(dim=1)
-                elif covariance_type == "diag":
-                    sum_q[:, k0:k1, :] += torch.bmm(resp.transpose(1, 2), xcf.square())
-                elif covariance_type == "full":
-                    sum_q[:, k0:k1, :, :] += torch.einsum("bnk,bnd,bne->bkde", resp, xcf, xcf)
+        nk, sum_x, sum_q, total_ll = _accumulate(x, x_sq_all, mdl, covariance_type, chunk_n,
+                                                 chunk_size_K, collect)
 
         means_new, covs_new, weights_new = finalize(
             covariance_type, nk, sum_x, sum_q, means, covs, n=n, reg_covar=reg_covar,

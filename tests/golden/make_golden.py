@@ -94,13 +94,15 @@ def cases():
                 "full": torch.eye(d).expand(b, k, d, d).clone()}[cov]
         out.append((f"{cov}_ties", cov, x, dict(init_means=means, init_variances=covs,
                                                   init_weights=None), dict(max_iters=2)))
-    # Singular covariance -> Cholesky jitter ladder (tied and full).
+    # Indefinite covariance -> Cholesky jitter ladder (tied and full).  diag(1, 1, -1e-3)
+    # first factorises at jitter 1e-2 and is then well conditioned; for full only
+    # one component is indefinite, so the batch-global retry is exercised too.
     for cov in ("tied", "full"):
         b, n, d, k = 1, 160, 3, 2
         x = _blobs(g, b, n, d, k, spread=2.0)
-        v = torch.tensor([1.0, 2.0, -1.0])
-        sing = torch.outer(v, v)                      # rank 1, not PD
-        covs = sing.expand(b, d, d).clone() if cov == "tied" else sing.expand(b, k, d, d).clone()
+        bad = torch.diag(torch.tensor([1.0, 1.0, -1e-3]))
+        good = torch.diag(torch.tensor([1.5, 0.8, 1.2]))
+        covs = bad.expand(b, d, d).clone() if cov == "tied" else torch.stack([bad, good]).unsqueeze(0)
         out.append((f"{cov}_jitter", cov, x, dict(init_means=x[:, :k, :].clone(),
                                                     init_variances=covs, init_weights=None),
                     dict(max_iters=2)))

@@ -1,0 +1,236 @@
+"""GPU parity of the HIP engine against the CPU oracle (entry-point level).
+
+Each case draws a seeded problem, runs one C-ABI entry point on the GPU and the
+oracle on the CPU from identical parameters.  Tolerances (stated per check):
+  * fp32 statistics / parameters: rtol 1e-4 (1e-4 relative);
+  * per-iteration mean log-likelihood: rtol 1e-5 fp32, 2e-3 bf16;
+  * labels: equal, except near-ties: rows whose float64 logit gap between the
+    two labels is below 1e-5·max(1, |logit|) (fp32) or 1e-3·max(1, |logit|) (bf16).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import torch_ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def make_problem(cov, b, n, d, k, seed, dtype=torch.float32, spread=4.0, init="centers"):
+    """Seeded blobs.  init="centers" starts the means near the true centres
+    (every component keeps its cluster: well conditioned); init="rows" draws
+    them from data rows (the reference default; components can collapse)."""
+    g = torch.Generator().manual_seed(seed)
+    centers = (torch.rand((b, k, d), generator=g) * 2 - 1) * spread
+    lab = torch.randint(0, k, (b, n), generator=g)
+    x = torch.gather(centers, 1, lab[..., None].expand(-1, -1, d)) + torch.randn((b, n, d), generator=g)
+    x = x.to(dtype).to(torch.float32)            # values exactly representable in dtype
+    if init == "rows":
+        means = x[:, torch.randperm(n, generator=g)[:k], :].clone()
+    else:
+        means = centers + 0.3 * torch.randn((b, k, d), generator=g)
+    if cov == "spherical":
+        covs = torch.rand((b, k), generator=g) + 0.5
+    elif cov == "diag":
+        covs = torch.rand((b, k, d), generator=g) + 0.5
+    else:
+        shape = (b, d, d) if cov == "tied" else (b, k, d, d)
+        a = torch.randn(shape, generator=g) * 0.3
+        covs = a @ a.transpose(-1, -2) + 0.7 * torch.eye(d)
+    w = torch.rand((b, k), generator=g) + 0.2
+    return x, means, covs.float(), (w / w.sum(-1, keepdim=True)).float()
+
+
+def to_dev(x, dtype=torch.float32):
+    return x.to(DEV).to(dtype).contiguous()
+
+
+def assert_labels(got, x, means, covs, w, cov, gap_tol):
+    """Labels equal, except near-ties: |Δlogit| < gap_tol·max(1, |logit|) in float64."""
+    exp = torch_ref.assign(x, means, covs, w, cov)
+    got = got.cpu()
+    bad = (got != exp).nonzero(as_tuple=False)
+    if bad.numel() == 0:
+        return
+    mdl = torch_ref._Model(cov, means.double(), covs.double(), w.double())
+    xs = x.double().square().sum(-1) if cov == "spherical" else None
+    logits = mdl.logits(x.double(), xs, 0, means.shape[1])
+    for bi, ni in bad.tolist():
+        l = logits[bi, ni]
+        gap = abs(float(l[got[bi, ni]] - l[exp[bi, ni]]))
+        scale = max(1.0, abs(float(l[exp[bi, ni]])))
+        assert gap < gap_tol * scale, f"label mismatch at ({bi},{ni}) with logit gap {gap}"
+
+
+CASES = [
+    # cov, B, N, D, K, dtype  -- at least ~50 rows per component (well conditioned)
+    ("spherical", 2, 6000, 32, 64, torch.float32),
+    ("spherical", 1, 24000, 128, 300, torch.float32),     # two k-tiles, partial second tile
+    ("spherical", 1, 30000, 128, 520, torch.bfloat16),    # three k-tiles
+    ("spherical", 2, 6000, 32, 64, torch.bfloat16),
+    ("spherical", 1, 777, 5, 3, torch.float32),           # D and N not multiples of the tile
+    ("diag", 1, 30000, 64, 512, torch.float32),           # two k-tiles
+    ("diag", 2, 3000, 20, 40, torch.float32),
+    ("diag", 1, 2000, 100, 17, torch.float32),
+    ("tied", 1, 20000, 64, 256, torch.float32),
+    ("tied", 2, 1000, 7, 9, torch.float32),
+    ("full", 4, 20000, 16, 32, torch.float32),
+    ("full", 2, 1000, 3, 5, torch.float32),
+]
+
+# Over-parameterised problems (a few rows per component): after one iteration
+# some variances collapse to reg_covar and logits become dist/1e-6, so fp32
+# cancellation noise dominates both implementations.  Judged against float64.
+DEGENERATE = [
+    ("spherical", 1, 2500, 128, 300, torch.float32),
+    ("diag", 1, 3000, 64, 512, torch.float32),
+]
+
+
+def _id(c):
+    return f"{c[0]}-B{c[1]}-N{c[2]}-D{c[3]}-K{c[4]}-{str(c[5]).split('.')[-1]}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=_id)
+def test_estep_stats_match_oracle(hip, case):
+    cov, b, n, d, k, dt = case
+    print(f"[estep_stats] {_id(case)}", flush=True)
+    x, means, covs, w = make_problem(cov, b, n, d, k, seed=11, dtype=dt)
+    nk, sx, sq, ll = hip.estep_stats(cov, to_dev(x, dt), to_dev(means), to_dev(covs), to_dev(w))
+    torch.cuda.synchronize()
+    e_nk, e_sx, e_sq, e_ll = torch_ref.estep_stats(x, cov, means, covs, w)
+    tol = 1e-4 if dt == torch.float32 else 2e-3
+    # Sums of responsibilities: compare against the scale of the whole statistic.
+    torch.testing.assert_close(nk.cpu(), e_nk, rtol=tol, atol=tol * float(e_nk.abs().max()))
+    torch.testing.assert_close(sx.cpu(), e_sx, rtol=tol, atol=tol * float(e_sx.abs().max()))
+    if sq is not None:
+        torch.testing.assert_close(sq.cpu(), e_sq, rtol=tol, atol=tol * float(e_sq.abs().max()))
+    ll_tol = 1e-5 if dt == torch.float32 else 2e-3
+    assert float(ll) == pytest.approx(float(e_ll), rel=ll_tol)
+
+
+@pytest.mark.parametrize("case", CASES, ids=_id)
+def test_score_labels_proba_match_oracle(hip, case):
+    cov, b, n, d, k, dt = case
+    print(f"[score] {_id(case)}", flush=True)
+    x, means, covs, w = make_problem(cov, b, n, d, k, seed=12, dtype=dt)
+    xd = to_dev(x, dt)
+    scores, labels = hip.score(cov, xd, to_dev(means), to_dev(covs), to_dev(w))
+    proba = hip.predict_proba(cov, xd, to_dev(means), to_dev(covs), to_dev(w))
+    torch.cuda.synchronize()
+    e_scores = torch_ref.score_samples(x, means, covs, w, cov)
+    tol = 1e-5 if dt == torch.float32 else 2e-3
+    torch.testing.assert_close(scores.cpu(), e_scores, rtol=tol, atol=tol * float(e_scores.abs().mean()))
+    assert_labels(labels, x, means, covs, w, cov, 1e-5 if dt == torch.float32 else 1e-3)
+    e_proba = torch_ref.predict_proba(x, means, covs, w, cov)
+    torch.testing.assert_close(proba.cpu(), e_proba, rtol=0, atol=2e-4 if dt == torch.float32 else 2e-2)
+    torch.testing.assert_close(proba.sum(-1).cpu(), torch.ones(b, n), rtol=0, atol=1e-4)
+
+
+@pytest.mark.parametrize("case", CASES, ids=_id)
+def test_em_step_matches_oracle_step(hip, case):
+    """Per-iteration parity: from the oracle's state at iteration i, one HIP
+    em_step must reproduce the oracle's iteration i+1 (parameters) and the
+    lower bound of iteration i.  Chaining oracle max_iters=1 calls is the
+    reference's own per-iteration protocol (its init clamps equal the loop
+    prelude, torch_fallback.py:1680-1682 vs :2061-2066)."""
+    cov, b, n, d, k, dt = case
+    print(f"[em-step] {_id(case)}", flush=True)
+    x, means, covs, w = make_problem(cov, b, n, d, k, seed=13, dtype=dt)
+    xd = to_dev(x, dt)
+    gram = hip.gram(xd) if cov == "tied" else None
+    lb = torch.zeros(1, device=DEV)
+    ll_tol = 1e-5 if dt == torch.float32 else 2e-3
+    ptol = 1e-4 if dt == torch.float32 else 2e-3
+    for it in range(4):
+        e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, cov, means, covs, w)
+        m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
+        hip.em_step(cov, xd, m_d, c_d, w_d, lb, gram_xx=gram)
+        torch.cuda.synchronize()
+        assert float(lb) == pytest.approx(e_lb, rel=ll_tol), f"iteration {it}"
+        torch.testing.assert_close(m_d.cpu(), e_m, rtol=ptol, atol=ptol * float(e_m.abs().max()))
+        torch.testing.assert_close(c_d.cpu(), e_c, rtol=ptol, atol=ptol * float(e_c.abs().max()))
+        torch.testing.assert_close(w_d.cpu(), e_w, rtol=ptol, atol=ptol * float(e_w.abs().max()))
+        means, covs, w = e_m, e_c, e_w
+
+
+WELL_CONDITIONED = [c for c in CASES if c[2] // c[4] >= 50]
+
+
+@pytest.mark.parametrize("case", WELL_CONDITIONED, ids=_id)
+def test_em_trajectory_matches_oracle(hip, case):
+    """Ten chained EM iterations (lower-bound history, final parameters, labels)
+    on problems with at least 50 rows per component, where EM is not chaotic."""
+    cov, b, n, d, k, dt = case
+    print(f"[em-traj] {_id(case)}", flush=True)
+    x, means, covs, w = make_problem(cov, b, n, d, k, seed=13, dtype=dt)
+    from gmmxx_amd import em
+    labels, m, c, wt, info = em.fit(to_dev(x, dt), k, cov, max_iters=10, tol=0.0, init_means=means,
+                                    init_covs=covs, init_weights=w)
+    e_lab, e_m, e_c, e_w, e_info = torch_ref.fit(x, k, cov, max_iters=10, tol=0.0, init_means=means,
+                                                 init_covs=covs, init_weights=w)
+    ll_tol = 1e-5 if dt == torch.float32 else 2e-3
+    assert info["n_iter"] == e_info["n_iter"] == 10
+    for got, exp in zip(info["lower_bound_history"], e_info["lower_bound_history"]):
+        assert got == pytest.approx(exp, rel=ll_tol)
+    ptol = 1e-4 if dt == torch.float32 else 2e-3
+    torch.testing.assert_close(m.cpu(), e_m, rtol=ptol, atol=ptol * float(e_m.abs().max()))
+    torch.testing.assert_close(c.cpu(), e_c, rtol=ptol, atol=ptol * float(e_c.abs().max()))
+    torch.testing.assert_close(wt.cpu(), e_w, rtol=ptol, atol=ptol * float(e_w.abs().max()))
+    assert_labels(labels, x, e_m, e_c, e_w, cov, 1e-5 if dt == torch.float32 else 1e-3)
+
+
+def _mean_ll64(cov, x, means, covs, w):
+    """Mean log-likelihood in float64 from scipy densities (independent of both sides)."""
+    import numpy as np
+    from scipy.special import logsumexp
+    from scipy.stats import multivariate_normal
+    b, n, d = x.shape
+    k = means.shape[1]
+    tot = 0.0
+    for bi in range(b):
+        lp = np.zeros((n, k))
+        for ki in range(k):
+            c = covs[bi, ki].double().numpy()
+            c = {"spherical": np.eye(d) * float(covs[bi, ki]) if cov == "spherical" else None,
+                 "diag": np.diag(covs[bi, ki].double().numpy()) if cov == "diag" else None,
+                 "full": c if cov == "full" else None}[cov]
+            lp[:, ki] = np.log(float(w[bi, ki])) + multivariate_normal(
+                means[bi, ki].double().numpy(), c, allow_singular=True).logpdf(x[bi].double().numpy())
+        tot += float(logsumexp(lp, axis=1).sum())
+    return tot / (b * n)
+
+
+@pytest.mark.parametrize("case", DEGENERATE, ids=_id)
+def test_em_step_degenerate_accuracy(hip, case):
+    """On collapsed-variance iterations the HIP lower bound must be at least as
+    close to the float64 value as the fp32 oracle's is (within 4x), or within 1e-5."""
+    cov, b, n, d, k, dt = case
+    print(f"[em-degenerate] {_id(case)}", flush=True)
+    x, means, covs, w = make_problem(cov, b, n, d, k, seed=13, dtype=dt, init="rows")
+    xd = to_dev(x, dt)
+    lb = torch.zeros(1, device=DEV)
+    for it in range(3):
+        e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, cov, means, covs, w)
+        m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
+        hip.em_step(cov, xd, m_d, c_d, w_d, lb)
+        torch.cuda.synchronize()
+        # the parameters this iteration actually used (prelude applied)
+        cu = covs.clamp_min(1e-6) if cov in ("spherical", "diag") else covs
+        wu = w.clamp_min(1e-8)
+        wu = wu / wu.sum(-1, keepdim=True)
+        truth = _mean_ll64(cov, x, means, cu, wu)
+        err_hip, err_ref = abs(float(lb) - truth), abs(e_lb - truth)
+        print(f"  it {it}: truth {truth:.6f} hip {float(lb):.6f} oracle {e_lb:.6f}", flush=True)
+        assert err_hip <= max(4.0 * err_ref, 1e-5 * abs(truth)), (it, truth, float(lb), e_lb)
+        means, covs, w = e_m, e_c, e_w
+
+
+def test_canary(hip):
+    inp = torch.arange(1000, dtype=torch.int32, device=DEV)
+    out = hip.canary_add_offset(inp, 7)
+    assert torch.equal(out.cpu(), torch.arange(1000, dtype=torch.int32) + 7)
