@@ -58,6 +58,7 @@ def _declare(lib):
         "gmmxx_hip_supported": (ctypes.c_int, [P]),
         "gmmxx_hip_workspace_bytes": (i64, [P]),
         "gmmxx_hip_em_step": (ctypes.c_int, [P, vp, vp, vp, vp, vp, f64, f64, vp, vp, i64, vp]),
+        "gmmxx_hip_em_phase": (ctypes.c_int, [P, ctypes.c_int, vp, vp, vp, vp, vp, f64, f64, vp, vp, i64, vp]),
         "gmmxx_hip_estep_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_score": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_predict_proba": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, i64, vp]),
@@ -72,7 +73,7 @@ def _declare(lib):
 
 def exported_symbols() -> Tuple[str, ...]:
     return ("gmmxx_hip_abi_version", "gmmxx_hip_last_error", "gmmxx_hip_canary",
-            "gmmxx_hip_supported", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step",
+            "gmmxx_hip_supported", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_phase",
             "gmmxx_hip_estep_stats", "gmmxx_hip_score", "gmmxx_hip_predict_proba",
             "gmmxx_hip_gram")
 
@@ -241,6 +242,23 @@ def em_step(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: to
     _check(_lib.gmmxx_hip_em_step(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
                                   _ptr(gram_xx), float(reg_covar), float(min_weight), _ptr(lower_bound_out),
                                   ws.ptr, ws.nbytes, _stream(x.device)), "gmmxx_hip_em_step")
+
+
+EM_PHASES = ("prepare", "lse_tile", "combine", "stats_tile", "reduce", "finalize")
+
+
+def em_phase(phase: str, covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+             weights: torch.Tensor, lower_bound_out: torch.Tensor, ws: Workspace, *,
+             reg_covar: float = 1e-6, min_weight: float = 1e-8,
+             gram_xx: Optional[torch.Tensor] = None) -> None:
+    """Runs one phase of em_step (see EM_PHASES) on the current stream; the
+    workspace carries the state between phases."""
+    B, N, D, K = _shape(x, means)
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    _check(_lib.gmmxx_hip_em_phase(ctypes.byref(prob), EM_PHASES.index(phase), _ptr(x), _ptr(means), _ptr(covs),
+                                   _ptr(weights), _ptr(gram_xx), float(reg_covar), float(min_weight),
+                                   _ptr(lower_bound_out), ws.ptr, ws.nbytes, _stream(x.device)),
+           f"gmmxx_hip_em_phase({phase})")
 
 
 def estep_stats(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,

@@ -256,9 +256,9 @@ int64_t gmmxx_hip_workspace_bytes(const gmmxx_problem* p) {
   return (int64_t)pl.total;
 }
 
-int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float* covs, float* weights,
-                      const float* gram, double reg_covar, double min_weight, float* lower_bound,
-                      void* ws, int64_t ws_bytes, void* stream) {
+int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* means, float* covs,
+                       float* weights, const float* gram, double reg_covar, double min_weight,
+                       float* lower_bound, void* ws, int64_t ws_bytes, void* stream) {
   Plan pl;
   int rc = begin(p, &pl, x, ws, ws_bytes);
   if (rc) return rc;
@@ -266,29 +266,74 @@ int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float
   if (pl.cov == TIED && !gram) return fail(GMMXX_ERR_INVALID_ARGUMENT, "tied EM needs the XᵀX buffer");
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   const hipStream_t s = (hipStream_t)stream;
-  if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
-  if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, true, s))) return rc;
-  launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
-  if ((rc = stats_pass(pl, x, ws, s))) return rc;
-  FinalizeArgs f{};
-  f.cov = pl.cov;
-  f.B = pl.B;
-  f.K = pl.K;
-  f.D = pl.D;
-  f.DP = pl.DP;
-  f.JP = pl.JP;
-  f.nk_col = pl.nk_col;
-  f.N = pl.N;
-  f.reg_covar = (float)reg_covar;
-  f.min_weight = (float)min_weight;
-  f.stats = at<float>(ws, pl.o_stats);
-  f.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
-  f.gram = gram;
-  f.means = means;
-  f.covs = covs;
-  f.weights = weights;
-  launch_finalize(f, s);
-  return check_hip("finalize");
+  switch (phase) {
+    case GMMXX_PHASE_PREPARE:
+      return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s);
+    case GMMXX_PHASE_LSE_TILE: {
+      const TileArgs t = tile_args(pl, x, ws);
+      if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_LSE, t, dim3(pl.slices * pl.ktiles, pl.B), pl.nw, s) != 0)
+        return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+      return check_hip("log-normaliser tile kernel");
+    }
+    case GMMXX_PHASE_COMBINE: {
+      CombineArgs c{};
+      c.B = pl.B;
+      c.ktiles = pl.ktiles;
+      c.N = pl.N;
+      c.part_ms = at<float>(ws, pl.o_pms);
+      c.part_idx = at<int>(ws, pl.o_pidx);
+      c.lse2 = at<float>(ws, pl.o_lse2);
+      c.ll_part = at<double>(ws, pl.o_ll);
+      launch_combine(c, s);
+      launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0 / ((double)pl.B * (double)pl.N),
+                       lower_bound, s);
+      return check_hip("combine");
+    }
+    case GMMXX_PHASE_STATS_TILE: {
+      const TileArgs t = tile_args(pl, x, ws);
+      if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_STATS, t, dim3(pl.slices * pl.ktiles, pl.B), pl.nw, s) != 0)
+        return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+      return check_hip("statistics tile kernel");
+    }
+    case GMMXX_PHASE_REDUCE:
+      launch_reduce_slices(at<float>(ws, pl.o_pstats), pl.slices, (int64_t)pl.B * pl.K * pl.JP,
+                           at<float>(ws, pl.o_stats), s);
+      return check_hip("statistics reduction");
+    case GMMXX_PHASE_FINALIZE: {
+      FinalizeArgs f{};
+      f.cov = pl.cov;
+      f.B = pl.B;
+      f.K = pl.K;
+      f.D = pl.D;
+      f.DP = pl.DP;
+      f.JP = pl.JP;
+      f.nk_col = pl.nk_col;
+      f.N = pl.N;
+      f.reg_covar = (float)reg_covar;
+      f.min_weight = (float)min_weight;
+      f.stats = at<float>(ws, pl.o_stats);
+      f.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
+      f.gram = gram;
+      f.means = means;
+      f.covs = covs;
+      f.weights = weights;
+      launch_finalize(f, s);
+      return check_hip("finalize");
+    }
+    default:
+      return fail(GMMXX_ERR_INVALID_ARGUMENT, "unknown phase");
+  }
+}
+
+int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float* covs, float* weights,
+                      const float* gram, double reg_covar, double min_weight, float* lower_bound,
+                      void* ws, int64_t ws_bytes, void* stream) {
+  for (int ph = GMMXX_PHASE_PREPARE; ph <= GMMXX_PHASE_FINALIZE; ++ph) {
+    const int rc = gmmxx_hip_em_phase(p, ph, x, means, covs, weights, gram, reg_covar, min_weight,
+                                      lower_bound, ws, ws_bytes, stream);
+    if (rc) return rc;
+  }
+  return GMMXX_OK;
 }
 
 int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* means, const float* covs,

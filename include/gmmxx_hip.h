@@ -77,6 +77,29 @@ int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float
                       float* weights, const float* gram, double reg_covar, double min_weight,
                       float* lower_bound, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The six phases of gmmxx_hip_em_step, for callers that time or interleave
+ * them; gmmxx_hip_em_step(...) == phases PREPARE..FINALIZE in order with the
+ * same arguments and workspace.  PREPARE: iteration prelude, Cholesky
+ * (tied/full), E-step operand packing, tied row forms.  LSE_TILE: the
+ * log-normaliser tile kernel.  COMBINE: per-row merge of the component tiles
+ * and the lower bound.  STATS_TILE: the responsibilities x statistics tile
+ * kernel.  REDUCE: ordered sum of the per-slice statistics.  FINALIZE: M-step
+ * parameter update.  Same role as the reference's separate _C ops
+ * prepare_spherical_estep / spherical_logsumexp / blocked_update_* /
+ * finalize_* (gmmxx/csrc/bindings.cpp:28-170). */
+enum gmmxx_em_phase {
+  GMMXX_PHASE_PREPARE = 0,
+  GMMXX_PHASE_LSE_TILE = 1,
+  GMMXX_PHASE_COMBINE = 2,
+  GMMXX_PHASE_STATS_TILE = 3,
+  GMMXX_PHASE_REDUCE = 4,
+  GMMXX_PHASE_FINALIZE = 5
+};
+int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* means,
+                       float* covariances, float* weights, const float* gram, double reg_covar,
+                       double min_weight, float* lower_bound, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
 /* E-step + M-step sufficient statistics only (no finalize, parameters untouched;
  * the iteration prelude is applied to the values used).  Outputs (device):
  *   nk (B, K); sum_x (B, K, D); sum_q: spherical Σ r‖x‖² (B, K), diag Σ r x² (B, K, D),
