@@ -194,7 +194,7 @@ int lse_pass(const Plan& pl, const void* x, void* ws, float* scores, int64_t* la
              hipStream_t s) {
   const TileArgs t = tile_args(pl, x, ws);
   const dim3 grid(pl.slices * pl.ktiles, pl.B);
-  if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_LSE, t, grid, pl.nw, s) != 0)
+  if (launch_tile(pl.cov, pl.bf, pl.DP, labels ? MODE_LSE_IDX : MODE_LSE, t, grid, pl.nw, s) != 0)
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
   CombineArgs c{};
   c.B = pl.B;

@@ -3,22 +3,31 @@
 // One workgroup owns a tile of KT = nwaves * CW mixture components and a
 // contiguous slice of rows of one batch.  Each wave keeps the E-step operand W
 // for its CW components resident in VGPRs as MFMA fragments for the whole
-// launch.  Per block of 32 rows the workgroup stages x into LDS, builds the
-// augmented row features, and then:
+// launch.  Rows are processed in blocks of 32 with one barrier per block: the
+// next block's x is fetched into registers before the current block is
+// computed and stashed into the other LDS buffer after it, and the loading
+// threads build the row features (‖x‖², the transposed M-step operand, the
+// xxᵀ products) from their own registers.
 //
-//   MODE_LSE    E-GEMM in "component rows" orientation (C = W·φᵀ) so a lane
-//               holds several components of one data row; per-row max,
-//               scaled sum and first-index argmax over the tile are reduced
-//               across lanes (2 shuffles) and waves (LDS) and written as a
-//               per-k-tile partial.
+//   MODE_LSE / MODE_LSE_IDX
+//               E-GEMM in "component rows" orientation (C = W·φᵀ), so a lane
+//               holds 4·CW/16 components of one data row; per-row max, scaled
+//               sum (and, for _IDX, first-index argmax) are reduced across
+//               lanes with two shuffles and across waves through LDS, and
+//               written as one partial per row and component tile.
 //   MODE_STATS  E-GEMM in "data rows" orientation (C = φ·Wᵀ); the epilogue turns
 //               logits into responsibilities r = 2^(l2 - lse2) in registers and
-//               feeds them directly as the A operand of the M-GEMM
-//               acc += rᵀ·ψ, so the (B, N, K) responsibility matrix never
-//               exists.  Each workgroup writes one partial statistics tile.
+//               feeds them directly as the A operand of the M-GEMM acc += rᵀ·ψ,
+//               so the (B, N, K) responsibility matrix never exists.  Each
+//               workgroup writes one partial statistics tile.
 //   MODE_PROBA  Same epilogue; r is written out (predict_proba needs it).
 //
-// Logits are kept in log2 units (l2 = l·log2 e) so exp2 maps to v_exp_f32.
+// Logits are kept in log2 units (l2 = l·log2 e) so exp2 maps to v_exp_f32:
+//   l2 = A_k·S + (a_k·rowq_n + C_k)
+// with S the E-GEMM output, rowq_n the per-row term (‖x‖² spherical, xᵀPx
+// tied, 0 otherwise) and (A_k, a_k, C_k) per-component constants.  The
+// reference clamps the squared distance at 0 before scaling; that clamp only
+// removes negative rounding residue and is dropped here.
 // bf16 inputs multiply exact bf16 x against a hi/lo bf16 split of the fp32
 // operand, which keeps the cross term at fp32-oracle noise level.
 
@@ -37,29 +46,46 @@ __host__ __device__ constexpr int cw_for() {
 template <typename T>
 __device__ __forceinline__ T ld16(const void* p) { return *reinterpret_cast<const T*>(p); }
 
+// Packed upper-triangle index -> (d, e) for the full covariance (DP = 16).
+struct SymTable {
+  unsigned char d[136], e[136];
+  constexpr SymTable() : d(), e() {
+    int s = 0;
+    for (int i = 0; i < 16; ++i)
+      for (int j = i; j < 16; ++j) { d[s] = (unsigned char)i; e[s] = (unsigned char)j; ++s; }
+  }
+};
+
 template <int COV, typename XT, int DP, int CW, int MODE>
 __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr bool BF = sizeof(XT) == 2;
+  constexpr bool LSE = (MODE == MODE_LSE || MODE == MODE_LSE_IDX);
+  constexpr bool WANT_IDX = MODE == MODE_LSE_IDX;
   using Dm = Dims<COV, DP, BF>;
   constexpr int EP = Dm::EP, JP = Dm::JP, J = Dm::J, S = Dm::S;
   constexpr int CT = CW / 16;
   constexpr int ECH = BF ? EP / 32 : EP / 16;
   constexpr int JT = JP / 16;
-  constexpr int XS = DP + (BF ? 8 : 4);                 // xs row stride, elements
-  constexpr int PS = EP + 4;                             // φ row stride (full only)
-  constexpr int QS = kBN + (BF ? 8 : 4);                 // ψᵀ row stride, elements
-  constexpr float SC = (COV == SPH || COV == TIED) ? -2.f : 1.f;
+  constexpr int VEC = 16 / sizeof(XT);                   // elements per 16-byte chunk
+  constexpr int CPR = DP / VEC;                          // chunks per row
+  constexpr int NCH = kBN * CPR;                         // chunks per row block
+  constexpr int PF = (NCH + 511) / 512;                  // prefetched chunks per thread at 512 threads
+  constexpr bool PSI_LDS = BF && MODE == MODE_STATS;     // materialised ψᵀ (bf16 spherical)
+  constexpr int XS = DP + (BF ? 8 : 4);                  // staged-row stride, elements
+  constexpr int PS = EP + 4;                             // φ row stride (full)
+  constexpr int QS = kBN + 8;                            // ψᵀ row stride, bf16 elements
   using FT = typename std::conditional<BF, __bf16, float>::type;
   using WF = typename std::conditional<BF, bf16x8, f32x4>::type;
+  static_assert(NCH % 64 == 0, "row block must split into whole waves of chunks");
 
-  __shared__ __align__(16) XT xs[kBN * XS];
-  __shared__ __align__(16) float phi[COV == FULL ? kBN * PS : 4];
-  __shared__ __align__(16) FT psiT[MODE == MODE_STATS ? JP * QS : 8];
-  __shared__ float rowq_s[kBN];
-  __shared__ float lse_s[kBN];
-  __shared__ float red_m[MODE == MODE_LSE ? 8 * kBN : 1];
-  __shared__ float red_s[MODE == MODE_LSE ? 8 * kBN : 1];
-  __shared__ int red_i[MODE == MODE_LSE ? 8 * kBN : 1];
+  __shared__ __align__(16) XT xs[COV == FULL ? 8 : 2 * kBN * XS];
+  __shared__ __align__(16) float phi[COV == FULL ? 2 * kBN * PS : 4];
+  __shared__ __align__(16) FT psiT[PSI_LDS ? 2 * JP * QS : 8];
+  __shared__ float rowq_s[2 * kBN];
+  __shared__ float lse_s[2 * kBN];
+  __shared__ float red_m[LSE ? 2 * 8 * kBN : 1];
+  __shared__ float red_s[LSE ? 2 * 8 * kBN : 1];
+  __shared__ int red_i[WANT_IDX ? 2 * 8 * kBN : 1];
 
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
@@ -106,6 +132,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       }
     }
   }
+  // (A_k, a_k, C_k): l2 = A_k*S + fma(a_k, rowq_n, C_k); invalid components get C = -inf.
   const float4 kInvalid = make_float4(0.f, 0.f, -INFINITY, 0.f);
   float4 cS[CT];           // data-row orientation: component kbase + 16ct + li
   float4 cL[CT][4];        // component-row orientation: kbase + 16ct + 4g + v
@@ -126,107 +153,159 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) acc[ct][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // ψᵀ padding rows [J, JP) stay zero for the whole launch.
-    for (int i = tid; i < (JP - J) * QS; i += nthr) psiT[J * QS + i] = (FT)0.f;
+  }
+  // Constant feature rows, written once for both buffers.
+  if constexpr (PSI_LDS) {
+    for (int i = tid; i < 2 * (JP - DP) * QS; i += nthr) {
+      const int bufi = i / ((JP - DP) * QS), rem = i % ((JP - DP) * QS);
+      const int j = DP + rem / QS;
+      psiT[bufi * JP * QS + j * QS + rem % QS] = (FT)(j == DP ? 1.f : 0.f);
+    }
+  }
+  if constexpr (COV == FULL) {
+    for (int i = tid; i < 2 * kBN * (EP - S - DP); i += nthr) {
+      const int row = i / (EP - S - DP), c = i % (EP - S - DP);
+      phi[row * PS + S + DP + c] = 0.f;
+    }
   }
 
   const XT* xb = reinterpret_cast<const XT*>(a.x) + (size_t)b * N * D;
 
-  // φ fragment (4 consecutive E-step features of one LDS row), fp32 path.
-  auto phi4 = [&](int r, int e0) -> f32x4 {
-    if constexpr (COV == FULL) {
-      return ld16<f32x4>(&phi[r * PS + e0]);
-    } else if constexpr (COV == DIAG) {
-      const int c = e0 < DP ? e0 : e0 - DP;
-      f32x4 v = ld16<f32x4>(&xs[r * XS + c]);
-      if (e0 < DP) v = v * v;
-      return v;
-    } else {
-      return ld16<f32x4>(&xs[r * XS + e0]);
+  // ---- row-block loader ----
+  uint4 pf[PF];
+  auto load_chunk = [&](int c, int64_t n0) -> uint4 {
+    const int r = c / CPR, cc = (c % CPR) * VEC;
+    const int64_t n = n0 + r;
+    if (n >= rend) return make_uint4(0, 0, 0, 0);
+    if (a.vec_ok) return *reinterpret_cast<const uint4*>(xb + (size_t)n * D + cc);
+    union { uint4 u; XT e[VEC]; } t;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) t.e[j] = (cc + j < D) ? xb[(size_t)n * D + cc + j] : (XT)0.f;
+    return t.u;
+  };
+  auto fetch = [&](int64_t n0) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int c = tid + i * nthr;
+      if (c < NCH) pf[i] = load_chunk(c, n0);
+    }
+  };
+  // Writes the block's staged rows and features into buffer `buf`.
+  auto stash = [&](int buf, int64_t n0) {
+    int i = 0;
+    for (int c = tid; c < NCH; c += nthr, ++i) {          // uniform per wave (NCH % 64 == 0)
+      const uint4 raw = (i < PF) ? pf[i < PF ? i : 0] : load_chunk(c, n0);
+      const int r = c / CPR, cc = (c % CPR) * VEC;
+      const int64_t n = n0 + r;
+      union { uint4 u; XT e[VEC]; } t;
+      t.u = raw;
+      float v[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) v[j] = to_f32(t.e[j]);
+      if constexpr (COV != FULL) {
+        *reinterpret_cast<uint4*>(&xs[buf * kBN * XS + r * XS + cc]) = raw;
+      }
+      if constexpr (PSI_LDS) {
+        FT* pt = psiT + buf * JP * QS;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) pt[(cc + j) * QS + r] = t.e[j];
+      }
+      if constexpr (COV == SPH) {
+        float q = 0.f;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) q = fmaf(v[j], v[j], q);
+#pragma unroll
+        for (int off = 1; off < CPR; off *= 2) q += __shfl_xor(q, off);
+        if (cc == 0) {
+          rowq_s[buf * kBN + r] = q;
+          if constexpr (PSI_LDS) {
+            const __bf16 hi = (__bf16)q;
+            psiT[buf * JP * QS + (DP + 1) * QS + r] = hi;
+            psiT[buf * JP * QS + (DP + 2) * QS + r] = (__bf16)(q - (float)hi);
+          }
+        }
+      } else if constexpr (COV == TIED) {
+        if (cc == 0) rowq_s[buf * kBN + r] = (n < rend) ? a.rowq[(size_t)b * N + n] : 0.f;
+      } else {
+        if (cc == 0) rowq_s[buf * kBN + r] = 0.f;
+      }
+      if constexpr (COV == FULL) {
+        // Gather the row (CPR = 4 consecutive lanes) and write this lane's share of
+        // the packed xxᵀ products plus its own x values into φ.
+        float* pr = phi + (buf * kBN + r) * PS;
+        const int q0 = lane & ~(CPR - 1), mine = lane - q0;
+        float xr[DP];
+#pragma unroll
+        for (int qq = 0; qq < CPR; ++qq)
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) xr[qq * VEC + j] = __shfl(v[j], q0 + qq);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) pr[S + cc + j] = v[j];
+        // Lane `mine` of the row's 4 lanes writes the products s with s % 4 == mine.
+        constexpr SymTable tab{};
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+          if ((s & (CPR - 1)) == mine) pr[s] = xr[tab.d[s]] * xr[tab.e[s]];
+      }
+      if constexpr (!LSE) {
+        if (cc == 0) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
+      }
     }
   };
 
-  for (int64_t n0 = rbeg; n0 < rend; n0 += kBN) {
-    __syncthreads();
-    // ---- stage x rows [n0, n0 + 32) into LDS, zero-padded ----
-    constexpr int VEC = 16 / sizeof(XT);
-    if (a.vec_ok) {
-      for (int c = tid; c < kBN * DP / VEC; c += nthr) {
-        const int r = c / (DP / VEC), cc = (c % (DP / VEC)) * VEC;
-        const int64_t n = n0 + r;
-        if (n < rend) {
-          *reinterpret_cast<uint4*>(&xs[r * XS + cc]) =
-              *reinterpret_cast<const uint4*>(xb + (size_t)n * D + cc);
-        } else {
-          *reinterpret_cast<uint4*>(&xs[r * XS + cc]) = make_uint4(0, 0, 0, 0);
-        }
-      }
-    } else {
-      for (int c = tid; c < kBN * DP; c += nthr) {
-        const int r = c / DP, cc = c % DP;
-        const int64_t n = n0 + r;
-        xs[r * XS + cc] = (n < rend && cc < D) ? xb[(size_t)n * D + cc] : (XT)0.f;
-      }
-    }
-    __syncthreads();
-
-    // ---- row quantities and feature tiles ----
-    if (tid < kBN) {
-      const int r = tid;
-      const int64_t n = n0 + r;
-      float q = 0.f;
-      if constexpr (COV == SPH) {
-        for (int d = 0; d < DP; ++d) { const float v = to_f32(xs[r * XS + d]); q = fmaf(v, v, q); }
-      } else if constexpr (COV == TIED) {
-        q = (n < rend) ? a.rowq[(size_t)b * N + n] : 0.f;
-      }
-      rowq_s[r] = q;
-      if constexpr (MODE != MODE_LSE) lse_s[r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
-      if constexpr (MODE == MODE_STATS && COV == SPH) {
-        if constexpr (BF) {
-          const __bf16 hi = (__bf16)q;
-          psiT[(DP + 1) * QS + r] = hi;
-          psiT[(DP + 2) * QS + r] = (__bf16)(q - (float)hi);
-        } else {
-          psiT[(DP + 1) * QS + r] = q;
-          psiT[(DP + 2) * QS + r] = 0.f;
-        }
-        psiT[DP * QS + r] = (FT)1.f;
-      }
-    }
-    if constexpr (MODE == MODE_STATS) {
-      for (int i = tid; i < DP * kBN; i += nthr) {
-        const int d = i / kBN, r = i % kBN;
-        const XT v = xs[r * XS + d];
-        psiT[d * QS + r] = (FT)v;
-        if constexpr (COV == DIAG) { const float f = to_f32(v); psiT[(DP + d) * QS + r] = f * f; }
-      }
-      if constexpr (COV == DIAG || COV == TIED) {
-        for (int r = tid; r < kBN; r += nthr) psiT[(COV == DIAG ? 2 * DP : DP) * QS + r] = (FT)1.f;
-      }
-    }
+  // φ fragment (4 consecutive E-step features of staged row r), fp32 path.
+  auto phi4 = [&](int buf, int r, int e0) -> f32x4 {
     if constexpr (COV == FULL) {
-      for (int i = tid; i < kBN * DP; i += nthr) {
-        const int r = i / DP, d = i % DP;
-        const float xd = to_f32(xs[r * XS + d]);
-        for (int e = d; e < DP; ++e) {
-          const float p = xd * to_f32(xs[r * XS + e]);
-          const int s = sym_index(d, e, DP);
-          phi[r * PS + s] = p;
-          if constexpr (MODE == MODE_STATS) psiT[(DP + s) * QS + r] = p;
-        }
-        phi[r * PS + S + d] = xd;
-      }
-      for (int i = tid; i < kBN * (EP - S - DP); i += nthr) {
-        const int r = i / (EP - S - DP), c = i % (EP - S - DP);
-        phi[r * PS + S + DP + c] = 0.f;
-      }
-      if constexpr (MODE == MODE_STATS)
-        for (int r = tid; r < kBN; r += nthr) psiT[(DP + S) * QS + r] = 1.f;
+      return ld16<f32x4>(&phi[(buf * kBN + r) * PS + e0]);
+    } else if constexpr (COV == DIAG) {
+      const int c = e0 < DP ? e0 : e0 - DP;
+      f32x4 v = ld16<f32x4>(&xs[buf * kBN * XS + r * XS + c]);
+      if (e0 < DP) v = v * v;
+      return v;
+    } else {
+      return ld16<f32x4>(&xs[buf * kBN * XS + r * XS + e0]);
     }
-    __syncthreads();
+  };
+  // ψ element (M-step feature j of staged row r), fp32 path.
+  auto psi1 = [&](int buf, int r, int j) -> float {
+    if constexpr (COV == FULL) {
+      const float* pr = phi + (buf * kBN + r) * PS;
+      if (j < DP) return pr[S + j];
+      if (j < DP + S) return pr[j - DP];
+      return j == DP + S ? 1.f : 0.f;
+    } else {
+      const float* xr = reinterpret_cast<const float*>(xs) + buf * kBN * XS + r * XS;
+      if (j < DP) return xr[j];
+      if constexpr (COV == SPH) return j == DP ? 1.f : (j == DP + 1 ? rowq_s[buf * kBN + r] : 0.f);
+      if constexpr (COV == DIAG) {
+        if (j < 2 * DP) { const float t = xr[j - DP]; return t * t; }
+        return j == 2 * DP ? 1.f : 0.f;
+      }
+      return j == DP ? 1.f : 0.f;  // tied
+    }
+  };
 
-    if constexpr (MODE == MODE_LSE) {
+  // Cross-wave merge of one block's per-row partials, written to global memory.
+  auto combine_out = [&](int buf, int64_t n0) {
+    if (tid < kBN) {
+      const int64_t n = n0 + tid;
+      const int base = buf * 8 * kBN;
+      float m = red_m[base + tid], s = red_s[base + tid];
+      int idx = WANT_IDX ? red_i[base + tid] : 0;
+      for (int w = 1; w < nw; ++w) {
+        const int o = base + w * kBN + tid;
+        lse_merge(m, s, idx, red_m[o], red_s[o], WANT_IDX ? red_i[o] : 0);
+      }
+      if (n < rend) {
+        const size_t o = ((size_t)ktile * a.B + b) * N + n;
+        reinterpret_cast<float2*>(a.part_ms)[o] = make_float2(m, s);
+        if constexpr (WANT_IDX) a.part_idx[o] = idx;
+      }
+    }
+  };
+
+  auto compute = [&](int buf, int64_t n0) {
+    if constexpr (LSE) {
       // ---- E-GEMM, component-row orientation: T[ct][nt] = W(16 comps) · φᵀ(16 rows) ----
       f32x4 T[CT][2];
 #pragma unroll
@@ -236,7 +315,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         if constexpr (BF) {
           bf16x8 bx[2];
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) bx[nt] = ld16<bf16x8>(&xs[(16 * nt + li) * XS + 32 * ec + 8 * g]);
+          for (int nt = 0; nt < 2; ++nt)
+            bx[nt] = ld16<bf16x8>(&xs[buf * kBN * XS + (16 * nt + li) * XS + 32 * ec + 8 * g]);
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -247,7 +327,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         } else {
           f32x4 b4[2];
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) b4[nt] = phi4(16 * nt + li, 16 * ec + 4 * g);
+          for (int nt = 0; nt < 2; ++nt) b4[nt] = phi4(buf, 16 * nt + li, 16 * ec + 4 * g);
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -256,11 +336,11 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               for (int t = 0; t < 4; ++t) T[ct][nt] = mfma_f32(whi[ct][ec][t], b4[nt][t], T[ct][nt]);
         }
       }
-      // ---- per data row: max / argmax / scaled sum over this wave's components ----
+      // ---- per data row: max (argmax) and scaled sum over this wave's components ----
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const int r = 16 * nt + li;
-        const float rq = rowq_s[r];
+        const float rq = rowq_s[buf * kBN + r];
         float l2v[CT][4];
         float m = -INFINITY;
         int idx = 0x7fffffff;
@@ -268,11 +348,14 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            float t = fmaf(T[ct][nt][v], SC, rq + cL[ct][v].x);
-            t = fmaxf(t, 0.f);
-            const float l2 = fmaf(t, cL[ct][v].y, cL[ct][v].z);
+            const float4 c = cL[ct][v];
+            const float l2 = fmaf(c.x, T[ct][nt][v], fmaf(c.y, rq, c.z));
             l2v[ct][v] = l2;
-            if (l2 > m) { m = l2; idx = kbase + 16 * ct + 4 * g + v; }
+            if constexpr (WANT_IDX) {
+              if (l2 > m) { m = l2; idx = kbase + 16 * ct + 4 * g + v; }
+            } else {
+              m = fmaxf(m, l2);
+            }
           }
         float s = 0.f;
         if (m != -INFINITY) {
@@ -285,26 +368,14 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         for (int off = 16; off <= 32; off *= 2) {
           const float m2 = __shfl_xor(m, off);
           const float s2 = __shfl_xor(s, off);
-          const int i2 = __shfl_xor(idx, off);
+          const int i2 = WANT_IDX ? __shfl_xor(idx, off) : 0;
           lse_merge(m, s, idx, m2, s2, i2);
         }
         if (g == 0) {
-          red_m[wave * kBN + r] = m;
-          red_s[wave * kBN + r] = s;
-          red_i[wave * kBN + r] = idx;
-        }
-      }
-      __syncthreads();
-      if (tid < kBN) {
-        const int64_t n = n0 + tid;
-        float m = red_m[tid], s = red_s[tid];
-        int idx = red_i[tid];
-        for (int w = 1; w < nw; ++w) lse_merge(m, s, idx, red_m[w * kBN + tid], red_s[w * kBN + tid], red_i[w * kBN + tid]);
-        if (n < rend) {
-          const size_t o = ((size_t)ktile * a.B + b) * N + n;
-          a.part_ms[2 * o] = m;
-          a.part_ms[2 * o + 1] = s;
-          a.part_idx[o] = idx;
+          const int o = buf * 8 * kBN + wave * kBN + r;
+          red_m[o] = m;
+          red_s[o] = s;
+          if constexpr (WANT_IDX) red_i[o] = idx;
         }
       }
     } else {
@@ -315,11 +386,12 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
 #pragma unroll
       for (int ec = 0; ec < ECH; ++ec) {
         if constexpr (BF) {
-          // Row permutation: tile rt, A-row i  ->  data row 8(i/4) + 4rt + i%4, so that
+          // Row permutation: tile rt, A-row i -> data row 8(i/4) + 4rt + i%4, so that
           // C-row 4g+v of tile rt is data row 8g + 4rt + v (8 consecutive rows per lane group).
           bf16x8 ax[2];
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt) ax[rt] = ld16<bf16x8>(&xs[(8 * (li / 4) + 4 * rt + (li % 4)) * XS + 32 * ec + 8 * g]);
+          for (int rt = 0; rt < 2; ++rt)
+            ax[rt] = ld16<bf16x8>(&xs[buf * kBN * XS + (8 * (li / 4) + 4 * rt + (li % 4)) * XS + 32 * ec + 8 * g]);
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -330,7 +402,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         } else {
           f32x4 a4[2];
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt) a4[rt] = phi4(16 * rt + li, 16 * ec + 4 * g);
+          for (int rt = 0; rt < 2; ++rt) a4[rt] = phi4(buf, 16 * rt + li, 16 * ec + 4 * g);
 #pragma unroll
           for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -339,43 +411,53 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               for (int t = 0; t < 4; ++t) Sv[rt][ct] = mfma_f32(a4[rt][t], whi[ct][ec][t], Sv[rt][ct]);
         }
       }
+      // Responsibilities for every component tile of this wave.
+      float rr[CT][2][4];
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         const float4 c = cS[ct];
-        float rr[2][4];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int r = BF ? 8 * g + 4 * rt + v : 16 * rt + 4 * g + v;
-            float t = fmaf(Sv[rt][ct][v], SC, rowq_s[r] + c.x);
-            t = fmaxf(t, 0.f);
-            const float l2 = fmaf(t, c.y, c.z);
-            rr[rt][v] = fast_exp2(l2 - lse_s[r]);
+            const float l2 = fmaf(c.x, Sv[rt][ct][v], fmaf(c.y, rowq_s[buf * kBN + r], c.z));
+            rr[ct][rt][v] = fast_exp2(l2 - lse_s[buf * kBN + r]);
           }
-        if constexpr (MODE == MODE_STATS) {
-          if constexpr (BF) {
-            bf16x8 ar;
+      }
+      if constexpr (MODE == MODE_STATS) {
+        // M-GEMM: each ψ fragment is loaded once and used by every component tile.
+        if constexpr (BF) {
+          bf16x8 ar[CT];
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-              for (int v = 0; v < 4; ++v) ar[4 * rt + v] = (__bf16)rr[rt][v];
+              for (int v = 0; v < 4; ++v) ar[ct][4 * rt + v] = (__bf16)rr[ct][rt][v];
 #pragma unroll
-            for (int jt = 0; jt < JT; ++jt) {
-              const bf16x8 bq = ld16<bf16x8>(&psiT[(16 * jt + li) * QS + 8 * g]);
-              acc[ct][jt] = mfma_bf16(ar, bq, acc[ct][jt]);
-            }
-          } else {
+          for (int jt = 0; jt < JT; ++jt) {
+            const bf16x8 bqv = ld16<bf16x8>(&psiT[buf * JP * QS + (16 * jt + li) * QS + 8 * g]);
 #pragma unroll
-            for (int jt = 0; jt < JT; ++jt)
-#pragma unroll
-              for (int rt = 0; rt < 2; ++rt) {
-                const f32x4 bq = ld16<f32x4>(&psiT[(16 * jt + li) * QS + 16 * rt + 4 * g]);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[ct][jt] = mfma_f32(rr[rt][v], bq[v], acc[ct][jt]);
-              }
+            for (int ct = 0; ct < CT; ++ct) acc[ct][jt] = mfma_bf16(ar[ct], bqv, acc[ct][jt]);
           }
-        } else {  // MODE_PROBA
+        } else {
+#pragma unroll
+          for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+              float bq[4];
+#pragma unroll
+              for (int v = 0; v < 4; ++v) bq[v] = psi1(buf, 16 * rt + 4 * g + v, 16 * jt + li);
+#pragma unroll
+              for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[ct][jt] = mfma_f32(rr[ct][rt][v], bq[v], acc[ct][jt]);
+            }
+        }
+      } else {  // MODE_PROBA
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
           const int kk = kbase + 16 * ct + li;
           if (kk < K) {
 #pragma unroll
@@ -384,12 +466,36 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               for (int v = 0; v < 4; ++v) {
                 const int r = BF ? 8 * g + 4 * rt + v : 16 * rt + 4 * g + v;
                 const int64_t n = n0 + r;
-                if (n < rend) a.proba[((size_t)b * N + n) * K + kk] = rr[rt][v];
+                if (n < rend) a.proba[((size_t)b * N + n) * K + kk] = rr[ct][rt][v];
               }
           }
         }
       }
     }
+  };
+
+  // ---- main loop: one barrier per block ----
+  const int64_t nblk = (rend > rbeg) ? (rend - rbeg + kBN - 1) / kBN : 0;
+  __syncthreads();  // constant feature rows are in place before the first stash overwrites any
+  if (nblk > 0) {
+    fetch(rbeg);
+    stash(0, rbeg);
+  }
+  __syncthreads();
+  for (int64_t ib = 0; ib < nblk; ++ib) {
+    const int buf = (int)(ib & 1);
+    const int64_t n0 = rbeg + ib * kBN;
+    const bool more = ib + 1 < nblk;
+    if (more) fetch(n0 + kBN);
+    if constexpr (LSE) {
+      if (ib > 0) combine_out(buf ^ 1, n0 - kBN);
+    }
+    compute(buf, n0);
+    if (more) stash(buf ^ 1, n0 + kBN);
+    __syncthreads();
+  }
+  if constexpr (LSE) {
+    if (nblk > 0) combine_out((int)((nblk - 1) & 1), rbeg + (nblk - 1) * kBN);
   }
 
   if constexpr (MODE == MODE_STATS) {
@@ -413,6 +519,7 @@ static int launch_tile_t(int mode, const TileArgs& a, dim3 grid, int nw, hipStre
   const dim3 block(64 * nw);
   switch (mode) {
     case MODE_LSE: em_tile_kernel<COV, XT, DP, CW, MODE_LSE><<<grid, block, 0, s>>>(a); break;
+    case MODE_LSE_IDX: em_tile_kernel<COV, XT, DP, CW, MODE_LSE_IDX><<<grid, block, 0, s>>>(a); break;
     case MODE_STATS: em_tile_kernel<COV, XT, DP, CW, MODE_STATS><<<grid, block, 0, s>>>(a); break;
     case MODE_PROBA: em_tile_kernel<COV, XT, DP, CW, MODE_PROBA><<<grid, block, 0, s>>>(a); break;
     default: return -1;

@@ -133,7 +133,10 @@ __global__ void prep_kernel(PrepArgs a) {
     ca = -0.5f * kLog2e;
     cb = (lw - 0.5f * (log2pi_d + a.logdet[bk])) * kLog2e;
   }
-  a.cconst[bk] = make_float4(colq, ca, cb, 0.f);
+  // l2 = ca * (sc * S + rowq + colq) + cb, folded to A*S + fma(a, rowq, C) for the tile kernel
+  // (sc = -2 where S is the cross term x·μ / x·Pμ, 1 where W already carries it).
+  const float sc = (a.cov == SPH || a.cov == TIED) ? -2.f : 1.f;
+  a.cconst[bk] = make_float4(sc * ca, ca, fmaf(ca, colq, cb), 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -276,7 +279,8 @@ __global__ void combine_kernel(CombineArgs a) {
     int idx = 0x7fffffff;
     for (int t = 0; t < a.ktiles; ++t) {
       const size_t o = ((size_t)t * a.B + b) * a.N + n;
-      lse_merge(m, s, idx, a.part_ms[2 * o], a.part_ms[2 * o + 1], a.part_idx[o]);
+      // Argmax partials exist only when the tile pass tracked them (labels requested).
+      lse_merge(m, s, idx, a.part_ms[2 * o], a.part_ms[2 * o + 1], a.labels ? a.part_idx[o] : 0);
     }
     const float lse2 = m + __log2f(s);
     const size_t o = (size_t)b * a.N + n;
