@@ -3,11 +3,13 @@
 // One workgroup owns a tile of KT = nwaves * CW mixture components and a
 // contiguous slice of rows of one batch.  Each wave keeps the E-step operand W
 // for its CW components resident in VGPRs as MFMA fragments for the whole
-// launch.  Rows are processed in blocks of 32 with one barrier per block: the
-// next block's x is fetched into registers before the current block is
-// computed and stashed into the other LDS buffer after it, and the loading
-// threads build the row features (‖x‖², the transposed M-step operand, the
-// xxᵀ products) from their own registers.
+// launch.  Rows are processed in blocks of 32 with one barrier per block: a
+// later block's x is fetched into registers before the current block is
+// computed and stashed into a free LDS buffer after it; the loading threads
+// build ‖x‖² and the xxᵀ products from their own registers.  For bf16 the
+// transposed M-step operand ψᵀ is built from the staged rows one block ahead
+// (the loader then runs two blocks ahead over three row buffers), which keeps
+// the LDS traffic free of bank conflicts.
 //
 //   MODE_LSE / MODE_LSE_IDX
 //               E-GEMM in "component rows" orientation (C = W·φᵀ), so a lane
@@ -46,6 +48,61 @@ __host__ __device__ constexpr int cw_for() {
 template <typename T>
 __device__ __forceinline__ T ld16(const void* p) { return *reinterpret_cast<const T*>(p); }
 
+// Lane maxima start at this floor instead of -inf so merges need no guards;
+// invalid components still contribute exp2(-inf - m) = 0.
+constexpr float kLogFloor = -1e30f;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over groups of G consecutive lanes (G = 1, 2, 4, 8, 16, 32), result in every lane.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 2) v += dpp<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (G >= 4) v += dpp<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (G >= 8) v += dpp<0x141>(v);   // row_half_mirror: the other quad of 8
+  if constexpr (G >= 16) v += dpp<0x140>(v);  // row_mirror: the other half of 16
+  if constexpr (G >= 32) {
+    const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+  }
+  return v;
+}
+
+// Symmetric merge of two (max, scaled sum, argmax) partials; both partners of
+// a lane swap compute bit-identical results.
+__device__ __forceinline__ void merge_sym(float& m, float& s, int& idx, float m2, float s2, int i2, bool with_idx) {
+  const float M = fmaxf(m, m2);
+  const float e1 = s * fast_exp2(m - M), e2 = s2 * fast_exp2(m2 - M);
+  if (with_idx) idx = (m2 > m || (m2 == m && i2 < idx)) ? i2 : idx;
+  m = M;
+  s = e1 + e2;
+}
+
+// Merge with the partner lane l ^ 16 (OFF = 16) or l ^ 32 (OFF = 32), no LDS.
+template <int OFF>
+__device__ __forceinline__ void merge_lanes(float& m, float& s, int& idx, bool with_idx) {
+  auto swap = [](unsigned v) {
+    if constexpr (OFF == 16) return __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    else return __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  };
+  const auto pm = swap(__float_as_uint(m));
+  const auto ps = swap(__float_as_uint(s));
+  float ma = __uint_as_float(pm[0]), sa = __uint_as_float(ps[0]);
+  int ia = idx, ib = idx;
+  if (with_idx) {
+    const auto pi = swap((unsigned)idx);
+    ia = (int)pi[0];
+    ib = (int)pi[1];
+  }
+  merge_sym(ma, sa, ia, __uint_as_float(pm[1]), __uint_as_float(ps[1]), ib, with_idx);
+  m = ma;
+  s = sa;
+  idx = ia;
+}
+
 // Packed upper-triangle index -> (d, e) for the full covariance (DP = 16).
 struct SymTable {
   unsigned char d[136], e[136];
@@ -71,6 +128,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr int NCH = kBN * CPR;                         // chunks per row block
   constexpr int PF = (NCH + 511) / 512;                  // prefetched chunks per thread at 512 threads
   constexpr bool PSI_LDS = BF && MODE == MODE_STATS;     // materialised ψᵀ (bf16 spherical)
+  constexpr bool PIPE = COV != FULL;                     // block i+1's E-GEMM overlaps block i's epilogue
+  constexpr int PD = PIPE ? 2 : 1;                       // loader runs PD blocks ahead
+  constexpr int NB = PD + 1;                             // staged-row buffers
   constexpr int XS = DP + (BF ? 8 : 4);                  // staged-row stride, elements
   constexpr int PS = EP + 4;                             // φ row stride (full)
   constexpr int QS = kBN + 8;                            // ψᵀ row stride, bf16 elements
@@ -78,11 +138,11 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   using WF = typename std::conditional<BF, bf16x8, f32x4>::type;
   static_assert(NCH % 64 == 0, "row block must split into whole waves of chunks");
 
-  __shared__ __align__(16) XT xs[COV == FULL ? 8 : 2 * kBN * XS];
-  __shared__ __align__(16) float phi[COV == FULL ? 2 * kBN * PS : 4];
+  __shared__ __align__(16) XT xs[COV == FULL ? 8 : NB * kBN * XS];
+  __shared__ __align__(16) float phi[COV == FULL ? NB * kBN * PS : 4];
   __shared__ __align__(16) FT psiT[PSI_LDS ? 2 * JP * QS : 8];
-  __shared__ float rowq_s[2 * kBN];
-  __shared__ float lse_s[2 * kBN];
+  __shared__ float rowq_s[NB * kBN];
+  __shared__ float lse_s[NB * kBN];
   __shared__ float red_m[LSE ? 2 * 8 * kBN : 1];
   __shared__ float red_s[LSE ? 2 * 8 * kBN : 1];
   __shared__ int red_i[WANT_IDX ? 2 * 8 * kBN : 1];
@@ -132,20 +192,28 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       }
     }
   }
-  // (A_k, a_k, C_k): l2 = A_k*S + fma(a_k, rowq_n, C_k); invalid components get C = -inf.
-  const float4 kInvalid = make_float4(0.f, 0.f, -INFINITY, 0.f);
-  float4 cS[CT];           // data-row orientation: component kbase + 16ct + li
-  float4 cL[CT][4];        // component-row orientation: kbase + 16ct + 4g + v
+  // Per-component (c, C): l2 = c*(rowq - 2S) + C (spherical, tied) or c*S + C (diag, full);
+  // components past K get C = -inf.
+  constexpr bool ROWQ = (COV == SPH || COV == TIED);
+  const float2 kInvalid = make_float2(0.f, -INFINITY);
+  float2 cS[CT];           // data-row orientation: component kbase + 16ct + li
+  float2 cL[CT][4];        // component-row orientation: kbase + 16ct + 4g + v
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int k1 = kbase + 16 * ct + li;
-    cS[ct] = (k1 < K) ? a.cconst[(size_t)b * K + k1] : kInvalid;
+    if (k1 < K) { const float4 c = a.cconst[(size_t)b * K + k1]; cS[ct] = make_float2(c.x, c.y); }
+    else cS[ct] = kInvalid;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int k2 = kbase + 16 * ct + 4 * g + v;
-      cL[ct][v] = (k2 < K) ? a.cconst[(size_t)b * K + k2] : kInvalid;
+      if (k2 < K) { const float4 c = a.cconst[(size_t)b * K + k2]; cL[ct][v] = make_float2(c.x, c.y); }
+      else cL[ct][v] = kInvalid;
     }
   }
+  auto logit = [&](float2 c, float S, float rq) -> float {
+    if constexpr (ROWQ) return fmaf(c.x, fmaf(-2.f, S, rq), c.y);
+    else return fmaf(c.x, S, c.y);
+  };
 
   f32x4 acc[MODE == MODE_STATS ? CT : 1][MODE == MODE_STATS ? JT : 1];
   if constexpr (MODE == MODE_STATS) {
@@ -163,7 +231,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     }
   }
   if constexpr (COV == FULL) {
-    for (int i = tid; i < 2 * kBN * (EP - S - DP); i += nthr) {
+    for (int i = tid; i < NB * kBN * (EP - S - DP); i += nthr) {
       const int row = i / (EP - S - DP), c = i % (EP - S - DP);
       phi[row * PS + S + DP + c] = 0.f;
     }
@@ -205,25 +273,12 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       if constexpr (COV != FULL) {
         *reinterpret_cast<uint4*>(&xs[buf * kBN * XS + r * XS + cc]) = raw;
       }
-      if constexpr (PSI_LDS) {
-        FT* pt = psiT + buf * JP * QS;
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) pt[(cc + j) * QS + r] = t.e[j];
-      }
       if constexpr (COV == SPH) {
         float q = 0.f;
 #pragma unroll
         for (int j = 0; j < VEC; ++j) q = fmaf(v[j], v[j], q);
-#pragma unroll
-        for (int off = 1; off < CPR; off *= 2) q += __shfl_xor(q, off);
-        if (cc == 0) {
-          rowq_s[buf * kBN + r] = q;
-          if constexpr (PSI_LDS) {
-            const __bf16 hi = (__bf16)q;
-            psiT[buf * JP * QS + (DP + 1) * QS + r] = hi;
-            psiT[buf * JP * QS + (DP + 2) * QS + r] = (__bf16)(q - (float)hi);
-          }
-        }
+        q = group_sum<CPR>(q);
+        if (cc == 0) rowq_s[buf * kBN + r] = q;
       } else if constexpr (COV == TIED) {
         if (cc == 0) rowq_s[buf * kBN + r] = (n < rend) ? a.rowq[(size_t)b * N + n] : 0.f;
       } else {
@@ -249,6 +304,29 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       }
       if constexpr (!LSE) {
         if (cc == 0) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
+      }
+    }
+  };
+
+  // Transposed M-step operand ψᵀ (bf16) from staged rows: each thread reads 8
+  // rows of one column (consecutive lanes -> consecutive columns, no bank
+  // conflicts) and writes one 16-byte chunk of a ψᵀ row.
+  auto build_psi = [&](int bx, int pb) {
+    if constexpr (PSI_LDS) {
+      const XT* xr = xs + bx * kBN * XS;
+      FT* pt = psiT + pb * JP * QS;
+      for (int t = tid; t < DP * (kBN / 8); t += nthr) {
+        const int j = t % DP, q = t / DP;
+        bf16x8 v;
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) v[s8] = xr[(8 * q + s8) * XS + j];
+        *reinterpret_cast<bf16x8*>(&pt[j * QS + 8 * q]) = v;
+      }
+      if (tid < kBN) {
+        const float q = rowq_s[bx * kBN + tid];
+        const __bf16 hi = (__bf16)q;
+        pt[(DP + 1) * QS + tid] = hi;
+        pt[(DP + 2) * QS + tid] = (__bf16)(q - (float)hi);
       }
     }
   };
@@ -294,7 +372,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       int idx = WANT_IDX ? red_i[base + tid] : 0;
       for (int w = 1; w < nw; ++w) {
         const int o = base + w * kBN + tid;
-        lse_merge(m, s, idx, red_m[o], red_s[o], WANT_IDX ? red_i[o] : 0);
+        merge_sym(m, s, idx, red_m[o], red_s[o], WANT_IDX ? red_i[o] : 0, WANT_IDX);
       }
       if (n < rend) {
         const size_t o = ((size_t)ktile * a.B + b) * N + n;
@@ -304,52 +382,69 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     }
   };
 
-  auto compute = [&](int buf, int64_t n0) {
-    if constexpr (LSE) {
-      // ---- E-GEMM, component-row orientation: T[ct][nt] = W(16 comps) · φᵀ(16 rows) ----
-      f32x4 T[CT][2];
+  // E-GEMM of one staged block.  LSE modes: component-row orientation,
+  // T[ct][nt] = W(16 comps) · φᵀ(16 rows).  Otherwise data-row orientation,
+  // T[ct][rt] = φ(16 rows) · Wᵀ(16 comps); for bf16 tile rt's A-row i is data row
+  // 8(i/4) + 4rt + i%4, so C-row 4g+v of tile rt is data row 8g + 4rt + v.
+  struct Acc { f32x4 t[CT][2]; };
+  auto egemm = [&](int bx) -> Acc {
+    Acc A;
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) { T[ct][0] = f32x4{0.f, 0.f, 0.f, 0.f}; T[ct][1] = T[ct][0]; }
+    for (int ct = 0; ct < CT; ++ct) { A.t[ct][0] = f32x4{0.f, 0.f, 0.f, 0.f}; A.t[ct][1] = A.t[ct][0]; }
 #pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) {
-        if constexpr (BF) {
-          bf16x8 bx[2];
+    for (int ec = 0; ec < ECH; ++ec) {
+      if constexpr (BF) {
+        bf16x8 xv[2];
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt)
-            bx[nt] = ld16<bf16x8>(&xs[buf * kBN * XS + (16 * nt + li) * XS + 32 * ec + 8 * g]);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-              T[ct][nt] = mfma_bf16(whi[ct][ec], bx[nt], T[ct][nt]);
-              T[ct][nt] = mfma_bf16(wlo[ct][ec], bx[nt], T[ct][nt]);
-            }
-        } else {
-          f32x4 b4[2];
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) b4[nt] = phi4(buf, 16 * nt + li, 16 * ec + 4 * g);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-              for (int t = 0; t < 4; ++t) T[ct][nt] = mfma_f32(whi[ct][ec][t], b4[nt][t], T[ct][nt]);
+        for (int h = 0; h < 2; ++h) {
+          const int row = LSE ? 16 * h + li : 8 * (li / 4) + 4 * h + (li % 4);
+          xv[h] = ld16<bf16x8>(&xs[bx * kBN * XS + row * XS + 32 * ec + 8 * g]);
         }
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            if constexpr (LSE) {
+              A.t[ct][h] = mfma_bf16(whi[ct][ec], xv[h], A.t[ct][h]);
+              A.t[ct][h] = mfma_bf16(wlo[ct][ec], xv[h], A.t[ct][h]);
+            } else {
+              A.t[ct][h] = mfma_bf16(xv[h], whi[ct][ec], A.t[ct][h]);
+              A.t[ct][h] = mfma_bf16(xv[h], wlo[ct][ec], A.t[ct][h]);
+            }
+          }
+      } else {
+        f32x4 xv[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) xv[h] = phi4(bx, 16 * h + li, 16 * ec + 4 * g);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              if constexpr (LSE) A.t[ct][h] = mfma_f32(whi[ct][ec][t], xv[h][t], A.t[ct][h]);
+              else A.t[ct][h] = mfma_f32(xv[h][t], whi[ct][ec][t], A.t[ct][h]);
+            }
       }
-      // ---- per data row: max (argmax) and scaled sum over this wave's components ----
+    }
+    return A;
+  };
+
+  auto epilogue = [&](const Acc& A, int bx, int pb, int64_t n0) {
+    if constexpr (LSE) {
+      // Per data row: max (argmax) and scaled sum over this wave's components.
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const int r = 16 * nt + li;
-        const float rq = rowq_s[buf * kBN + r];
+        const float rq = rowq_s[bx * kBN + r];
         float l2v[CT][4];
-        float m = -INFINITY;
+        float m = kLogFloor;
         int idx = 0x7fffffff;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const float4 c = cL[ct][v];
-            const float l2 = fmaf(c.x, T[ct][nt][v], fmaf(c.y, rq, c.z));
+            const float l2 = logit(cL[ct][v], A.t[ct][nt][v], rq);
             l2v[ct][v] = l2;
             if constexpr (WANT_IDX) {
               if (l2 > m) { m = l2; idx = kbase + 16 * ct + 4 * g + v; }
@@ -358,73 +453,32 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
             }
           }
         float s = 0.f;
-        if (m != -INFINITY) {
 #pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
+        for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) s += fast_exp2(l2v[ct][v] - m);
-        }
-#pragma unroll
-        for (int off = 16; off <= 32; off *= 2) {
-          const float m2 = __shfl_xor(m, off);
-          const float s2 = __shfl_xor(s, off);
-          const int i2 = WANT_IDX ? __shfl_xor(idx, off) : 0;
-          lse_merge(m, s, idx, m2, s2, i2);
-        }
+          for (int v = 0; v < 4; ++v) s += fast_exp2(l2v[ct][v] - m);
+        merge_lanes<16>(m, s, idx, WANT_IDX);
+        merge_lanes<32>(m, s, idx, WANT_IDX);
         if (g == 0) {
-          const int o = buf * 8 * kBN + wave * kBN + r;
+          const int o = pb * 8 * kBN + wave * kBN + r;
           red_m[o] = m;
           red_s[o] = s;
           if constexpr (WANT_IDX) red_i[o] = idx;
         }
       }
     } else {
-      // ---- E-GEMM, data-row orientation: S[rt][ct] = φ(16 rows) · Wᵀ(16 comps) ----
-      f32x4 Sv[2][CT];
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) { Sv[0][ct] = f32x4{0.f, 0.f, 0.f, 0.f}; Sv[1][ct] = Sv[0][ct]; }
-#pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) {
-        if constexpr (BF) {
-          // Row permutation: tile rt, A-row i -> data row 8(i/4) + 4rt + i%4, so that
-          // C-row 4g+v of tile rt is data row 8g + 4rt + v (8 consecutive rows per lane group).
-          bf16x8 ax[2];
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt)
-            ax[rt] = ld16<bf16x8>(&xs[buf * kBN * XS + (8 * (li / 4) + 4 * rt + (li % 4)) * XS + 32 * ec + 8 * g]);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-              Sv[rt][ct] = mfma_bf16(ax[rt], whi[ct][ec], Sv[rt][ct]);
-              Sv[rt][ct] = mfma_bf16(ax[rt], wlo[ct][ec], Sv[rt][ct]);
-            }
-        } else {
-          f32x4 a4[2];
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt) a4[rt] = phi4(buf, 16 * rt + li, 16 * ec + 4 * g);
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-              for (int t = 0; t < 4; ++t) Sv[rt][ct] = mfma_f32(a4[rt][t], whi[ct][ec][t], Sv[rt][ct]);
-        }
-      }
       // Responsibilities for every component tile of this wave.
       float rr[CT][2][4];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const float4 c = cS[ct];
+      for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int r = BF ? 8 * g + 4 * rt + v : 16 * rt + 4 * g + v;
-            const float l2 = fmaf(c.x, Sv[rt][ct][v], fmaf(c.y, rowq_s[buf * kBN + r], c.z));
-            rr[ct][rt][v] = fast_exp2(l2 - lse_s[buf * kBN + r]);
+            const float l2 = logit(cS[ct], A.t[ct][rt][v], rowq_s[bx * kBN + r]);
+            rr[ct][rt][v] = fast_exp2(l2 - lse_s[bx * kBN + r]);
           }
-      }
       if constexpr (MODE == MODE_STATS) {
         // M-GEMM: each ψ fragment is loaded once and used by every component tile.
         if constexpr (BF) {
@@ -437,7 +491,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               for (int v = 0; v < 4; ++v) ar[ct][4 * rt + v] = (__bf16)rr[ct][rt][v];
 #pragma unroll
           for (int jt = 0; jt < JT; ++jt) {
-            const bf16x8 bqv = ld16<bf16x8>(&psiT[buf * JP * QS + (16 * jt + li) * QS + 8 * g]);
+            const bf16x8 bqv = ld16<bf16x8>(&psiT[pb * JP * QS + (16 * jt + li) * QS + 8 * g]);
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) acc[ct][jt] = mfma_bf16(ar[ct], bqv, acc[ct][jt]);
           }
@@ -448,7 +502,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
             for (int rt = 0; rt < 2; ++rt) {
               float bq[4];
 #pragma unroll
-              for (int v = 0; v < 4; ++v) bq[v] = psi1(buf, 16 * rt + 4 * g + v, 16 * jt + li);
+              for (int v = 0; v < 4; ++v) bq[v] = psi1(bx, 16 * rt + 4 * g + v, 16 * jt + li);
 #pragma unroll
               for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -474,24 +528,45 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     }
   };
 
-  // ---- main loop: one barrier per block ----
+  // ---- main loop: one barrier per block; the loader runs PD blocks ahead ----
   const int64_t nblk = (rend > rbeg) ? (rend - rbeg + kBN - 1) / kBN : 0;
-  __syncthreads();  // constant feature rows are in place before the first stash overwrites any
-  if (nblk > 0) {
-    fetch(rbeg);
-    stash(0, rbeg);
+  __syncthreads();  // constant feature rows are in place before any stash or build
+  for (int p = 0; p < PD; ++p) {
+    if (p < nblk) {
+      fetch(rbeg + p * kBN);
+      stash(p, rbeg + p * kBN);
+    }
   }
   __syncthreads();
+  if constexpr (PSI_LDS) {
+    if (nblk > 0) build_psi(0, 0);
+    __syncthreads();
+  }
+  Acc cur;
+  if constexpr (PIPE) {
+    if (nblk > 0) cur = egemm(0);
+  }
   for (int64_t ib = 0; ib < nblk; ++ib) {
-    const int buf = (int)(ib & 1);
+    const int bx = (int)(ib % NB), pb = (int)(ib & 1);
     const int64_t n0 = rbeg + ib * kBN;
-    const bool more = ib + 1 < nblk;
-    if (more) fetch(n0 + kBN);
+    const bool ahead = ib + PD < nblk;
+    if (ahead) fetch(n0 + PD * kBN);
     if constexpr (LSE) {
-      if (ib > 0) combine_out(buf ^ 1, n0 - kBN);
+      if (ib > 0) combine_out(pb ^ 1, n0 - kBN);
     }
-    compute(buf, n0);
-    if (more) stash(buf ^ 1, n0 + kBN);
+    if constexpr (PIPE) {
+      // Block ib+1 was staged an iteration ago: its MFMAs run under this block's epilogue.
+      Acc nxt;
+      if (ib + 1 < nblk) nxt = egemm((int)((ib + 1) % NB));
+      epilogue(cur, bx, pb, n0);
+      cur = nxt;
+    } else {
+      epilogue(egemm(bx), bx, pb, n0);
+    }
+    if constexpr (PSI_LDS) {
+      if (ib + 1 < nblk) build_psi((int)((ib + 1) % NB), pb ^ 1);
+    }
+    if (ahead) stash((int)((ib + PD) % NB), n0 + PD * kBN);
     __syncthreads();
   }
   if constexpr (LSE) {

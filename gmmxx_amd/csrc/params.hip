@@ -133,10 +133,9 @@ __global__ void prep_kernel(PrepArgs a) {
     ca = -0.5f * kLog2e;
     cb = (lw - 0.5f * (log2pi_d + a.logdet[bk])) * kLog2e;
   }
-  // l2 = ca * (sc * S + rowq + colq) + cb, folded to A*S + fma(a, rowq, C) for the tile kernel
-  // (sc = -2 where S is the cross term x·μ / x·Pμ, 1 where W already carries it).
-  const float sc = (a.cov == SPH || a.cov == TIED) ? -2.f : 1.f;
-  a.cconst[bk] = make_float4(sc * ca, ca, fmaf(ca, colq, cb), 0.f);
+  // l2 = ca * (rowq - 2S + colq) + cb (spherical, tied: S is the cross term x·μ / x·Pμ) or
+  // ca * (S + colq) + cb (diag, full: W already carries the -2), stored as (ca, ca*colq + cb).
+  a.cconst[bk] = make_float4(ca, fmaf(ca, colq, cb), 0.f, 0.f);
 }
 
 // ---------------------------------------------------------------------------
