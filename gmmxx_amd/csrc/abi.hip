@@ -75,7 +75,9 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.JP = round_up(J, 16);
   q.nk_col = (q.cov == SPH) ? q.DP : (q.cov == DIAG ? 2 * q.DP : (q.cov == TIED ? q.DP : q.DP + S));
   q.CW = tile_cw(q.cov, q.DP, q.bf);
-  q.nw = std::min(8, (q.K + q.CW - 1) / q.CW);
+  // Waves per workgroup: a power of two (the cross-wave combine reduces lane groups).
+  const int need = (q.K + q.CW - 1) / q.CW;
+  q.nw = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
   q.ktiles = (q.K + q.nw * q.CW - 1) / (q.nw * q.CW);
   const int64_t row_blocks = (q.N + kBN - 1) / kBN;
   int64_t slices = std::max<int64_t>(1, (kTargetBlocks + (int64_t)q.ktiles * q.B - 1) / ((int64_t)q.ktiles * q.B));

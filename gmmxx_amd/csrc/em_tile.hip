@@ -71,36 +71,35 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// Symmetric merge of two (max, scaled sum, argmax) partials; both partners of
-// a lane swap compute bit-identical results.
-__device__ __forceinline__ void merge_sym(float& m, float& s, int& idx, float m2, float s2, int i2, bool with_idx) {
-  const float M = fmaxf(m, m2);
-  const float e1 = s * fast_exp2(m - M), e2 = s2 * fast_exp2(m2 - M);
-  if (with_idx) idx = (m2 > m || (m2 == m && i2 < idx)) ? i2 : idx;
-  m = M;
-  s = e1 + e2;
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (G >= 2) v = fmaxf(v, dpp<0xB1>(v));
+  if constexpr (G >= 4) v = fmaxf(v, dpp<0x4E>(v));
+  if constexpr (G >= 8) v = fmaxf(v, dpp<0x141>(v));
+  return v;
+}
+template <int G>
+__device__ __forceinline__ int group_min_i(int v) {
+  auto d = [](int x, auto ctrl) { return __builtin_amdgcn_update_dpp(0, x, decltype(ctrl)::value, 0xF, 0xF, false); };
+  if constexpr (G >= 2) v = min(v, d(v, std::integral_constant<int, 0xB1>{}));
+  if constexpr (G >= 4) v = min(v, d(v, std::integral_constant<int, 0x4E>{}));
+  if constexpr (G >= 8) v = min(v, d(v, std::integral_constant<int, 0x141>{}));
+  return v;
 }
 
-// Merge with the partner lane l ^ 16 (OFF = 16) or l ^ 32 (OFF = 32), no LDS.
+// Value combined with its partner lane l ^ 16 (OFF = 16) or l ^ 32 (OFF = 32) by OP, no LDS.
+template <int OFF, bool MAX>
+__device__ __forceinline__ float lanes_op(float v) {
+  const auto t = (OFF == 16) ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float a = __uint_as_float(t[0]), b = __uint_as_float(t[1]);
+  return MAX ? fmaxf(a, b) : a + b;
+}
 template <int OFF>
-__device__ __forceinline__ void merge_lanes(float& m, float& s, int& idx, bool with_idx) {
-  auto swap = [](unsigned v) {
-    if constexpr (OFF == 16) return __builtin_amdgcn_permlane16_swap(v, v, false, false);
-    else return __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  };
-  const auto pm = swap(__float_as_uint(m));
-  const auto ps = swap(__float_as_uint(s));
-  float ma = __uint_as_float(pm[0]), sa = __uint_as_float(ps[0]);
-  int ia = idx, ib = idx;
-  if (with_idx) {
-    const auto pi = swap((unsigned)idx);
-    ia = (int)pi[0];
-    ib = (int)pi[1];
-  }
-  merge_sym(ma, sa, ia, __uint_as_float(pm[1]), __uint_as_float(ps[1]), ib, with_idx);
-  m = ma;
-  s = sa;
-  idx = ia;
+__device__ __forceinline__ int lanes_min_i(int v) {
+  const auto t = (OFF == 16) ? __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false)
+                             : __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return min((int)t[0], (int)t[1]);
 }
 
 // Packed upper-triangle index -> (d, e) for the full covariance (DP = 16).
@@ -128,7 +127,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr int NCH = kBN * CPR;                         // chunks per row block
   constexpr int PF = (NCH + 511) / 512;                  // prefetched chunks per thread at 512 threads
   constexpr bool PSI_LDS = BF && MODE == MODE_STATS;     // materialised ψᵀ (bf16 spherical)
-  constexpr bool PIPE = COV != FULL;                     // block i+1's E-GEMM overlaps block i's epilogue
+  // Block i+1's E-GEMM overlaps block i's epilogue (off where it would not fit
+  // the LDS budget (full) or the register file (diag at D = 128)).
+  constexpr bool PIPE = COV != FULL && !(COV == DIAG && DP >= 128);
   constexpr int PD = PIPE ? 2 : 1;                       // loader runs PD blocks ahead
   constexpr int NB = PD + 1;                             // staged-row buffers
   constexpr int XS = DP + (BF ? 8 : 4);                  // staged-row stride, elements
@@ -143,9 +144,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   __shared__ __align__(16) FT psiT[PSI_LDS ? 2 * JP * QS : 8];
   __shared__ float rowq_s[NB * kBN];
   __shared__ float lse_s[NB * kBN];
-  __shared__ float red_m[LSE ? 2 * 8 * kBN : 1];
-  __shared__ float red_s[LSE ? 2 * 8 * kBN : 1];
-  __shared__ int red_i[WANT_IDX ? 2 * 8 * kBN : 1];
+  __shared__ float red_m[LSE ? 2 * kBN * 8 : 1];   // [parity][row][wave]
+  __shared__ float red_s[LSE ? 2 * kBN * 8 : 1];
+  __shared__ int red_i[WANT_IDX ? 2 * kBN * 8 : 1];
 
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
@@ -363,21 +364,35 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     }
   };
 
-  // Cross-wave merge of one block's per-row partials, written to global memory.
-  auto combine_out = [&](int buf, int64_t n0) {
-    if (tid < kBN) {
-      const int64_t n = n0 + tid;
-      const int base = buf * 8 * kBN;
-      float m = red_m[base + tid], s = red_s[base + tid];
-      int idx = WANT_IDX ? red_i[base + tid] : 0;
-      for (int w = 1; w < nw; ++w) {
-        const int o = base + w * kBN + tid;
-        merge_sym(m, s, idx, red_m[o], red_s[o], WANT_IDX ? red_i[o] : 0, WANT_IDX);
+  // Cross-wave merge of one block's per-row partials, written to global memory:
+  // lane (row, wave) of the first 32*nw threads holds one partial; the nw
+  // partials of a row sit in consecutive lanes and are reduced with DPP.
+  auto combine_out = [&](int pb, int64_t n0) {
+    if (tid < kBN * nw) {
+      const int r = tid / nw, w = tid % nw;
+      const int o = (pb * kBN + r) * 8 + w;
+      const float mw = red_m[o], sw = red_s[o];
+      float M;
+      switch (nw) {
+        case 1: M = mw; break;
+        case 2: M = group_max<2>(mw); break;
+        case 4: M = group_max<4>(mw); break;
+        default: M = group_max<8>(mw); break;
       }
-      if (n < rend) {
-        const size_t o = ((size_t)ktile * a.B + b) * N + n;
-        reinterpret_cast<float2*>(a.part_ms)[o] = make_float2(m, s);
-        if constexpr (WANT_IDX) a.part_idx[o] = idx;
+      float t = sw * fast_exp2(mw - M);
+      int idx = 0;
+      if constexpr (WANT_IDX) idx = (mw == M) ? red_i[o] : 0x7fffffff;
+      switch (nw) {
+        case 1: break;
+        case 2: t = group_sum<2>(t); if (WANT_IDX) idx = group_min_i<2>(idx); break;
+        case 4: t = group_sum<4>(t); if (WANT_IDX) idx = group_min_i<4>(idx); break;
+        default: t = group_sum<8>(t); if (WANT_IDX) idx = group_min_i<8>(idx); break;
+      }
+      const int64_t n = n0 + r;
+      if (w == 0 && n < rend) {
+        const size_t og = ((size_t)ktile * a.B + b) * N + n;
+        reinterpret_cast<float2*>(a.part_ms)[og] = make_float2(M, t);
+        if constexpr (WANT_IDX) a.part_idx[og] = idx;
       }
     }
   };
@@ -432,7 +447,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
 
   auto epilogue = [&](const Acc& A, int bx, int pb, int64_t n0) {
     if constexpr (LSE) {
-      // Per data row: max (argmax) and scaled sum over this wave's components.
+      // Per data row: wave max (and first argmax) by max-only lane swaps, then one
+      // exp per element against that max and a plain sum -- no rescaling.
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const int r = 16 * nt + li;
@@ -452,19 +468,23 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               m = fmaxf(m, l2);
             }
           }
+        const float lm = m;
+        m = lanes_op<32, true>(lanes_op<16, true>(m));
+        if constexpr (WANT_IDX) {
+          idx = (lm == m) ? idx : 0x7fffffff;
+          idx = lanes_min_i<32>(lanes_min_i<16>(idx));
+        }
         float s = 0.f;
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
           for (int v = 0; v < 4; ++v) s += fast_exp2(l2v[ct][v] - m);
-        merge_lanes<16>(m, s, idx, WANT_IDX);
-        merge_lanes<32>(m, s, idx, WANT_IDX);
-        if (g == 0) {
-          const int o = pb * 8 * kBN + wave * kBN + r;
-          red_m[o] = m;
-          red_s[o] = s;
-          if constexpr (WANT_IDX) red_i[o] = idx;
-        }
+        s = lanes_op<32, false>(lanes_op<16, false>(s));
+        // Every lane of the row group holds the same values; all write (no branch).
+        const int o = (pb * kBN + r) * 8 + wave;
+        red_m[o] = m;
+        red_s[o] = s;
+        if constexpr (WANT_IDX) red_i[o] = idx;
       }
     } else {
       // Responsibilities for every component tile of this wave.
@@ -556,8 +576,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     }
     if constexpr (PIPE) {
       // Block ib+1 was staged an iteration ago: its MFMAs run under this block's epilogue.
-      Acc nxt;
-      if (ib + 1 < nblk) nxt = egemm((int)((ib + 1) % NB));
+      // Unconditional (the last iteration reads a stale, in-bounds buffer and
+      // discards the result) so the MFMAs share a basic block with the epilogue.
+      const Acc nxt = egemm((int)((ib + 1) % NB));
       epilogue(cur, bx, pb, n0);
       cur = nxt;
     } else {
