@@ -128,10 +128,14 @@ def _stream(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def last_error() -> str:
+    """The calling thread's last error message from the library."""
+    return load_library().gmmxx_hip_last_error().decode(errors="replace")
+
+
 def _check(rc: int, what: str) -> None:
     if rc != 0:
-        msg = _lib.gmmxx_hip_last_error().decode(errors="replace")
-        raise HipRuntimeError(f"{what} failed (status {rc}): {msg}")
+        raise HipRuntimeError(f"{what} failed (status {rc}): {last_error()}")
 
 
 def problem(covariance_type: str, x_dtype: torch.dtype, B: int, N: int, D: int, K: int) -> _Problem:

@@ -1,0 +1,448 @@
+"""``GMMXX`` estimator with the HIP/gfx950 engine behind it.
+
+The public surface is the reference's ``gmmxx.interface.GMMXX``
+(gmmxx/interface.py:128-2558): the same constructor arguments and sklearn
+aliases, ``fit`` / ``train`` / ``fit_predict`` / ``predict`` /
+``predict_proba`` / ``score_samples`` / ``score`` / ``bic`` / ``aic``,
+``get_params`` / ``set_params`` and the fitted attributes (``means_``,
+``weights_``, ``covariances_``, ``labels_``, ``lower_bound_``,
+``lower_bound_history_``, ``n_iter_``, ``last_backend_used_`` ...).  The
+``backend=`` kwarg gains ``"hip"``; ``"auto"`` resolves to it.  Every compute
+call goes to ``libgmmxx_hip.so``; there is no CPU or PyTorch fallback (see
+``gmmxx_amd._dispatch``).
+
+Input handling follows the reference: ``(N, D)`` or ``(B, N, D)`` floating
+point tensors, fitted attributes squeezed when the input was unbatched
+(:322-325, :401-424), half-precision inputs computed in fp32 unless ``dtype=``
+says otherwise (:426-433).  bf16 spherical input stays bf16 in HBM: the engine
+multiplies the exact bf16 values with fp32 accumulation, which is the fp32
+algorithm on the same values.
+"""
+
+from __future__ import annotations
+
+import contextlib
+import math
+import warnings
+from typing import Any, Optional
+
+import torch
+
+from . import _dispatch, _hip, em
+
+_VALID_COVARIANCE_TYPES = {"spherical", "diag", "tied", "full"}
+_COVARIANCE_ALIASES = {"diagonal": "diag"}
+_SKLEARN_PARAM_ALIASES = {"n_components": "k", "max_iter": "niter", "random_state": "seed", "n_features": "d"}
+_PARAM_NAMES = (
+    "d", "n_components", "max_iter", "tol", "random_state", "chunk_size_data", "chunk_size_centroids",
+    "chunk_size_data_cpu", "verbose", "dtype", "device", "init_params", "reg_covar", "init_kmeans_iters",
+    "init_kmeans_tol", "covariance_type", "matmul_precision", "compute_labels_on_fit", "approx_top_k", "backend",
+)
+
+
+def _normalize_covariance_type(covariance_type: str) -> str:
+    covariance_type = _COVARIANCE_ALIASES.get(covariance_type, covariance_type)
+    if covariance_type not in _VALID_COVARIANCE_TYPES:
+        raise ValueError("covariance_type must be 'spherical', 'diag', 'diagonal', 'tied', or 'full'")
+    return covariance_type
+
+
+def _optional_positive_int(value: Optional[int], name: str) -> Optional[int]:
+    if value is None:
+        return None
+    value = int(value)
+    if value <= 0:
+        raise ValueError(f"{name} must be positive")
+    return value
+
+
+def _positive_int(value: int, name: str) -> int:
+    value = int(value)
+    if value <= 0:
+        raise ValueError(f"{name} must be positive")
+    return value
+
+
+def _resolve_alias(primary, alias, *, primary_name: str, alias_name: str):
+    if primary is not None and alias is not None and int(primary) != int(alias):
+        raise ValueError(f"Received conflicting {primary_name}={primary} and {alias_name}={alias}")
+    return primary if primary is not None else alias
+
+
+def _check_backend(backend: str) -> None:
+    if backend not in _dispatch.VALID_BACKENDS:
+        raise ValueError(f"backend must be one of {sorted(_dispatch.VALID_BACKENDS)}, got {backend!r}")
+
+
+class GMMXX:
+    """Gaussian mixture model fitted by soft EM on MI355X (gfx950).
+
+    ``covariance_type`` is ``spherical``, ``diag``/``diagonal``, ``tied`` or
+    ``full``.  Supported shapes: D <= 128 (spherical, diag), D <= 64 (tied),
+    D <= 16 (full); any N, K <= 65536, B <= 65535.  bf16 input is kept in bf16
+    for spherical.  ``approx_top_k`` (the reference's opt-in approximate EM)
+    is not provided and raises.
+    """
+
+    def __init__(
+        self,
+        d: Optional[int] = None,
+        k: Optional[int] = None,
+        niter: Optional[int] = None,
+        tol: float = 1e-4,
+        use_triton: Optional[bool] = None,
+        seed: Optional[int] = None,
+        chunk_size_data: int = 32768,
+        chunk_size_centroids: int = 1024,
+        chunk_size_data_cpu: int = 1048576,
+        verbose: bool = False,
+        dtype: Optional[torch.dtype] = None,
+        device: Optional[torch.device] = None,
+        init_params: str = "kmeans",
+        reg_covar: float = 1e-6,
+        init_kmeans_iters: int = 10,
+        init_kmeans_tol: float = 1e-4,
+        covariance_type: str = "spherical",
+        matmul_precision: Optional[str] = None,
+        compute_labels_on_fit: bool = True,
+        approx_top_k: Optional[int] = None,
+        n_components: Optional[int] = None,
+        max_iter: Optional[int] = None,
+        random_state: Optional[int] = None,
+        n_features: Optional[int] = None,
+        backend: str = "auto",
+    ):
+        d = _resolve_alias(d, n_features, primary_name="d", alias_name="n_features")
+        k = _resolve_alias(k, n_components, primary_name="k", alias_name="n_components")
+        niter = _resolve_alias(niter, max_iter, primary_name="niter", alias_name="max_iter")
+        seed = _resolve_alias(seed, random_state, primary_name="seed", alias_name="random_state")
+        _check_backend(backend)
+        if use_triton is not None:
+            # Deprecated knob of the reference (gmmxx/interface.py:180-199); it
+            # selects nothing here since the only engine is HIP.
+            if backend != "auto":
+                raise ValueError("Cannot pass both backend= and use_triton= to GMMXX. "
+                                 "Drop use_triton; backend= is the canonical kwarg.")
+            warnings.warn("use_triton is deprecated and has no effect with gmmxx_amd; use backend='hip'",
+                          DeprecationWarning, stacklevel=2)
+        self._legacy_no_triton = use_triton is False
+        self.backend = backend
+        if k is None:
+            raise ValueError("k or n_components is required")
+        self.d = _optional_positive_int(d, "d")
+        self.k = _positive_int(k, "k")
+        self.niter = _positive_int(100 if niter is None else niter, "niter")
+        self.tol = float(tol)
+        if self.tol < 0.0:
+            raise ValueError("tol must be non-negative")
+        self.seed = int(0 if seed is None else seed)
+        self.chunk_size_data = _positive_int(chunk_size_data, "chunk_size_data")
+        self.chunk_size_centroids = _positive_int(chunk_size_centroids, "chunk_size_centroids")
+        self.chunk_size_data_cpu = _positive_int(chunk_size_data_cpu, "chunk_size_data_cpu")
+        self.verbose = bool(verbose)
+        self.dtype = dtype
+        self.init_params = init_params
+        self.reg_covar = float(reg_covar)
+        if self.reg_covar < 0.0:
+            raise ValueError("reg_covar must be non-negative")
+        self.init_kmeans_iters = _positive_int(init_kmeans_iters, "init_kmeans_iters")
+        self.init_kmeans_tol = float(init_kmeans_tol)
+        if self.init_kmeans_tol < 0.0:
+            raise ValueError("init_kmeans_tol must be non-negative")
+        self.covariance_type = _normalize_covariance_type(covariance_type)
+        if matmul_precision is not None and matmul_precision not in {"highest", "high", "medium"}:
+            raise ValueError("matmul_precision must be None, 'highest', 'high', or 'medium'")
+        self.matmul_precision = matmul_precision
+        self.compute_labels_on_fit = bool(compute_labels_on_fit)
+        self.approx_top_k = _optional_positive_int(approx_top_k, "approx_top_k")
+        self._raw_device = device
+        self.device = torch.device(device) if device is not None else torch.device(
+            "cuda:0" if torch.cuda.is_available() else "cpu")
+        self._reset_fit_state()
+
+    # -- state --------------------------------------------------------------
+
+    @property
+    def use_triton(self) -> bool:
+        """Always False: no Triton path exists in this package."""
+        return False
+
+    def _reset_fit_state(self) -> None:
+        self.means_b = self.variances_b = self.covariances_b = self.weights_b = None
+        self.cluster_ids_b = None
+        self.means_ = self.weights_ = self.covariances_ = self.labels_ = None
+        self.lower_bound_: Optional[float] = None
+        self.lower_bound_history_: Optional[list] = None
+        self.n_iter_: Optional[int] = None
+        self.init_source_: Optional[str] = None
+        self.fit_info_: Optional[dict] = None
+        self.hip_estep_enabled_: Optional[bool] = None
+        self.triton_estep_enabled_ = self.triton_fused_update_enabled_ = None
+        self.triton_approx_topk_enabled_ = self.triton_streaming_update_enabled_ = None
+        self.triton_labels_enabled_ = self.approximate_em_enabled_ = None
+        self.approx_top_k_ = None
+        self.large_n_streaming_enabled_ = self.copy_stream_prefetch_enabled_ = None
+        self.cuda_estep_enabled_ = self.cuda_fused_update_enabled_ = self.cuda_approx_topk_enabled_ = None
+        self.last_fallback_reason_: Optional[str] = None
+        self.last_backend_used_: Optional[str] = None
+        self._batch_size: Optional[int] = None
+
+    def _squeeze_if_unbatched(self, value: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        if value is None:
+            return None
+        return value.squeeze(0) if self._batch_size is None else value
+
+    @contextlib.contextmanager
+    def _matmul_precision_scope(self):
+        """Applies ``matmul_precision`` for one call and restores it
+        (gmmxx/interface.py:285-315).  The engine's own products are not
+        affected; torch-side helpers (initial covariances) are."""
+        prev = None
+        if self.matmul_precision is not None:
+            prev = torch.get_float32_matmul_precision()
+            torch.set_float32_matmul_precision(self.matmul_precision)
+        try:
+            yield
+        finally:
+            if prev is not None:
+                torch.set_float32_matmul_precision(prev)
+
+    # -- input handling (gmmxx/interface.py:401-450) ------------------------
+
+    def _normalize_input(self, data: torch.Tensor) -> tuple[torch.Tensor, Optional[int]]:
+        if not torch.is_tensor(data):
+            raise TypeError("data must be a torch.Tensor")
+        if not data.dtype.is_floating_point:
+            raise TypeError("data must be a floating point tensor")
+        if data.ndim == 2:
+            n, d = data.shape
+            if n == 0:
+                raise ValueError("data must contain at least one sample")
+            batch = None
+            data = data.unsqueeze(0)
+        elif data.ndim == 3:
+            bsz, n, d = data.shape
+            if bsz == 0 or n == 0:
+                raise ValueError("data must contain at least one sample")
+            batch = bsz
+        else:
+            raise ValueError("data must have shape (N, D) or (B, N, D)")
+        if self.d is None:
+            self.d = int(d)
+        elif d != self.d:
+            raise ValueError(f"Expected d={self.d}, got d={d}")
+        return data, batch
+
+    def _compute_dtype_for_input(self, x_b: torch.Tensor) -> torch.dtype:
+        if self.dtype is not None:
+            return self.dtype
+        return torch.float32 if x_b.dtype in (torch.float16, torch.bfloat16) else x_b.dtype
+
+    def _engine_tensor(self, x_b: torch.Tensor) -> torch.Tensor:
+        """x on the estimator's GPU in the dtype the engine reads: fp32, or
+        bf16 kept as is for spherical when no explicit dtype asks otherwise."""
+        if self.device.type != "cuda":
+            raise _hip.HipBackendUnavailable(
+                f"the hip backend runs on a ROCm GPU; estimator device is {self.device}")
+        compute = self._compute_dtype_for_input(x_b)
+        if compute == torch.float64:
+            raise TypeError("float64 data is not supported by the hip backend; pass dtype=torch.float32")
+        if x_b.dtype == torch.bfloat16 and self.dtype is None and self.covariance_type == "spherical":
+            target = torch.bfloat16
+        elif compute == torch.bfloat16 and self.covariance_type == "spherical":
+            target = torch.bfloat16
+        else:
+            target = torch.float32
+        return x_b.to(device=self.device, dtype=target).contiguous()
+
+    def _resolve(self, x_b: torch.Tensor, k: int) -> str:
+        if self.approx_top_k is not None:
+            raise NotImplementedError("approximate top-k EM is not provided by the hip backend")
+        shape = (x_b.shape[0], x_b.shape[1], x_b.shape[2], k)
+        return _dispatch.resolve_backend_with_env(self.backend, self.covariance_type, shape, x_b.dtype,
+                                                  legacy_no_triton=self._legacy_no_triton)
+
+    # -- fit (gmmxx/interface.py:1277-1506) ---------------------------------
+
+    def train(self, data: torch.Tensor):
+        with self._matmul_precision_scope():
+            return self._train_impl(data)
+
+    def _train_impl(self, data: torch.Tensor):
+        self._reset_fit_state()
+        x_b, batch_size = self._normalize_input(data)
+        torch.manual_seed(self.seed)
+        if torch.cuda.is_available():
+            torch.cuda.manual_seed_all(self.seed)
+        x_b = self._engine_tensor(x_b)
+        self.last_backend_used_ = self._resolve(x_b, self.k)
+        labels_b, means_b, covs_b, weights_b, info = em.fit(
+            x_b, self.k, self.covariance_type, max_iters=self.niter, tol=self.tol, verbose=self.verbose,
+            init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit)
+        self.cluster_ids_b = labels_b
+        self.means_b = means_b
+        self.variances_b = covs_b
+        self.covariances_b = covs_b
+        self.weights_b = weights_b
+        self._batch_size = batch_size
+        self.means_ = self._squeeze_if_unbatched(means_b)
+        self.weights_ = self._squeeze_if_unbatched(weights_b)
+        self.covariances_ = self._squeeze_if_unbatched(covs_b)
+        self.labels_ = self._squeeze_if_unbatched(labels_b)
+        self.lower_bound_ = float(info["lower_bound"])
+        self.lower_bound_history_ = list(info["lower_bound_history"])
+        self.n_iter_ = int(info["n_iter"])
+        self.init_source_ = str(info["init_source"])
+        self.fit_info_ = dict(info)
+        self.hip_estep_enabled_ = True
+        self.triton_estep_enabled_ = self.triton_fused_update_enabled_ = False
+        self.triton_approx_topk_enabled_ = self.triton_streaming_update_enabled_ = False
+        self.triton_labels_enabled_ = self.approximate_em_enabled_ = False
+        self.large_n_streaming_enabled_ = self.copy_stream_prefetch_enabled_ = False
+        self.cuda_estep_enabled_ = self.cuda_fused_update_enabled_ = self.cuda_approx_topk_enabled_ = False
+        self.last_backend_used_ = "hip"
+
+    def fit(self, data: torch.Tensor, y: Any = None):
+        del y
+        self.train(data)
+        return self
+
+    def fit_predict(self, data: torch.Tensor, y: Any = None) -> torch.Tensor:
+        del y
+        self.train(data)
+        if self.cluster_ids_b is None:
+            labels = self.predict(data)
+            self.cluster_ids_b = labels.unsqueeze(0) if self._batch_size is None else labels
+            self.labels_ = labels
+            return labels
+        return self._squeeze_if_unbatched(self.cluster_ids_b)
+
+    # -- params (gmmxx/interface.py:1508-1603) ------------------------------
+
+    def get_params(self, deep: bool = True) -> dict:
+        del deep
+        return {
+            "d": self.d, "n_components": self.k, "max_iter": self.niter, "tol": self.tol,
+            "random_state": self.seed, "chunk_size_data": self.chunk_size_data,
+            "chunk_size_centroids": self.chunk_size_centroids, "chunk_size_data_cpu": self.chunk_size_data_cpu,
+            "verbose": self.verbose, "dtype": self.dtype, "device": self.device, "init_params": self.init_params,
+            "reg_covar": self.reg_covar, "init_kmeans_iters": self.init_kmeans_iters,
+            "init_kmeans_tol": self.init_kmeans_tol, "covariance_type": self.covariance_type,
+            "matmul_precision": self.matmul_precision, "compute_labels_on_fit": self.compute_labels_on_fit,
+            "approx_top_k": self.approx_top_k, "backend": self.backend,
+        }
+
+    def set_params(self, **params: Any):
+        if not params:
+            return self
+        valid = set(_PARAM_NAMES) | {"k", "niter", "seed", "use_triton"}
+        for raw_name, value in params.items():
+            if raw_name not in valid:
+                raise ValueError(f"Invalid parameter {raw_name!r} for GMMXX")
+            name = _SKLEARN_PARAM_ALIASES.get(raw_name, raw_name)
+            if name == "d":
+                value = _optional_positive_int(value, "d")
+            elif name in {"k", "niter", "chunk_size_data", "chunk_size_centroids", "chunk_size_data_cpu",
+                          "init_kmeans_iters"}:
+                value = _positive_int(value, name)
+            elif name in {"tol", "reg_covar", "init_kmeans_tol"}:
+                value = float(value)
+                if value < 0.0:
+                    raise ValueError(f"{name} must be non-negative")
+            elif name == "seed":
+                value = int(value)
+            elif name == "use_triton":
+                if value is not None:
+                    if self.backend != "auto":
+                        raise ValueError("Cannot set use_triton when backend is already explicit "
+                                         f"(self.backend={self.backend!r}). Drop use_triton; "
+                                         "backend= is the canonical kwarg.")
+                    warnings.warn("use_triton is deprecated and has no effect with gmmxx_amd; use backend='hip'",
+                                  DeprecationWarning, stacklevel=2)
+                    self._legacy_no_triton = not bool(value)
+                continue
+            elif name == "backend":
+                _check_backend(value)
+            elif name in {"verbose", "compute_labels_on_fit"}:
+                value = bool(value)
+            elif name == "covariance_type":
+                value = _normalize_covariance_type(value)
+            elif name == "matmul_precision" and value is not None and value not in {"highest", "high", "medium"}:
+                raise ValueError("matmul_precision must be None, 'highest', 'high', or 'medium'")
+            elif name == "approx_top_k":
+                value = _optional_positive_int(value, "approx_top_k")
+            elif name == "device":
+                value = torch.device(value)
+                self._raw_device = value
+            setattr(self, name, value)
+        self._reset_fit_state()
+        return self
+
+    # -- inference (gmmxx/interface.py:1605-2521) ---------------------------
+
+    def _require_trained(self) -> None:
+        if self.means_b is None or self.variances_b is None or self.weights_b is None:
+            raise RuntimeError("Model not trained. Call train() or fit() first.")
+
+    def _prepare_predict_input(self, data: torch.Tensor) -> tuple[torch.Tensor, Optional[int]]:
+        self._require_trained()
+        x_b, batch_size = self._normalize_input(data)
+        if batch_size != self._batch_size:
+            raise ValueError(f"Model was trained with batch size B={self._batch_size}, "
+                             f"but received B={batch_size}.")
+        x_b = self._engine_tensor(x_b)
+        self.last_backend_used_ = self._resolve(x_b, int(self.means_b.shape[1]))
+        return x_b, batch_size
+
+    def _params(self):
+        return self.means_b.contiguous(), self.variances_b.contiguous(), self.weights_b.contiguous()
+
+    def predict(self, data: torch.Tensor) -> torch.Tensor:
+        """First-max component index per sample, int64 (gmmxx/interface.py:1753-1971)."""
+        with self._matmul_precision_scope():
+            x_b, batch_size = self._prepare_predict_input(data)
+            means, covs, weights = self._params()
+            _, labels = _hip.score(self.covariance_type, x_b, means, covs, weights, want_scores=False)
+            return labels.squeeze(0) if batch_size is None else labels
+
+    def predict_proba(self, data: torch.Tensor) -> torch.Tensor:
+        """Responsibilities (B, N, K) fp32 (gmmxx/interface.py:1973-2268)."""
+        with self._matmul_precision_scope():
+            x_b, batch_size = self._prepare_predict_input(data)
+            means, covs, weights = self._params()
+            probs = _hip.predict_proba(self.covariance_type, x_b, means, covs, weights)
+            return probs.squeeze(0) if batch_size is None else probs
+
+    def score_samples(self, data: torch.Tensor) -> torch.Tensor:
+        """Per-sample log-likelihood log Σ_k w_k N(x | μ_k, Σ_k), fp32
+        (gmmxx/interface.py:2270-2521)."""
+        with self._matmul_precision_scope():
+            x_b, batch_size = self._prepare_predict_input(data)
+            means, covs, weights = self._params()
+            scores, _ = _hip.score(self.covariance_type, x_b, means, covs, weights, want_labels=False)
+            return scores.squeeze(0) if batch_size is None else scores
+
+    def score(self, data: torch.Tensor, y: Any = None) -> float:
+        del y
+        return float(self.score_samples(data).mean().item())
+
+    # -- model selection (gmmxx/interface.py:2537-2558) ---------------------
+
+    def _n_parameters(self, batch_size: int = 1) -> int:
+        self._require_trained()
+        d = int(self.means_b.shape[-1])
+        k = int(self.means_b.shape[1])
+        covariance_params = {"spherical": k, "diag": k * d, "tied": d * (d + 1) // 2,
+                             "full": k * d * (d + 1) // 2}[self.covariance_type]
+        return int(batch_size * (k * d + covariance_params + k - 1))
+
+    def bic(self, data: torch.Tensor) -> float:
+        scores = self.score_samples(data)
+        n_samples = int(scores.numel())
+        batch_size = int(scores.shape[0]) if scores.ndim == 2 else 1
+        return float(-2.0 * scores.sum().item() + self._n_parameters(batch_size) * math.log(float(n_samples)))
+
+    def aic(self, data: torch.Tensor) -> float:
+        scores = self.score_samples(data)
+        batch_size = int(scores.shape[0]) if scores.ndim == 2 else 1
+        return float(-2.0 * scores.sum().item() + 2.0 * self._n_parameters(batch_size))
