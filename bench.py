@@ -1,31 +1,41 @@
 """Benchmark of the HIP GMM EM hot path on one MI355X.
 
-Workload (the headline metric): spherical GMM,
-bf16 inputs with fp32 accumulation, N = 4,194,304, D = 128, K = 1024, one
-batch.  Synthetic data, seed 1: centres ~ N(0, 4I), per-component std
-~ U[0.5, 1.5], Dirichlet(1) weights, labels ~ multinomial(weights),
-x = centre + std * N(0, I) rounded to bf16.  Initial means are K distinct
-random rows, variances the global spherical variance, weights 1/K.
+Headline: spherical GMM, bf16 inputs with fp32
+accumulation, N = 4,194,304, D = 128, K = 1024, one batch.  A "step" is one
+soft-EM iteration over all N rows (prelude, E-step log-normaliser,
+responsibilities, M-step statistics, finalize) with x resident in HBM;
+``value`` is EM iterations per second.
 
-A "step" is one soft-EM iteration over all N rows (gmmxx_hip_em_step: prelude,
-E-step log-normaliser, responsibilities, M-step statistics, finalize), with x
-resident in HBM.  ``value`` is EM iterations per second.
+The other BASELINE configs (C1, C3, C4, C5) and the supplementary small-D
+large-N bf16 case (C1L) are measured the same way and reported under
+``configs`` with their own roofline fractions and CPU baselines.  Data follow
+the BASELINE recipes, generated on the device with seeded generators.
 
-Also reported:
-  * roofline: the dominant kernel's algorithmic MFMA rate, from its average
-    launch time measured with HIP events on its own stream over the timed
-    region (each phase of the iteration is launched between events);
-  * em_iteration: the whole iteration's algorithmic rate against the bf16
-    dense MFMA peak (the BASELINE target is >= 60 %);
+Reported per config:
+  * iter_per_s / ms_per_iter: wall time of the timed EM iterations;
+  * roofline: the dominant kernel's algorithmic rate (FLOP/s, or bytes/s for
+    the HBM-bound case) from its launch times, measured with HIP events
+    recorded on the stream the kernels are launched on, against the MI355X
+    peak of its bound;
+  * em_iteration: the whole iteration's algorithmic rate;
   * cpu_baseline: the CPU oracle (a restatement of the reference torch
-    fallback) timed on the host on a bounded row sample, scaled to full N.
+    fallback) timed on a bounded row sample, scaled linearly to full N.
+``roofline.traffic`` (HBM bytes per launch of the dominant kernel) is read
+from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when one exists
+for that kernel and workload.
+
+``--copy-calibration`` additionally runs a plain 1 GiB device copy, so that a
+``rocprofv3 --pmc`` pass over this program can scale the counters by a copy
+of known size.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
+import re
 import sys
 import time
 
@@ -34,141 +44,357 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-N, D, K = 4_194_304, 128, 1024
-SEED = 1
-PEAK_BF16_TFLOPS = 2516.6            # MI355X dense bf16 MFMA
-PEAK_HBM_GBS = 8000.0
+PEAK = {"bf16": 2516.6, "fp32": 157.3, "hbm": 8000.0}   # TFLOP/s, TFLOP/s, GB/s (MI355X)
 METRIC = "EM iter/s + % bf16 MFMA peak, spherical bf16 N=4M D=128 K=1024"
+HEADLINE = "c2"
+
+CONFIGS = {
+    "c1": dict(cov="spherical", B=1, N=100_000, D=32, K=64, dtype="fp32", iters=20, seed=0, bound="fp32",
+               desc="spherical fp32 N=100000 D=32 K=64, 20 iterations"),
+    "c2": dict(cov="spherical", B=1, N=4_194_304, D=128, K=1024, dtype="bf16", iters=10, seed=1, bound="bf16",
+               desc="spherical bf16 N=4194304 D=128 K=1024, 10 iterations"),
+    "c3": dict(cov="diag", B=1, N=2_097_152, D=64, K=512, dtype="fp32", iters=10, seed=2, bound="fp32",
+               desc="diag fp32 N=2097152 D=64 K=512, 10 iterations"),
+    "c4": dict(cov="tied", B=1, N=1_048_576, D=64, K=256, dtype="fp32", iters=10, seed=3, bound="fp32",
+               desc="tied fp32 N=1048576 D=64 K=256, 10 iterations"),
+    "c5": dict(cov="full", B=16, N=262_144, D=16, K=32, dtype="fp32", iters=10, seed=4, bound="fp32",
+               desc="full fp32 B=16 N=262144 D=16 K=32, 10 iterations + predict_proba + score_samples"),
+    "c1l": dict(cov="spherical", B=1, N=1 << 24, D=32, K=64, dtype="bf16", iters=20, seed=0, bound="hbm",
+                desc="spherical bf16 N=16777216 D=32 K=64 (C1 recipe, large N), 20 iterations"),
+}
+# CPU-baseline samples: rows per batch and oracle iterations (about 2-8 s each on 16 cores).
+CPU_SAMPLE = {"c1": (100_000, 20), "c2": (131_072, 2), "c3": (131_072, 2), "c4": (262_144, 2),
+              "c5": (16_384, 2), "c1l": (1_048_576, 2)}
 
 
-def algorithmic_flops(n, d, k):
-    """Minimal contractions per EM iteration: E-step x·μᵀ (2NKD) and M-step
-    rᵀ·[x | ‖x‖² | 1] (2NK(D+2))."""
-    return {"lse_tile": 2.0 * n * k * d, "stats_tile": 2.0 * n * k * (d + 2),
-            "iteration": 2.0 * n * k * (2 * d + 2)}
+def flops(cfg):
+    """Algorithmic FLOPs of the minimal contractions (E-step logits and M-step
+    rᵀ·[x-features | 1]) per EM iteration, split by the kernel computing them."""
+    b, n, d, k = cfg["B"], cfg["N"], cfg["D"], cfg["K"]
+    bn = b * n
+    s = d * (d + 1) // 2
+    e, m = {
+        "spherical": (2 * bn * k * d, 2 * bn * k * (d + 2)),
+        "diag": (2 * bn * k * 2 * d, 2 * bn * k * (2 * d + 1)),
+        "tied": (2 * bn * d * d + 2 * bn * k * d, 2 * bn * k * (d + 1)),
+        "full": (2 * bn * k * (s + d), 2 * bn * k * (s + d + 1)),
+    }[cfg["cov"]]
+    return {"lse_tile": float(e), "stats_tile": float(m), "iteration": float(e + m)}
 
 
-def make_data(device, n=N, d=D, k=K, seed=SEED):
-    g = torch.Generator(device=device).manual_seed(seed)
-    centers = 2.0 * torch.randn((k, d), generator=g, device=device)
-    sigma = 0.5 + torch.rand((k,), generator=g, device=device)
-    w = -torch.log(torch.rand((k,), generator=g, device=device))
-    w = w / w.sum()
-    labels = torch.multinomial(w, n, replacement=True, generator=g)
-    x = torch.empty((1, n, d), dtype=torch.bfloat16, device=device)
-    chunk = 1 << 20
-    for s in range(0, n, chunk):
-        e = min(n, s + chunk)
-        lab = labels[s:e]
-        noise = torch.randn((e - s, d), generator=g, device=device)
-        x[0, s:e] = (centers[lab] + sigma[lab, None] * noise).to(torch.bfloat16)
-    idx = torch.randperm(n, generator=g, device=device)[:k]
-    means0 = x[0, idx].to(torch.float32).unsqueeze(0).contiguous()
-    # Global spherical variance (torch_fallback.py:1348-1363), fixed by the harness.
-    s1 = torch.zeros(d, dtype=torch.float64, device=device)
-    s2 = torch.zeros((), dtype=torch.float64, device=device)
-    for s in range(0, n, chunk):
-        xf = x[0, s:s + chunk].to(torch.float64)
-        s1 += xf.sum(0)
-        s2 += xf.square().sum()
-    mean = s1 / n
-    gv = float(((s2 / n) - mean.square().sum()).clamp_min(0.0) / d)
-    var0 = torch.full((1, k), max(gv, 1e-6), dtype=torch.float32, device=device)
-    w0 = torch.full((1, k), 1.0 / k, dtype=torch.float32, device=device)
-    return x, means0, var0, w0
+def x_bytes(cfg):
+    return cfg["B"] * cfg["N"] * cfg["D"] * (2 if cfg["dtype"] == "bf16" else 4)
 
 
-def cpu_baseline(x_dev, means0, var0, w0, sample_rows, iters):
-    """Oracle EM iterations on the first `sample_rows` rows (fp32 on the
-    bf16 values), scaled linearly in N to the full workload."""
-    from oracle import torch_ref
-    torch.set_num_threads(min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "64"))))
-    xs = x_dev[:, :sample_rows].to(torch.float32).cpu()
-    m, v, w = means0.cpu(), var0.cpu(), w0.cpu()
-    torch_ref.fit(xs[:, :4096], K, "spherical", max_iters=1, tol=0.0, init_means=m, init_covs=v,
-                  init_weights=w, compute_labels=False)  # warm the thread pool
-    t0 = time.perf_counter()
-    torch_ref.fit(xs, K, "spherical", max_iters=iters, tol=0.0, init_means=m, init_covs=v,
-                  init_weights=w, compute_labels=False)
-    dt = (time.perf_counter() - t0) / iters
-    full_iter_s = dt * (x_dev.shape[1] / sample_rows)
-    return {"value": 1.0 / full_iter_s, "unit": "EM iter/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{iters} oracle EM iterations on the first {sample_rows} of {x_dev.shape[1]} rows "
-                      f"({dt:.3f} s/iter), scaled linearly in N"}
+# ---------------------------------------------------------------------------
+# Synthetic data (BASELINE.json recipes), generated on the device
+# ---------------------------------------------------------------------------
+
+def _chunks(n, size=1 << 20):
+    for s in range(0, n, size):
+        yield s, min(n, s + size)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-sample-rows", type=int, default=131072)
-    ap.add_argument("--cpu-iters", type=int, default=2)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sharding design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
-        sys.exit(2)
+def _distinct_rows(x, k, g):
+    idx = torch.randperm(x.shape[1], generator=g, device=x.device)[:k]
+    return x[:, idx].to(torch.float32).contiguous()
 
+
+def _global_spherical_var(x, k, reg=1e-6):
+    b, n, d = x.shape
+    out = []
+    for bi in range(b):
+        s1 = torch.zeros(d, dtype=torch.float64, device=x.device)
+        s2 = torch.zeros((), dtype=torch.float64, device=x.device)
+        for s, e in _chunks(n):
+            xf = x[bi, s:e].to(torch.float64)
+            s1 += xf.sum(0)
+            s2 += xf.square().sum()
+        mean = s1 / n
+        out.append(max(float(((s2 / n) - mean.square().sum()).clamp_min(0.0) / d), reg))
+    return torch.tensor(out, dtype=torch.float32, device=x.device)[:, None].expand(b, k).contiguous()
+
+
+def _global_cov(x, reg=1e-6):
+    xf = x.to(torch.float64)
+    c = xf - xf.mean(dim=1, keepdim=True)
+    cov = torch.bmm(c.transpose(1, 2), c) / x.shape[1]
+    cov = 0.5 * (cov + cov.transpose(1, 2)) + reg * torch.eye(x.shape[2], device=x.device, dtype=torch.float64)
+    return cov.to(torch.float32)
+
+
+def make_data(name, device):
+    cfg = CONFIGS[name]
+    b, n, d, k = cfg["B"], cfg["N"], cfg["D"], cfg["K"]
+    g = torch.Generator(device=device).manual_seed(cfg["seed"])
+    xdt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+    x = torch.empty((b, n, d), dtype=xdt, device=device)
+    w0 = torch.full((b, k), 1.0 / k, dtype=torch.float32, device=device)
+    if name in ("c1", "c1l"):
+        # K centres ~ U[-10, 10]^D, balanced labels (n mod K) permuted, unit noise;
+        # means = first K rows, variances 1, weights 1/K.
+        centers = torch.rand((k, d), generator=g, device=device) * 20.0 - 10.0
+        lab = (torch.arange(n, device=device) % k)[torch.randperm(n, generator=g, device=device)]
+        for s, e in _chunks(n):
+            x[0, s:e] = (centers[lab[s:e]] + torch.randn((e - s, d), generator=g, device=device)).to(xdt)
+        means0 = x[:, :k].to(torch.float32).contiguous()
+        covs0 = torch.ones((b, k), dtype=torch.float32, device=device)
+    elif name == "c2":
+        # centres ~ N(0, 4I), std ~ U[0.5, 1.5], Dirichlet(1) weights, multinomial labels;
+        # means = K distinct random rows, global spherical variance, weights 1/K.
+        centers = 2.0 * torch.randn((k, d), generator=g, device=device)
+        sigma = 0.5 + torch.rand((k,), generator=g, device=device)
+        w = -torch.log(torch.rand((k,), generator=g, device=device))
+        lab = torch.multinomial(w / w.sum(), n, replacement=True, generator=g)
+        for s, e in _chunks(n):
+            noise = torch.randn((e - s, d), generator=g, device=device)
+            x[0, s:e] = (centers[lab[s:e]] + sigma[lab[s:e], None] * noise).to(xdt)
+        means0 = _distinct_rows(x, k, g)
+        covs0 = _global_spherical_var(x, k)
+    elif name == "c3":
+        # centres ~ U[-8, 8]^D, per-dimension std log-uniform in [0.5, 2], equal weights;
+        # means = K distinct random rows, global per-feature variance, weights 1/K.
+        centers = torch.rand((k, d), generator=g, device=device) * 16.0 - 8.0
+        lo, hi = math.log(0.5), math.log(2.0)
+        sigma = torch.exp(lo + (hi - lo) * torch.rand((k, d), generator=g, device=device))
+        lab = torch.randint(0, k, (n,), generator=g, device=device)
+        for s, e in _chunks(n):
+            noise = torch.randn((e - s, d), generator=g, device=device)
+            x[0, s:e] = centers[lab[s:e]] + sigma[lab[s:e]] * noise
+        means0 = _distinct_rows(x, k, g)
+        xf = x[0].to(torch.float64)
+        gv = (xf - xf.mean(0)).square().mean(0).clamp_min(1e-6).to(torch.float32)
+        covs0 = gv[None, None].expand(b, k, d).contiguous()
+    elif name == "c4":
+        # Σ = AAᵀ/D + 0.1I, A ~ N(0,1)^{DxD}; centres ~ N(0, 9I); equal weights;
+        # x = c + chol(Σ)·z; means = K distinct random rows, global covariance, weights 1/K.
+        a = torch.randn((d, d), generator=g, device=device, dtype=torch.float64)
+        sig = a @ a.T / d + 0.1 * torch.eye(d, device=device, dtype=torch.float64)
+        chol = torch.linalg.cholesky(sig).to(torch.float32)
+        centers = 3.0 * torch.randn((k, d), generator=g, device=device)
+        lab = torch.randint(0, k, (n,), generator=g, device=device)
+        for s, e in _chunks(n):
+            z = torch.randn((e - s, d), generator=g, device=device)
+            x[0, s:e] = centers[lab[s:e]] + z @ chol.T
+        means0 = _distinct_rows(x, k, g)
+        covs0 = _global_cov(x)
+    elif name == "c5":
+        # per problem and component L lower-triangular ~ N(0, 0.5²), Σ = LLᵀ + 0.05I;
+        # centres ~ U[-6, 6]^D; Dirichlet(2) weights; means = K distinct rows per
+        # problem, the problem's global covariance for every component, weights 1/K.
+        L = torch.tril(0.5 * torch.randn((b, k, d, d), generator=g, device=device, dtype=torch.float64))
+        sig = L @ L.transpose(-1, -2) + 0.05 * torch.eye(d, device=device, dtype=torch.float64)
+        chol = torch.linalg.cholesky(sig).to(torch.float32)
+        centers = torch.rand((b, k, d), generator=g, device=device) * 12.0 - 6.0
+        u = torch.rand((b, k, 2), generator=g, device=device)
+        w = -torch.log(u).sum(-1)
+        means0 = torch.empty((b, k, d), dtype=torch.float32, device=device)
+        for bi in range(b):
+            lab = torch.multinomial(w[bi] / w[bi].sum(), n, replacement=True, generator=g)
+            z = torch.randn((n, d), generator=g, device=device)
+            x[bi] = centers[bi, lab] + torch.einsum("nde,ne->nd", chol[bi, lab], z)
+            means0[bi] = x[bi, torch.randperm(n, generator=g, device=device)[:k]]
+        covs0 = _global_cov(x)[:, None].expand(b, k, d, d).contiguous()
+    else:
+        raise KeyError(name)
+    return x, means0, covs0, w0
+
+
+# ---------------------------------------------------------------------------
+# Measurement
+# ---------------------------------------------------------------------------
+
+def _traffic_from_profile(name, phase):
+    """HBM bytes per launch of (config, phase) from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"em_tile_{name}_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        m = re.match(r"\s*(\w+)\s*=\s*([0-9.eE+-]+)\s*$", line)
+        if m:
+            vals[m.group(1)] = float(m.group(2))
+    key = f"{phase}_bytes_per_launch"
+    return vals.get(key)
+
+
+def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
     from gmmxx_amd import _hip
-    _hip.require_hip()
-    dev = torch.device("cuda:0")
-    print(f"[bench] generating data N={N} D={D} K={K}", file=sys.stderr, flush=True)
-    x, means0, var0, w0 = make_data(dev)
-    means, var, w = means0.clone(), var0.clone(), w0.clone()
-    prob = _hip.problem("spherical", x.dtype, 1, N, D, K)
+    cfg = CONFIGS[name]
+    steps = cfg["iters"] if steps is None else steps
+    cov = cfg["cov"]
+    print(f"[bench] {name}: generating data ({cfg['desc']})", file=sys.stderr, flush=True)
+    x, means0, covs0, w0 = make_data(name, dev)
+    b, n, d, k = cfg["B"], cfg["N"], cfg["D"], cfg["K"]
+    prob = _hip.problem(cov, x.dtype, b, n, d, k)
     ws = _hip.Workspace(prob, dev)
-    lb = torch.zeros((max(1, args.steps + args.warmup),), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    gram = _hip.gram(x, ws) if cov == "tied" else None
+    torch.cuda.synchronize()
+    setup_ms = 1e3 * (time.perf_counter() - t0)
+    lb = torch.zeros((max(1, steps + warmup),), dtype=torch.float32, device=dev)
     phases = _hip.EM_PHASES
+    means, covs, w = means0.clone(), covs0.clone(), w0.clone()
 
     def step(i, events=None):
         for j, ph in enumerate(phases):
             if events is not None:
                 events[j].record()
-            _hip.em_phase(ph, "spherical", x, means, var, w, lb[i:i + 1], ws)
+            _hip.em_phase(ph, cov, x, means, covs, w, lb[i:i + 1], ws, gram_xx=gram)
         if events is not None:
             events[len(phases)].record()
 
-    print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
-    for i in range(args.warmup):
+    print(f"[bench] {name}: warmup {warmup}", file=sys.stderr, flush=True)
+    for i in range(warmup):
         step(i)
-    torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(args.steps)]
-    print(f"[bench] timing {args.steps} EM iterations", file=sys.stderr, flush=True)
+    # The timed iterations start from the initial parameters again: one fit's EM loop.
+    means.copy_(means0)
+    covs.copy_(covs0)
+    w.copy_(w0)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(steps)]
+    print(f"[bench] {name}: timing {steps} EM iterations", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i, evs[i])
+    for i in range(steps):
+        step(warmup + i, evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = 1e3 * wall / args.steps
-    phase_ms = {ph: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / args.steps for j, ph in enumerate(phases)}
-    flops = algorithmic_flops(N, D, K)
+    ms_per_step = 1e3 * wall / steps
+    phase_ms = {ph: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, ph in enumerate(phases)}
+    fl = flops(cfg)
     dominant = max(("lse_tile", "stats_tile"), key=lambda p: phase_ms[p])
-    achieved = flops[dominant] / (phase_ms[dominant] * 1e-3) / 1e12
-    iter_tflops = flops["iteration"] / (ms_per_step * 1e-3) / 1e12
-    lbs = lb[args.warmup:args.warmup + args.steps].tolist()
-
-    result = {
-        "metric": METRIC, "value": 1e3 / ms_per_step, "unit": "EM iter/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (BASELINE config 2 recipe, seed 1, generated on device)",
-        "config": {"workload": "spherical GMM EM iteration, bf16 x with fp32 accumulation",
-                   "B": 1, "N": N, "D": D, "K": K, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": f"em_tile ({dominant})",
-                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None},
-        "em_iteration": {"algorithmic_tflop": flops["iteration"] / 1e12, "achieved_tflops": iter_tflops,
-                         "frac_of_bf16_peak": iter_tflops / PEAK_BF16_TFLOPS,
-                         "phase_ms": phase_ms},
-        "lower_bound_last": lbs[-1] if lbs else None,
+    bound = cfg["bound"]
+    if bound == "hbm":
+        # Each tile pass must read x once: the algorithmic bytes of one launch.
+        achieved = x_bytes(cfg) / (phase_ms[dominant] * 1e-3) / 1e9
+        unit = "GB/s"
+        it_rate = x_bytes(cfg) / (ms_per_step * 1e-3) / 1e9
+        it_unit = "GB/s (x read once per iteration)"
+    else:
+        achieved = fl[dominant] / (phase_ms[dominant] * 1e-3) / 1e12
+        unit = "TFLOP/s"
+        it_rate = fl["iteration"] / (ms_per_step * 1e-3) / 1e12
+        it_unit = "TFLOP/s"
+    peak = PEAK[bound]
+    out = {
+        "config": cfg["desc"], "covariance_type": cov, "B": b, "N": n, "D": d, "K": k, "dtype": cfg["dtype"],
+        "steps": steps, "warmup": warmup, "ms_per_iter": ms_per_step, "iter_per_s": 1e3 / ms_per_step,
+        "gflop_per_s": fl["iteration"] / (ms_per_step * 1e-3) / 1e9,
+        "roofline": {"bound": "hbm" if bound == "hbm" else "mfma", "peak_kind": bound,
+                     "kernel": f"em_tile ({dominant})", "achieved": achieved, "peak": peak, "unit": unit,
+                     "frac": achieved / peak, "traffic": _traffic_from_profile(name, dominant)},
+        "em_iteration": {"algorithmic_tflop": fl["iteration"] / 1e12, "achieved": it_rate, "unit": it_unit,
+                         "frac": it_rate / peak, "phase_ms": phase_ms},
+        "setup_ms": setup_ms,
+        "lower_bound_last": float(lb[warmup + steps - 1].item()),
     }
-    if not args.no_cpu_baseline:
-        print(f"[bench] cpu baseline on {args.cpu_sample_rows} rows", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(x, means0, var0, w0, args.cpu_sample_rows, args.cpu_iters)
+    if name == "c5":
+        # Tail of the config: predict_proba + score_samples on all points.
+        for _ in range(2):
+            _hip.predict_proba(cov, x, means, covs, w, ws=ws)
+            _hip.score(cov, x, means, covs, w, want_labels=False, ws=ws)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = 5
+        for _ in range(reps):
+            _hip.predict_proba(cov, x, means, covs, w, ws=ws)
+            _hip.score(cov, x, means, covs, w, want_labels=False, ws=ws)
+        torch.cuda.synchronize()
+        tail_ms = 1e3 * (time.perf_counter() - t0) / reps
+        out["tail"] = {"ms": tail_ms, "what": "predict_proba (B,N,K fp32 written) + score_samples",
+                       "proba_write_gb_per_s": b * n * k * 4 / (tail_ms * 1e-3) / 1e9}
+    if copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_calibration"] = {"bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4, "launches": 3}
+    return out, (x, means0, covs0, w0)
+
+
+def cpu_baseline(name, data):
+    """Oracle EM iterations on the first rows of each problem (fp32 on the
+    same values), scaled linearly in N to the full workload."""
+    from oracle import torch_ref
+    cfg = CONFIGS[name]
+    rows, iters = CPU_SAMPLE[name]
+    x, m0, c0, w0 = data
+    rows = min(rows, cfg["N"])
+    torch.set_num_threads(max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")))))
+    xs = x[:, :rows].to(torch.float32).cpu()
+    m, c, w = m0.cpu(), c0.cpu(), w0.cpu()
+    torch_ref.fit(xs[:, :min(rows, 4096)], cfg["K"], cfg["cov"], max_iters=1, tol=0.0, init_means=m,
+                  init_covs=c, init_weights=w, compute_labels=False)  # warm the thread pool
+    t0 = time.perf_counter()
+    torch_ref.fit(xs, cfg["K"], cfg["cov"], max_iters=iters, tol=0.0, init_means=m, init_covs=c,
+                  init_weights=w, compute_labels=False)
+    dt = (time.perf_counter() - t0) / iters
+    full_iter_s = dt * (cfg["N"] / rows)
+    sample = ("the full workload" if rows == cfg["N"] else
+              f"the first {rows} of {cfg['N']} rows per problem, scaled linearly in N")
+    return {"value": 1.0 / full_iter_s, "unit": "EM iter/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{iters} oracle EM iterations on {sample} ({dt:.3f} s per sampled iteration)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20, help="timed EM iterations of the headline config")
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default=None, help="comma-separated configs (default: all)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path; the EM iteration "
+              "would shard over rows with one all-reduce of the statistics. Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from gmmxx_amd import _hip
+    _hip.require_hip()
+    dev = torch.device("cuda:0")
+    names = args.only.split(",") if args.only else list(CONFIGS)
+    for nm in names:
+        if nm not in CONFIGS:
+            sys.exit(f"unknown config {nm!r}; choose from {sorted(CONFIGS)}")
+    results = {}
+    for nm in names:
+        steps = args.steps if nm == HEADLINE else None
+        res, data = run_config(nm, dev, steps=steps, warmup=args.warmup,
+                               copy_calibration=args.copy_calibration and nm == names[-1])
+        if not args.no_cpu_baseline:
+            print(f"[bench] {nm}: cpu baseline", file=sys.stderr, flush=True)
+            res["cpu_baseline"] = cpu_baseline(nm, data)
+        del data
+        torch.cuda.empty_cache()
+        results[nm] = res
+        print(f"[bench] {nm}: {res['ms_per_iter']:.3f} ms/iter, {res['roofline']['kernel']} "
+              f"{100 * res['roofline']['frac']:.1f}% of {res['roofline']['peak_kind']} peak",
+              file=sys.stderr, flush=True)
+
+    head = results.get(HEADLINE) or results[names[0]]
+    head_name = HEADLINE if HEADLINE in results else names[0]
+    cfg = CONFIGS[head_name]
+    result = {
+        "metric": METRIC if head_name == HEADLINE else f"EM iter/s, {cfg['desc']}",
+        "value": head["iter_per_s"], "unit": "EM iter/s", "n_gpus": 1,
+        "steps": head["steps"], "warmup": head["warmup"], "ms_per_step": head["ms_per_iter"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": cfg["dtype"],
+        "data": f"synthetic (BASELINE config recipe, seed {cfg['seed']}, generated on device)",
+        "config": {"workload": f"GMM soft-EM iteration: {cfg['desc'].split(',')[0]}",
+                   "covariance_type": cfg["cov"], "B": cfg["B"], "N": cfg["N"], "D": cfg["D"], "K": cfg["K"],
+                   "parallelism": "single GPU"},
+        "roofline": {kk: v for kk, v in head["roofline"].items() if kk != "peak_kind"},
+        "em_iteration": head["em_iteration"],
+    }
+    if "cpu_baseline" in head:
+        result["cpu_baseline"] = head["cpu_baseline"]
+    result["configs"] = results
     print(json.dumps(result), flush=True)
 
 

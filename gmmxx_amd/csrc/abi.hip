@@ -37,7 +37,8 @@ struct Plan {
   size_t o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_prec = 0, o_logdet = 0, o_gram = 0, total = 0;
 };
 
-constexpr int kTargetBlocks = 512;  // ~2 workgroups per CU on 256 CUs
+constexpr int kTargetWaves = 4096;      // 16 waves per CU on 256 CUs
+constexpr int kMinBlocksPerSlice = 8;  // row blocks of one slice (bounds the partial-statistics count)
 
 int dp_for(int64_t d) {
   const int dps[] = {16, 32, 64, 128};
@@ -80,8 +81,9 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.nw = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
   q.ktiles = (q.K + q.nw * q.CW - 1) / (q.nw * q.CW);
   const int64_t row_blocks = (q.N + kBN - 1) / kBN;
-  int64_t slices = std::max<int64_t>(1, (kTargetBlocks + (int64_t)q.ktiles * q.B - 1) / ((int64_t)q.ktiles * q.B));
-  slices = std::min(slices, row_blocks);
+  const int64_t target_blocks = (kTargetWaves + q.nw - 1) / q.nw;
+  int64_t slices = std::max<int64_t>(1, (target_blocks + (int64_t)q.ktiles * q.B - 1) / ((int64_t)q.ktiles * q.B));
+  slices = std::min(slices, std::max<int64_t>(1, row_blocks / kMinBlocksPerSlice));
   q.rows_per_slice = ((q.N + slices - 1) / slices + kBN - 1) / kBN * kBN;
   q.slices = (int)((q.N + q.rows_per_slice - 1) / q.rows_per_slice);
   q.cblocks = combine_blocks(q.N);

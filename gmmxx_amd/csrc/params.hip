@@ -244,24 +244,35 @@ __global__ void chol_finish_kernel(const float* cov, int D, int M, const int* fi
 // Tied: per-row quadratic form xᵀ P x (torch_fallback.py:451)
 // ---------------------------------------------------------------------------
 
-__global__ void rowquad_kernel(const float* x, int64_t N, int D, const float* prec, float* rowq) {
-  __shared__ float Ps[kMaxCholD * kMaxCholD];
+// One thread per row; P staged in LDS, zero-padded to DP x DP so the unrolled
+// loops need no bounds (all lanes read the same P entry: LDS broadcast).
+// q = Σ_d x_d (P_dd x_d + 2 Σ_{e>d} P_de x_e), P symmetric.
+template <int DP>
+__global__ __launch_bounds__(256) void rowquad_kernel(const float* __restrict__ x, int64_t N, int D,
+                                                      const float* __restrict__ prec, float* __restrict__ rowq) {
+  __shared__ float Ps[DP * DP];
   const int b = blockIdx.y;
   const float* P = prec + (size_t)b * D * D;
-  for (int i = threadIdx.x; i < D * D; i += blockDim.x) Ps[i] = P[i];
+  for (int i = threadIdx.x; i < DP * DP; i += blockDim.x) {
+    const int r = i / DP, c = i % DP;
+    Ps[i] = (r < D && c < D) ? P[r * D + c] : 0.f;
+  }
   __syncthreads();
   const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= N) return;
   const float* xr = x + ((size_t)b * N + n) * D;
-  float xv[kMaxCholD];
-  for (int d = 0; d < D; ++d) xv[d] = xr[d];
+  float xv[DP];
+#pragma unroll
+  for (int d = 0; d < DP; ++d) xv[d] = d < D ? xr[d] : 0.f;
   float q = 0.f;
-  for (int d = 0; d < D; ++d) {
-    float t = 0.f;
-    for (int e = 0; e < D; ++e) t = fmaf(Ps[d * D + e], xv[e], t);
+#pragma unroll
+  for (int d = 0; d < DP; ++d) {
+    float t = 0.5f * Ps[d * DP + d] * xv[d];
+#pragma unroll
+    for (int e = d + 1; e < DP; ++e) t = fmaf(Ps[d * DP + e], xv[e], t);
     q = fmaf(xv[d], t, q);
   }
-  rowq[(size_t)b * N + n] = q;
+  rowq[(size_t)b * N + n] = 2.f * q;
 }
 
 // ---------------------------------------------------------------------------
@@ -302,13 +313,25 @@ __global__ void ll_reduce_kernel(const double* ll_part, int count, double inv_to
   if (threadIdx.x == 0) out[0] = (float)(s * inv_total);
 }
 
-// out[i] = Σ_s part[s * M + i], fixed slice order (deterministic).
-__global__ void reduce_slices_kernel(const float* part, int slices, int64_t M, float* out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= M) return;
+// out[i] = Σ_s part[s * M + i] in a fixed order (deterministic): a block owns
+// 64 outputs; wave g sums slices g, g + 16, ...; the 16 wave sums are then
+// added in wave order.
+constexpr int kRedWaves = 16;
+__global__ __launch_bounds__(64 * kRedWaves) void reduce_slices_kernel(const float* part, int slices, int64_t M,
+                                                                       float* out) {
+  __shared__ float red[kRedWaves][64];
+  const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
   float s = 0.f;
-  for (int t = 0; t < slices; ++t) s += part[(size_t)t * M + i];
-  out[i] = s;
+  if (i < M)
+    for (int t = g; t < slices; t += kRedWaves) s += part[(size_t)t * M + i];
+  red[g][lane] = s;
+  __syncthreads();
+  if (g == 0 && i < M) {
+    float tot = red[0][lane];
+    for (int w = 1; w < kRedWaves; ++w) tot += red[w][lane];
+    out[i] = tot;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -480,7 +503,12 @@ void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, flo
 
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s) {
   dim3 grid((unsigned)((N + 255) / 256), B);
-  rowquad_kernel<<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
+  if (D <= 16)
+    rowquad_kernel<16><<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
+  else if (D <= 32)
+    rowquad_kernel<32><<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
+  else
+    rowquad_kernel<64><<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
 }
 
 int combine_blocks(int64_t N) { return (int)((N + 255) / 256); }
@@ -496,7 +524,7 @@ void launch_ll_reduce(const double* ll_part, int count, double inv_total, float*
 }
 
 void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s) {
-  reduce_slices_kernel<<<(unsigned)((M + 255) / 256), 256, 0, s>>>(part, slices, M, out);
+  reduce_slices_kernel<<<(unsigned)((M + 63) / 64), 64 * kRedWaves, 0, s>>>(part, slices, M, out);
 }
 
 void launch_finalize(const FinalizeArgs& a, hipStream_t s) {
