@@ -16,7 +16,7 @@ that order is what defines parity at fp32 rounding level.
 
 How each part is pinned (checked independently of this restatement):
   * logits / log-likelihood: float64 closed-form Gaussian log densities on
-    tiny inputs, and scikit-learn's GaussianMixture E-step (tests/test_oracle.py);
+    tiny inputs, and scikit-learn's GaussianMixture E-step (tests/test_oracle_pinned.py);
   * finalize, prelude clamps, jitter retry, label tie-breaking and the
     lower-bound bookkeeping: golden vectors written by the reference's own
     torch fallback (tests/golden/make_golden.py) and closed-form known answers
