@@ -28,12 +28,12 @@ int fail(int code, const std::string& msg) {
 struct Plan {
   int cov = 0, bf = 0, B = 0, D = 0, K = 0;
   int64_t N = 0;
-  int DP = 0, EP = 0, JP = 0, nk_col = 0, CW = 0, nw = 0, ktiles = 0, slices = 0, cblocks = 0;
+  int DP = 0, EP = 0, JP = 0, nk_col = 0, sq_col = 0, sq_n = 0, CW = 0, nw = 0, ktiles = 0, slices = 0, cblocks = 0;
   int64_t rows_per_slice = 0;
   int gram_slices = 0;
   int64_t gram_rows = 0;
   int chol_m = 0;
-  size_t o_whi = 0, o_wlo = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
+  size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
   size_t o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_prec = 0, o_logdet = 0, o_gram = 0, total = 0;
 };
 
@@ -69,16 +69,27 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   const int dmax = (q.cov == FULL) ? 16 : (q.cov == TIED ? 64 : 128);
   if (p->D > dmax) return fail(GMMXX_ERR_UNSUPPORTED, "D exceeds the supported maximum for this covariance type");
   q.DP = dp_for(q.D);
+  const bool sph_bf = q.bf && q.cov == SPH;          // dedicated kernel, DP >= 32
+  if (sph_bf) q.DP = std::max(q.DP, 32);
   const int S = q.DP * (q.DP + 1) / 2;
   const int E = (q.cov == SPH || q.cov == TIED) ? q.DP : (q.cov == DIAG ? 2 * q.DP : S + q.DP);
   const int J = (q.cov == SPH) ? q.DP + 3 : (q.cov == DIAG ? 2 * q.DP + 1 : (q.cov == TIED ? q.DP + 1 : q.DP + S + 1));
   q.EP = round_up(E, q.bf ? 32 : 16);
   q.JP = round_up(J, 16);
   q.nk_col = (q.cov == SPH) ? q.DP : (q.cov == DIAG ? 2 * q.DP : (q.cov == TIED ? q.DP : q.DP + S));
+  q.sq_col = q.DP + 1;
+  q.sq_n = 2;
+  if (sph_bf) {
+    // statistics row = [Σr·x | Σr·(augmented columns q_h q_m q_l q_h q_m q_h 1 1 1 0 ...)]
+    q.nk_col = q.DP + 6;
+    q.sq_col = q.DP;
+    q.sq_n = 3;
+  }
   q.CW = tile_cw(q.cov, q.DP, q.bf);
   // Waves per workgroup: a power of two (the cross-wave combine reduces lane groups).
   const int need = (q.K + q.CW - 1) / q.CW;
   q.nw = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+  if (sph_bf) q.nw = std::max(q.nw, 2);
   q.ktiles = (q.K + q.nw * q.CW - 1) / (q.nw * q.CW);
   const int64_t row_blocks = (q.N + kBN - 1) / kBN;
   const int64_t target_blocks = (kTargetWaves + q.nw - 1) / q.nw;
@@ -101,6 +112,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   const size_t BK = (size_t)q.B * q.K, BN = (size_t)q.B * q.N;
   q.o_whi = take(BK * q.EP * (q.bf ? 2 : 4));
   q.o_wlo = take(q.bf ? BK * q.EP * 2 : 0);
+  q.o_waug = take(sph_bf ? BK * 32 * 2 : 0);
   q.o_cconst = take(BK * 16);
   q.o_covs_used = take(q.cov == SPH ? BK * 4 : (q.cov == DIAG ? BK * q.D * 4 : 0));
   q.o_rowq = take(q.cov == TIED ? BN * 4 : 0);
@@ -147,6 +159,7 @@ TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
   a.rows_per_slice = pl.rows_per_slice;
   a.w_hi = at<void>(ws, pl.o_whi);
   a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
+  a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
   a.rowq = pl.cov == TIED ? at<float>(ws, pl.o_rowq) : nullptr;
   a.lse2 = at<float>(ws, pl.o_lse2);
@@ -155,6 +168,13 @@ TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
   a.part_stats = at<float>(ws, pl.o_pstats);
   a.proba = nullptr;
   return a;
+}
+
+// Launches the tile kernel of `mode` over the plan's grid.
+int run_tile(const Plan& pl, int mode, const TileArgs& t, hipStream_t s) {
+  const dim3 grid(pl.slices * pl.ktiles, pl.B);
+  if (pl.bf && pl.cov == SPH) return launch_sph_bf16(pl.DP, pl.nw, mode, t, grid, s);
+  return launch_tile(pl.cov, pl.bf, pl.DP, mode, t, grid, pl.nw, s);
 }
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
@@ -186,6 +206,7 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   a.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
   a.w_hi = at<void>(ws, pl.o_whi);
   a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
+  a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
   launch_prep(a, s);
   if (pl.cov == TIED)
@@ -197,8 +218,7 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
 int lse_pass(const Plan& pl, const void* x, void* ws, float* scores, int64_t* labels, bool with_ll,
              hipStream_t s) {
   const TileArgs t = tile_args(pl, x, ws);
-  const dim3 grid(pl.slices * pl.ktiles, pl.B);
-  if (launch_tile(pl.cov, pl.bf, pl.DP, labels ? MODE_LSE_IDX : MODE_LSE, t, grid, pl.nw, s) != 0)
+  if (run_tile(pl, labels ? MODE_LSE_IDX : MODE_LSE, t, s) != 0)
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
   CombineArgs c{};
   c.B = pl.B;
@@ -216,8 +236,7 @@ int lse_pass(const Plan& pl, const void* x, void* ws, float* scores, int64_t* la
 
 int stats_pass(const Plan& pl, const void* x, void* ws, hipStream_t s) {
   const TileArgs t = tile_args(pl, x, ws);
-  const dim3 grid(pl.slices * pl.ktiles, pl.B);
-  if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_STATS, t, grid, pl.nw, s) != 0)
+  if (run_tile(pl, MODE_STATS, t, s) != 0)
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
   launch_reduce_slices(t.part_stats, pl.slices, (int64_t)pl.B * pl.K * pl.JP, at<float>(ws, pl.o_stats), s);
   return check_hip("statistics pass");
@@ -275,7 +294,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s);
     case GMMXX_PHASE_LSE_TILE: {
       const TileArgs t = tile_args(pl, x, ws);
-      if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_LSE, t, dim3(pl.slices * pl.ktiles, pl.B), pl.nw, s) != 0)
+      if (run_tile(pl, MODE_LSE, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip("log-normaliser tile kernel");
     }
@@ -295,7 +314,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     }
     case GMMXX_PHASE_STATS_TILE: {
       const TileArgs t = tile_args(pl, x, ws);
-      if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_STATS, t, dim3(pl.slices * pl.ktiles, pl.B), pl.nw, s) != 0)
+      if (run_tile(pl, MODE_STATS, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip("statistics tile kernel");
     }
@@ -312,6 +331,8 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       f.DP = pl.DP;
       f.JP = pl.JP;
       f.nk_col = pl.nk_col;
+      f.sq_col = pl.sq_col;
+      f.sq_n = pl.sq_n;
       f.N = pl.N;
       f.reg_covar = (float)reg_covar;
       f.min_weight = (float)min_weight;
@@ -362,6 +383,8 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   u.DP = pl.DP;
   u.JP = pl.JP;
   u.nk_col = pl.nk_col;
+  u.sq_col = pl.sq_col;
+  u.sq_n = pl.sq_n;
   u.stats = at<float>(ws, pl.o_stats);
   u.nk = nk;
   u.sum_x = sum_x;
@@ -393,8 +416,7 @@ int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* 
   if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, false, s))) return rc;
   TileArgs t = tile_args(pl, x, ws);
   t.proba = proba;
-  const dim3 grid(pl.slices * pl.ktiles, pl.B);
-  if (launch_tile(pl.cov, pl.bf, pl.DP, MODE_PROBA, t, grid, pl.nw, s) != 0)
+  if (run_tile(pl, MODE_PROBA, t, s) != 0)
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
   return check_hip("predict_proba");
 }

@@ -644,8 +644,7 @@ static int launch_tile_dp(int dp, int mode, const TileArgs& a, dim3 grid, int nw
 int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s) {
   switch (cov) {
     case SPH:
-      return bf ? launch_tile_dp<SPH, __bf16>(dp, mode, a, grid, nw, s)
-                : launch_tile_dp<SPH, float>(dp, mode, a, grid, nw, s);
+      return bf ? -1 : launch_tile_dp<SPH, float>(dp, mode, a, grid, nw, s);  // bf16: em_sph_bf16.hip
     case DIAG:
       return bf ? -1 : launch_tile_dp<DIAG, float>(dp, mode, a, grid, nw, s);
     case TIED:

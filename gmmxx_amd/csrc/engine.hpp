@@ -15,7 +15,8 @@ struct TileArgs {
   int64_t rows_per_slice;      // multiple of 32
   const void* w_hi;            // [B][K][EP] E-step operand (bf16 hi or fp32)
   const void* w_lo;            // [B][K][EP] bf16 lo part (bf16 path only)
-  const float4* cconst;        // [B][K] (colq, a, b, 0): l2 = a*max(sc*S + rowq + colq, 0) + b
+  const void* w_aug;           // [B][K][32] bf16 augmented constants (spherical bf16 path)
+  const float4* cconst;        // [B][K] (A, C, 0, 0): l2 = A*(rowq - 2S) + C (spherical, tied) or A*S + C
   const float* rowq;           // [B][N] tied: xᵀPx
   const float* lse2;           // [B][N] log2-domain log-normaliser (STATS / PROBA)
   float* part_ms;              // [ktiles][B][N][2] (max, scaled sum)   (LSE)
@@ -26,5 +27,7 @@ struct TileArgs {
 
 int tile_cw(int cov, int dp, int bf);
 int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s);
+// Spherical bf16 kernel (em_sph_bf16.hip): dp in {32, 64, 128}, nw in {2, 4, 8}.
+int launch_sph_bf16(int dp, int nw, int mode, const TileArgs& a, dim3 grid, hipStream_t s);
 
 }  // namespace gx

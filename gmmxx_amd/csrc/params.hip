@@ -74,11 +74,28 @@ __global__ void prep_kernel(PrepArgs a) {
     a.covs_used[bk] = var;
     float msq = 0.f;
     for (int d = 0; d < D; ++d) msq = fmaf(mu[d], mu[d], msq);
-    for (int e = 0; e < EP; ++e) put(e, e < D ? mu[e] : 0.f);
     const float lognorm = (float)D * ((float)kLog2Pi + logf(var));
     colq = msq;
     ca = -0.5f * kLog2e / var;
     cb = (lw - 0.5f * lognorm) * kLog2e;
+    if (a.bf) {
+      // bf16 kernel: W' = -2·ca·μ (hi/lo) and the augmented constants
+      // [A_h A_h A_h A_m A_m A_l C_h C_m | C_l 0 ...] with A = ca, C = ca·‖μ‖² + cb.
+      for (int e = 0; e < EP; ++e) put_bf(e, e < D ? -2.f * ca * mu[e] : 0.f);
+      __bf16* aug = reinterpret_cast<__bf16*>(a.w_aug) + bk * 32;
+      const float cy = fmaf(ca, colq, cb);
+      const __bf16 ah = (__bf16)ca;
+      const __bf16 am = (__bf16)(ca - (float)ah);
+      const __bf16 al = (__bf16)(ca - (float)ah - (float)am);
+      const __bf16 ch = (__bf16)cy;
+      const __bf16 cm = (__bf16)(cy - (float)ch);
+      const __bf16 cl = (__bf16)(cy - (float)ch - (float)cm);
+      const __bf16 zero = (__bf16)0.f;
+      const __bf16 vals[9] = {ah, ah, ah, am, am, al, ch, cm, cl};
+      for (int e = 0; e < 32; ++e) aug[e] = e < 9 ? vals[e] : zero;
+    } else {
+      for (int e = 0; e < EP; ++e) put(e, e < D ? mu[e] : 0.f);
+    }
   } else if (a.cov == DIAG) {
     // torch_fallback.py:2491-2494
     const float* vr = a.covs + bk * D;
@@ -364,7 +381,8 @@ __global__ void finalize_kernel(FinalizeArgs a) {
     msq = fmaf(m, m, msq);
   }
   if (a.cov == SPH) {
-    const float sq = sk[a.nk_col + 1] + sk[a.nk_col + 2];
+    float sq = 0.f;
+    for (int i = 0; i < a.sq_n; ++i) sq += sk[a.sq_col + i];
     float v = fmaxf(sq - nk * msq, 0.f) / (nk_safe * (float)D);
     v = fmaxf(v, a.reg_covar);
     a.covs[bk] = active ? v : a.covs_used[bk];
@@ -432,7 +450,9 @@ __global__ void unpack_stats_kernel(UnpackArgs a) {
   for (int d = 0; d < D; ++d) a.sum_x[bk * D + d] = sk[d];
   if (!a.sum_q) return;
   if (a.cov == SPH) {
-    a.sum_q[bk] = sk[a.nk_col + 1] + sk[a.nk_col + 2];
+    float sq = 0.f;
+    for (int i = 0; i < a.sq_n; ++i) sq += sk[a.sq_col + i];
+    a.sum_q[bk] = sq;
   } else if (a.cov == DIAG) {
     for (int d = 0; d < D; ++d) a.sum_q[bk * D + d] = sk[DP + d];
   } else if (a.cov == FULL) {

@@ -18,6 +18,7 @@ struct PrepArgs {
   float* covs_used;        // spherical/diag: the (clamped) variances this iteration used
   void* w_hi;              // [B][K][EP]
   void* w_lo;              // [B][K][EP] (bf16 path)
+  void* w_aug;             // [B][K][32] (spherical bf16 path)
   float4* cconst;          // [B][K]
 };
 
@@ -34,6 +35,7 @@ struct CombineArgs {
 
 struct FinalizeArgs {
   int cov, B, K, D, DP, JP, nk_col;
+  int sq_col, sq_n;        // spherical: Σ r‖x‖² = Σ_{i < sq_n} stats[sq_col + i]
   int64_t N;
   float reg_covar, min_weight;
   const float* stats;      // [B][K][JP]
@@ -46,6 +48,7 @@ struct FinalizeArgs {
 
 struct UnpackArgs {
   int cov, K, D, DP, JP, nk_col;
+  int sq_col, sq_n;
   const float* stats;
   float* nk;
   float* sum_x;
