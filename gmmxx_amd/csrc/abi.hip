@@ -34,7 +34,7 @@ struct Plan {
   int64_t gram_rows = 0;
   int chol_m = 0;
   size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
-  size_t o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_prec = 0, o_logdet = 0, o_gram = 0, total = 0;
+  size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_prec = 0, o_logdet = 0, o_gram = 0, total = 0;
 };
 
 constexpr int kTargetWaves = 4096;      // 16 waves per CU on 256 CUs
@@ -117,6 +117,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_covs_used = take(q.cov == SPH ? BK * 4 : (q.cov == DIAG ? BK * q.D * 4 : 0));
   q.o_rowq = take(q.cov == TIED ? BN * 4 : 0);
   q.o_lse2 = take(BN * 4);
+  q.o_rowaux = take(sph_bf && q.DP >= 128 ? BN * 16 : 0);
   q.o_pms = take((size_t)q.ktiles * BN * 8);
   q.o_pidx = take((size_t)q.ktiles * BN * 4);
   q.o_pstats = take((size_t)q.slices * BK * q.JP * 4);
@@ -163,6 +164,7 @@ TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
   a.cconst = at<float4>(ws, pl.o_cconst);
   a.rowq = pl.cov == TIED ? at<float>(ws, pl.o_rowq) : nullptr;
   a.lse2 = at<float>(ws, pl.o_lse2);
+  a.rowaux = (pl.bf && pl.cov == SPH && pl.DP >= 128) ? at<uint4>(ws, pl.o_rowaux) : nullptr;
   a.part_ms = at<float>(ws, pl.o_pms);
   a.part_idx = at<int>(ws, pl.o_pidx);
   a.part_stats = at<float>(ws, pl.o_pstats);

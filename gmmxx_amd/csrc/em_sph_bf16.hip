@@ -102,14 +102,17 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
   constexpr bool STATS = MODE == MODE_STATS;
   constexpr int CW = 32, CT = 2;                 // components per wave, 16-wide tiles
   constexpr int ECH = DP / 32;                   // x chunks of the E-GEMM
-  // Staged row stride (bf16).  With s = XS/2 dwords, s/4 odd keeps the b128 E-GEMM
-  // reads (16 consecutive rows, one column) conflict free, and {0, s, 2s, 3s} + [0, 8)
-  // disjoint mod 64 does the same for the transposing ψ reads (4 rows x 32 bytes):
-  // s = 36, 52, 92 dwords.
-  constexpr int XS = DP <= 32 ? 72 : (DP <= 64 ? 104 : 184);
+  // Staged row stride (bf16): s = XS/2 dwords ≡ 8 or 24 (mod 32) measured fastest for
+  // both the b128 E-GEMM reads (16 consecutive rows, one column) and the
+  // transposing ψ reads (4 rows x 32 bytes); s = 40, 56, 88.
+  constexpr int XS = DP <= 32 ? 80 : (DP <= 64 ? 112 : 176);
   static_assert(DP + kAug <= XS, "row does not fit the staging stride");
   constexpr int JT = DP / 16 + 1;                // ψ = the staged row: [x | augmented columns 0..15]
   constexpr int JP = 16 * JT;                    // statistics row length
+  // Wide rows: the statistics/proba passes read the augmented chunk the
+  // log-normaliser pass stored (16 bytes per row) instead of recomputing ‖x‖²;
+  // narrow rows are HBM bound, where the extra bytes cost more than the VALU.
+  constexpr bool AUX = DP >= 128;
   constexpr int CPR = DP / 8;                    // 16-byte chunks per row
   constexpr int NCH = kBN * CPR;                 // chunks per row block
   constexpr int NTHR = 64 * NW;
@@ -171,6 +174,14 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
       for (int jt = 0; jt < JT; ++jt) acc[ct][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Constant augmented columns 8..31 of every staged row: [1 0 0 ...].
+  for (int i = tid; i < NB * kBN * 3; i += NTHR) {
+    const int row = i / 3, ch = 1 + i % 3;
+    const uint4 w = make_uint4(ch == 1 ? pack2((__bf16)1.f, (__bf16)0.f) : 0u, 0u, 0u, 0u);
+    *reinterpret_cast<uint4*>(xs + row * XS + DP + 8 * ch) = w;
+  }
+  __syncthreads();
+
   const __bf16* xb = reinterpret_cast<const __bf16*>(a.x) + (size_t)b * N * D;
 
   // ---- row-block loader: 16-byte chunks, PF per thread ----
@@ -190,15 +201,30 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
     for (int j = 0; j < 8; ++j) t.e[j] = (cc + j < D) ? xb[(size_t)n * D + cc + j] : (__bf16)0.f;
     return t.u;
   };
+  // Per-row extras fetched with the x chunks by each row's first chunk-lane:
+  // the statistics / proba passes take the augmented chunk written by the
+  // log-normaliser pass (rowaux) and the row's lse2.
+  uint4 pa[PF];
+  float pl[PF];
   auto fetch = [&](int64_t n0) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int c = tid + i * NTHR;
-      if (NCH % NTHR == 0 || c < NCH) pf[i] = load_chunk(c, n0);
+      if (NCH % NTHR == 0 || c < NCH) {
+        pf[i] = load_chunk(c, n0);
+        if constexpr (!LSE) {
+          const int64_t n = n0 + c / CPR;
+          const size_t o = (size_t)b * N + (n < rend ? n : rend - 1);
+          if (c % CPR == 0) {
+            if constexpr (AUX) pa[i] = a.rowaux[o];
+            pl[i] = (n < rend) ? a.lse2[o] : kHuge;
+          }
+        }
+      }
     }
   };
-  // Stages the prefetched block into buffer `buf`: x, and the augmented chunk
-  // (written by the first four chunk-lanes of each row).
+  // Stages the prefetched block into buffer `buf`: x, and columns 0..7 of the
+  // augmented chunk (columns 8..31 are constant and written once).
   auto stash = [&](int buf, int64_t n0) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
@@ -208,26 +234,31 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
         const uint4 raw = pf[i];
         __bf16* row = xs + buf * kBN * XS + r * XS;
         *reinterpret_cast<uint4*>(row + 8 * cc) = raw;
-        union { uint4 u; __bf16 e[8]; } t;
-        t.u = raw;
-        float q = 0.f;
+        if constexpr (LSE || !AUX) {
+          union { uint4 u; __bf16 e[8]; } t;
+          t.u = raw;
+          float q = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = (float)t.e[j];
-          q = fmaf(v, v, q);
+          for (int j = 0; j < 8; ++j) {
+            const float v = (float)t.e[j];
+            q = fmaf(v, v, q);
+          }
+          q = group_sum<CPR>(q);
+          if (cc == 0) {
+            __bf16 h, m, l;
+            split3(q, h, m, l);
+            const uint4 w = make_uint4(pack2(h, m), pack2(l, h), pack2(m, h), pack2((__bf16)1.f, (__bf16)1.f));
+            *reinterpret_cast<uint4*>(row + DP) = w;
+            if constexpr (LSE && AUX) {
+              const int64_t n = n0 + r;
+              if (n < rend) a.rowaux[(size_t)b * N + n] = w;
+            }
+          }
+        } else {
+          if (cc == 0) *reinterpret_cast<uint4*>(row + DP) = pa[i];
         }
-        q = group_sum<CPR>(q);
-        // Augmented chunk: every lane builds it, the first four chunk-lanes of the row store it.
-        __bf16 h, m, l;
-        split3(q, h, m, l);
-        const uint32_t one2 = pack2((__bf16)1.f, (__bf16)1.f), one0 = pack2((__bf16)1.f, (__bf16)0.f);
-        const uint4 w = make_uint4(cc == 0 ? pack2(h, m) : (cc == 1 ? one0 : 0u), cc == 0 ? pack2(l, h) : 0u,
-                                   cc == 0 ? pack2(m, h) : 0u, cc == 0 ? one2 : 0u);
-        if (cc < 4) *reinterpret_cast<uint4*>(row + DP + 8 * cc) = w;
         if constexpr (!LSE) {
-          const int64_t n = n0 + r;
-          const float lv = a.lse2[(size_t)b * N + (n < rend ? n : rend - 1)];
-          if (cc == 0) lse_s[buf * kBN + r] = (n < rend) ? lv : kHuge;
+          if (cc == 0) lse_s[buf * kBN + r] = pl[i];
         }
       }
     }

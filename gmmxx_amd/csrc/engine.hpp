@@ -19,6 +19,7 @@ struct TileArgs {
   const float4* cconst;        // [B][K] (A, C, 0, 0): l2 = A*(rowq - 2S) + C (spherical, tied) or A*S + C
   const float* rowq;           // [B][N] tied: xᵀPx
   const float* lse2;           // [B][N] log2-domain log-normaliser (STATS / PROBA)
+  uint4* rowaux;               // [B][N] spherical bf16: augmented row chunk (written by LSE)
   float* part_ms;              // [ktiles][B][N][2] (max, scaled sum)   (LSE)
   int* part_idx;               // [ktiles][B][N] first argmax           (LSE)
   float* part_stats;           // [slices][B][K][JP]                    (STATS)
