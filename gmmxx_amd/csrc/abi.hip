@@ -29,6 +29,7 @@ struct Plan {
   int cov = 0, bf = 0, B = 0, D = 0, K = 0;
   int64_t N = 0;
   int DP = 0, EP = 0, JP = 0, nk_col = 0, sq_col = 0, sq_n = 0, CW = 0, nw = 0, ktiles = 0, slices = 0, cblocks = 0;
+  int lnw = 0, lktiles = 0;  // waves / component tiles of the plain log-normaliser pass (MODE_LSE)
   int64_t rows_per_slice = 0;
   int gram_slices = 0;
   int64_t gram_rows = 0;
@@ -89,8 +90,15 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   // Waves per workgroup: a power of two (the cross-wave combine reduces lane groups).
   const int need = (q.K + q.CW - 1) / q.CW;
   q.nw = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
-  if (sph_bf) q.nw = std::max(q.nw, 2);
+  // bf16 spherical: at least 2 waves; at D = 128 always 8 (the 2- and 4-wave
+  // variants prefetch several chunks per thread and run out of registers).
+  if (sph_bf) q.nw = q.DP >= 128 ? 8 : std::max(q.nw, 2);
   q.ktiles = (q.K + q.nw * q.CW - 1) / (q.nw * q.CW);
+  // The bf16 D = 128 log-normaliser pass runs 16-wave workgroups (512 components)
+  // when K needs more than one 8-wave tile: the staged rows are shared by twice
+  // the waves and four waves per SIMD hide each other's VALU work.
+  q.lnw = (sph_bf && q.DP == 128 && q.K > 8 * q.CW) ? 16 : q.nw;
+  q.lktiles = (q.K + q.lnw * q.CW - 1) / (q.lnw * q.CW);
   const int64_t row_blocks = (q.N + kBN - 1) / kBN;
   const int64_t target_blocks = (kTargetWaves + q.nw - 1) / q.nw;
   int64_t slices = std::max<int64_t>(1, (target_blocks + (int64_t)q.ktiles * q.B - 1) / ((int64_t)q.ktiles * q.B));
@@ -118,7 +126,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_rowq = take(q.cov == TIED ? BN * 4 : 0);
   q.o_lse2 = take(BN * 4);
   q.o_rowaux = take(sph_bf && q.DP >= 128 ? BN * 16 : 0);
-  q.o_pms = take((size_t)q.ktiles * BN * 8);
+  q.o_pms = take((size_t)std::max(q.ktiles, q.lktiles) * BN * 8);
   q.o_pidx = take((size_t)q.ktiles * BN * 4);
   q.o_pstats = take((size_t)q.slices * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
@@ -174,8 +182,12 @@ TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
 
 // Launches the tile kernel of `mode` over the plan's grid.
 int run_tile(const Plan& pl, int mode, const TileArgs& t, hipStream_t s) {
+  if (pl.bf && pl.cov == SPH) {
+    TileArgs u = t;
+    u.ktiles = mode == MODE_LSE ? pl.lktiles : pl.ktiles;
+    return launch_sph_bf16(pl.DP, mode == MODE_LSE ? pl.lnw : pl.nw, mode, u, dim3(pl.slices * u.ktiles, pl.B), s);
+  }
   const dim3 grid(pl.slices * pl.ktiles, pl.B);
-  if (pl.bf && pl.cov == SPH) return launch_sph_bf16(pl.DP, pl.nw, mode, t, grid, s);
   return launch_tile(pl.cov, pl.bf, pl.DP, mode, t, grid, pl.nw, s);
 }
 
@@ -224,7 +236,7 @@ int lse_pass(const Plan& pl, const void* x, void* ws, float* scores, int64_t* la
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
   CombineArgs c{};
   c.B = pl.B;
-  c.ktiles = pl.ktiles;
+  c.ktiles = labels ? pl.ktiles : pl.lktiles;
   c.N = pl.N;
   c.part_ms = t.part_ms;
   c.part_idx = t.part_idx;
@@ -303,7 +315,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     case GMMXX_PHASE_COMBINE: {
       CombineArgs c{};
       c.B = pl.B;
-      c.ktiles = pl.ktiles;
+      c.ktiles = pl.lktiles;
       c.N = pl.N;
       c.part_ms = at<float>(ws, pl.o_pms);
       c.part_idx = at<int>(ws, pl.o_pidx);

@@ -43,7 +43,7 @@ __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-// Sum / max over groups of G consecutive lanes (G <= 16), result in every lane.
+// Sum / max / min over groups of G consecutive lanes (G <= 16), result in every lane.
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
   if constexpr (G >= 2) v += dpp<0xB1>(v);    // lane ^ 1
@@ -57,6 +57,7 @@ __device__ __forceinline__ float group_max(float v) {
   if constexpr (G >= 2) v = fmaxf(v, dpp<0xB1>(v));
   if constexpr (G >= 4) v = fmaxf(v, dpp<0x4E>(v));
   if constexpr (G >= 8) v = fmaxf(v, dpp<0x141>(v));
+  if constexpr (G >= 16) v = fmaxf(v, dpp<0x140>(v));
   return v;
 }
 template <int G>
@@ -64,6 +65,7 @@ __device__ __forceinline__ int group_min_i(int v) {
   if constexpr (G >= 2) v = min(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
   if constexpr (G >= 4) v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
   if constexpr (G >= 8) v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+  if constexpr (G >= 16) v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
   return v;
 }
 
@@ -143,7 +145,13 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
   const int64_t rend = (rbeg + a.rows_per_slice < N) ? rbeg + a.rows_per_slice : N;
 
   // ---- resident component operands: lane (li, g) holds component kbase+16ct+li, k-group g ----
-  bf16x8 whi[CT][ECH], wlo[CT][ECH], waug[CT];
+  // 16-wave workgroups keep the augmented constants in LDS (row stride 40
+  // bf16: conflict-free b128 reads, read once per block) to stay within 128
+  // VGPRs; otherwise they are resident in VGPRs like the x·W' operands.
+  constexpr bool AUG_LDS = NW >= 16;
+  constexpr int AS = kAug + 8;
+  __shared__ __align__(16) __bf16 augc[AUG_LDS ? NW * CW * AS : 8];
+  bf16x8 whi[CT][ECH], wlo[CT][ECH], waug[AUG_LDS ? 1 : CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int kk = kbase + 16 * ct + li;
@@ -154,14 +162,18 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
         whi[ct][ec] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_hi) + bk * DP + 32 * ec + 8 * g);
         wlo[ct][ec] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_lo) + bk * DP + 32 * ec + 8 * g);
       }
-      waug[ct] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * g);
+      const bf16x8 v = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * g);
+      if constexpr (AUG_LDS) *reinterpret_cast<bf16x8*>(&augc[(wave * CW + 16 * ct + li) * AS + 8 * g]) = v;
+      else waug[ct] = v;
     } else {
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
 #pragma unroll
         for (int ec = 0; ec < ECH; ++ec) { whi[ct][ec][s] = (__bf16)0.f; wlo[ct][ec][s] = (__bf16)0.f; }
         // padding component: C = -1e30 (column 6)
-        waug[ct][s] = (__bf16)((8 * g + s) == 6 ? -kHuge : 0.f);
+        const __bf16 v = (__bf16)((8 * g + s) == 6 ? -kHuge : 0.f);
+        if constexpr (AUG_LDS) augc[(wave * CW + 16 * ct + li) * AS + 8 * g + s] = v;
+        else waug[ct][s] = v;
       }
     }
   }
@@ -290,6 +302,10 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
   // rows 16h + 4g + v of component li).  Both read consecutive rows per lane
   // group, which the row stride keeps free of bank conflicts.
   struct Acc { f32x4 t[CT][2]; };
+  auto wa = [&](int ct) -> bf16x8 {
+    if constexpr (AUG_LDS) return ld16<bf16x8>(&augc[(wave * CW + 16 * ct + li) * AS + 8 * g]);
+    else return waug[ct];
+  };
   struct Frag { bf16x8 x[ECH + 1][2]; };          // [chunk (last = augmented)][row tile]
   auto load_frags = [&](int bx) -> Frag {
     Frag F;
@@ -310,7 +326,7 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) A.t[ct][h] = mm(waug[ct], F.x[ECH][h], f32x4{0.f, 0.f, 0.f, 0.f});
+      for (int h = 0; h < 2; ++h) A.t[ct][h] = mm(wa(ct), F.x[ECH][h], f32x4{0.f, 0.f, 0.f, 0.f});
     // consecutive MFMAs write different accumulators (no back-to-back dependency)
 #pragma unroll
     for (int ec = 0; ec < ECH; ++ec) {
@@ -322,6 +338,36 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
         for (int h = 0; h < 2; ++h) A.t[ct][h] = mm(wlo[ct][ec], F.x[ec][h], A.t[ct][h]);
+    }
+    return A;
+  };
+
+  // E-GEMM loading one k-chunk of operands at a time (fewer live registers).
+  auto egemm_direct = [&](int bx) -> Acc {
+    Acc A;
+    const __bf16* xr = xs + bx * kBN * XS + li * XS + 8 * g;
+    auto mm = [&](const bf16x8& w, const bf16x8& x, const f32x4& c) {
+      return LSE ? mfma_bf16(w, x, c) : mfma_bf16(x, w, c);
+    };
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bf16x8 xa = ld16<bf16x8>(xr + 16 * h * XS + DP);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) A.t[ct][h] = mm(wa(ct), xa, f32x4{0.f, 0.f, 0.f, 0.f});
+    }
+#pragma unroll
+    for (int ec = 0; ec < ECH; ++ec) {
+      bf16x8 xv[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xv[h] = ld16<bf16x8>(xr + 16 * h * XS + 32 * ec);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) A.t[ct][h] = mm(whi[ct][ec], xv[h], A.t[ct][h]);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) A.t[ct][h] = mm(wlo[ct][ec], xv[h], A.t[ct][h]);
     }
     return A;
   };
@@ -439,8 +485,12 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
   if (nblk > 0) { fetch(rbeg); stash(0, rbeg); }
   if (nblk > 1) { fetch(rbeg + kBN); stash(1, rbeg + kBN); }
   __syncthreads();
+  // With 16 waves there are no registers for a second accumulator set: the
+  // E-GEMM and epilogue of a block run back to back, and the other waves of
+  // the SIMD fill the gaps.
+  constexpr bool PIPE = NW < 16;
   Acc cur;
-  if (nblk > 0) cur = egemm(load_frags(0));
+  if (PIPE && nblk > 0) cur = egemm(load_frags(0));
   int bx = 0;
   for (int ib = 0; ib < nblk; ++ib) {
     const int pb = ib & 1;
@@ -454,10 +504,14 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
     // stale in-bounds buffer and discards the result).
     f32x4 ls0, ls1;
     load_lse(bx, ls0, ls1);
-    const Acc nxt = egemm(load_frags(b1));
-    epilogue(cur, ls0, ls1, bx, pb, n0);
-    interleave();
-    cur = nxt;
+    if constexpr (PIPE) {
+      const Acc nxt = egemm(load_frags(b1));
+      epilogue(cur, ls0, ls1, bx, pb, n0);
+      interleave();
+      cur = nxt;
+    } else {
+      epilogue(egemm_direct(bx), ls0, ls1, bx, pb, n0);
+    }
     if (ahead) stash(b2, n0 + 2 * kBN);
     __syncthreads();
     bx = b1;
@@ -495,9 +549,14 @@ static int launch_sph_bf16_nw(int mode, const TileArgs& a, dim3 grid, hipStream_
 template <int DP>
 static int launch_sph_bf16_dp(int nw, int mode, const TileArgs& a, dim3 grid, hipStream_t s) {
   switch (nw) {
-    case 2: return launch_sph_bf16_nw<DP, 2>(mode, a, grid, s);
-    case 4: return launch_sph_bf16_nw<DP, 4>(mode, a, grid, s);
+    case 2: if constexpr (DP < 128) return launch_sph_bf16_nw<DP, 2>(mode, a, grid, s); else return -1;
+    case 4: if constexpr (DP < 128) return launch_sph_bf16_nw<DP, 4>(mode, a, grid, s); else return -1;
     case 8: return launch_sph_bf16_nw<DP, 8>(mode, a, grid, s);
+    case 16:  // plain log-normaliser pass at D = 128 only
+      if constexpr (DP == 128) {
+        if (mode == MODE_LSE) { sph_bf16_kernel<DP, 16, MODE_LSE><<<grid, dim3(1024), 0, s>>>(a); return 0; }
+      }
+      return -1;
     default: return -1;
   }
 }

@@ -28,7 +28,8 @@ struct TileArgs {
 
 int tile_cw(int cov, int dp, int bf);
 int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s);
-// Spherical bf16 kernel (em_sph_bf16.hip): dp in {32, 64, 128}, nw in {2, 4, 8}.
+// Spherical bf16 kernel (em_sph_bf16.hip): dp in {32, 64} with nw in {2, 4, 8};
+// dp 128 with nw 8 (and 16 for MODE_LSE).
 int launch_sph_bf16(int dp, int nw, int mode, const TileArgs& a, dim3 grid, hipStream_t s);
 
 }  // namespace gx
