@@ -207,7 +207,7 @@ def make_data(name, device):
 def _traffic_from_profile(name, phase):
     """HBM bytes per launch of (config, phase) from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary, or None."""
-    path = os.path.join(ROOT, "profiles", f"em_tile_{name}_hbm_traffic.txt")
+    path = os.path.join(ROOT, "profiles", f"tile_{name}_hbm_traffic.txt")
     if not os.path.exists(path):
         return None
     vals = {}
