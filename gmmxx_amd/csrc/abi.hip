@@ -30,6 +30,9 @@ struct Plan {
   int64_t N = 0;
   int DP = 0, EP = 0, JP = 0, nk_col = 0, sq_col = 0, sq_n = 0, CW = 0, nw = 0, ktiles = 0, slices = 0, cblocks = 0;
   int lnw = 0, lktiles = 0;  // waves / component tiles of the plain log-normaliser pass (MODE_LSE)
+  bool fused = false;        // EM iteration as one fused pass (small K; em_fused.hip)
+  int fslices = 0;           // fused: one wave per row slice
+  int64_t frows = 0;
   int64_t rows_per_slice = 0;
   int gram_slices = 0;
   int64_t gram_rows = 0;
@@ -106,6 +109,15 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.rows_per_slice = ((q.N + slices - 1) / slices + kBN - 1) / kBN * kBN;
   q.slices = (int)((q.N + q.rows_per_slice - 1) / q.rows_per_slice);
   q.cblocks = combine_blocks(q.N);
+  // Fused single pass: spherical bf16 with every component in one wave's registers.
+  q.fused = sph_bf && q.DP <= 64 && q.K <= 64;
+  if (q.fused) {
+    // ~6144 waves: two full rounds at three resident waves per SIMD.
+    int64_t fs = std::max<int64_t>(1, (6144 + q.B - 1) / q.B);
+    fs = std::min(fs, std::max<int64_t>(1, row_blocks / kMinBlocksPerSlice));
+    q.frows = ((q.N + fs - 1) / fs + kBN - 1) / kBN * kBN;
+    q.fslices = (int)((q.N + q.frows - 1) / q.frows);
+  }
   int64_t gs = std::min<int64_t>(64, row_blocks);
   q.gram_rows = ((q.N + gs - 1) / gs + kBN - 1) / kBN * kBN;
   q.gram_slices = (int)((q.N + q.gram_rows - 1) / q.gram_rows);
@@ -128,9 +140,9 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_rowaux = take(sph_bf && q.DP >= 128 ? BN * 16 : 0);
   q.o_pms = take((size_t)std::max(q.ktiles, q.lktiles) * BN * 8);
   q.o_pidx = take((size_t)q.ktiles * BN * 4);
-  q.o_pstats = take((size_t)q.slices * BK * q.JP * 4);
+  q.o_pstats = take((size_t)std::max(q.slices, q.fslices) * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
-  q.o_ll = take((size_t)q.B * q.cblocks * 8);
+  q.o_ll = take((size_t)q.B * std::max(q.cblocks, q.fslices) * 8);
   q.o_first = take((size_t)q.chol_m * 4);
   q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
   q.o_logdet = take((size_t)q.chol_m * 4);
@@ -177,6 +189,8 @@ TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
   a.part_idx = at<int>(ws, pl.o_pidx);
   a.part_stats = at<float>(ws, pl.o_pstats);
   a.proba = nullptr;
+  a.nslices = pl.fslices;
+  a.ll_part = at<double>(ws, pl.o_ll);
   return a;
 }
 
@@ -190,6 +204,19 @@ int run_tile(const Plan& pl, int mode, const TileArgs& t, hipStream_t s) {
   const dim3 grid(pl.slices * pl.ktiles, pl.B);
   return launch_tile(pl.cov, pl.bf, pl.DP, mode, t, grid, pl.nw, s);
 }
+
+// Fused pass: partial statistics per row slice and partial log-likelihoods.
+int run_fused(const Plan& pl, const TileArgs& t, hipStream_t s) {
+  TileArgs u = t;
+  u.rows_per_slice = pl.frows;
+  return launch_sph_bf16_fused(pl.DP, pl.K, u, pl.fslices, s);
+}
+int stat_slices(const Plan& pl) { return pl.fused ? pl.fslices : pl.slices; }
+// The tile-partial buffer is free once the statistics are being reduced: it is
+// the scratch of the grouped slice reduction.
+float* red_tmp(const Plan& pl, void* ws) { return at<float>(ws, pl.o_pms); }
+int64_t red_tmp_floats(const Plan& pl) { return (int64_t)std::max(pl.ktiles, pl.lktiles) * pl.B * pl.N * 2; }
+int ll_parts(const Plan& pl) { return pl.B * (pl.fused ? pl.fslices : pl.cblocks); }
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
 int prepare(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights,
@@ -252,7 +279,8 @@ int stats_pass(const Plan& pl, const void* x, void* ws, hipStream_t s) {
   const TileArgs t = tile_args(pl, x, ws);
   if (run_tile(pl, MODE_STATS, t, s) != 0)
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
-  launch_reduce_slices(t.part_stats, pl.slices, (int64_t)pl.B * pl.K * pl.JP, at<float>(ws, pl.o_stats), s);
+  launch_reduce_slices(t.part_stats, pl.slices, (int64_t)pl.B * pl.K * pl.JP, at<float>(ws, pl.o_stats), s,
+                       red_tmp(pl, ws), red_tmp_floats(pl));
   return check_hip("statistics pass");
 }
 
@@ -308,11 +336,16 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s);
     case GMMXX_PHASE_LSE_TILE: {
       const TileArgs t = tile_args(pl, x, ws);
-      if (run_tile(pl, MODE_LSE, t, s) != 0)
+      if ((pl.fused ? run_fused(pl, t, s) : run_tile(pl, MODE_LSE, t, s)) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
-      return check_hip("log-normaliser tile kernel");
+      return check_hip(pl.fused ? "fused tile kernel" : "log-normaliser tile kernel");
     }
     case GMMXX_PHASE_COMBINE: {
+      if (pl.fused) {  // the fused pass already produced per-slice log-likelihoods
+        launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0 / ((double)pl.B * (double)pl.N),
+                         lower_bound, s);
+        return check_hip("log-likelihood reduction");
+      }
       CombineArgs c{};
       c.B = pl.B;
       c.ktiles = pl.lktiles;
@@ -327,14 +360,15 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip("combine");
     }
     case GMMXX_PHASE_STATS_TILE: {
+      if (pl.fused) return GMMXX_OK;  // statistics came out of the fused pass
       const TileArgs t = tile_args(pl, x, ws);
       if (run_tile(pl, MODE_STATS, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip("statistics tile kernel");
     }
     case GMMXX_PHASE_REDUCE:
-      launch_reduce_slices(at<float>(ws, pl.o_pstats), pl.slices, (int64_t)pl.B * pl.K * pl.JP,
-                           at<float>(ws, pl.o_stats), s);
+      launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
+                           at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
       return check_hip("statistics reduction");
     case GMMXX_PHASE_FINALIZE: {
       FinalizeArgs f{};
@@ -387,9 +421,17 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
-  if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, true, s))) return rc;
-  launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0, ll_sum, s);
-  if ((rc = stats_pass(pl, x, ws, s))) return rc;
+  if (pl.fused) {
+    if (run_fused(pl, tile_args(pl, x, ws), s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
+    launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0, ll_sum, s);
+    launch_reduce_slices(at<float>(ws, pl.o_pstats), pl.fslices, (int64_t)pl.B * pl.K * pl.JP,
+                         at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
+    if ((rc = check_hip("fused statistics pass"))) return rc;
+  } else {
+    if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, true, s))) return rc;
+    launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0, ll_sum, s);
+    if ((rc = stats_pass(pl, x, ws, s))) return rc;
+  }
   UnpackArgs u{};
   u.cov = pl.cov;
   u.K = pl.K;

@@ -24,6 +24,8 @@ struct TileArgs {
   int* part_idx;               // [ktiles][B][N] first argmax           (LSE)
   float* part_stats;           // [slices][B][K][JP]                    (STATS)
   float* proba;                // [B][N][K]                             (PROBA)
+  int nslices;                 // row slices of the fused kernel
+  double* ll_part;             // [B][nslices] partial log-likelihood   (fused)
 };
 
 int tile_cw(int cov, int dp, int bf);
@@ -31,5 +33,8 @@ int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid,
 // Spherical bf16 kernel (em_sph_bf16.hip): dp in {32, 64} with nw in {2, 4, 8};
 // dp 128 with nw 8 (and 16 for MODE_LSE).
 int launch_sph_bf16(int dp, int nw, int mode, const TileArgs& a, dim3 grid, hipStream_t s);
+// Fused single-pass kernel (em_fused.hip): spherical bf16, dp in {32, 64}, K <= 64;
+// one wave per row slice, `slices` slices.
+int launch_sph_bf16_fused(int dp, int k, const TileArgs& a, int slices, hipStream_t s);
 
 }  // namespace gx

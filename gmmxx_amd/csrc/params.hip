@@ -6,6 +6,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "params.hpp"
 
@@ -334,11 +336,15 @@ __global__ void ll_reduce_kernel(const double* ll_part, int count, double inv_to
 // 64 outputs; wave g sums slices g, g + 16, ...; the 16 wave sums are then
 // added in wave order.
 constexpr int kRedWaves = 16;
+// blockIdx.y selects a group of `per` consecutive slices (written to out + y*M).
 __global__ __launch_bounds__(64 * kRedWaves) void reduce_slices_kernel(const float* part, int slices, int64_t M,
-                                                                       float* out) {
+                                                                       float* out, int per) {
   __shared__ float red[kRedWaves][64];
   const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  part += (size_t)blockIdx.y * per * M;
+  out += (size_t)blockIdx.y * M;
+  slices = min(per, slices - (int)blockIdx.y * per);
   float s = 0.f;
   if (i < M)
     for (int t = g; t < slices; t += kRedWaves) s += part[(size_t)t * M + i];
@@ -543,8 +549,23 @@ void launch_ll_reduce(const double* ll_part, int count, double inv_total, float*
   ll_reduce_kernel<<<1, 1024, 0, s>>>(ll_part, count, inv_total, out);
 }
 
-void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s) {
-  reduce_slices_kernel<<<(unsigned)((M + 63) / 64), 64 * kRedWaves, 0, s>>>(part, slices, M, out);
+void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s, float* tmp,
+                          int64_t tmp_floats) {
+  // Many slices over few outputs: first sum groups of slices in parallel into
+  // tmp (fixed grouping, so the result stays deterministic), then the groups.
+  const int64_t blocks = (M + 63) / 64;
+  int groups = 1;
+  while (groups < 64 && blocks * groups < 512 && slices / (2 * groups) >= 4 * kRedWaves &&
+         (int64_t)(2 * groups) * M <= tmp_floats)
+    groups *= 2;
+  if (groups == 1 || !tmp) {
+    reduce_slices_kernel<<<(unsigned)blocks, 64 * kRedWaves, 0, s>>>(part, slices, M, out, slices);
+    return;
+  }
+  const int per = (slices + groups - 1) / groups;
+  groups = (slices + per - 1) / per;  // every group non-empty
+  reduce_slices_kernel<<<dim3((unsigned)blocks, groups), 64 * kRedWaves, 0, s>>>(part, slices, M, tmp, per);
+  reduce_slices_kernel<<<(unsigned)blocks, 64 * kRedWaves, 0, s>>>(tmp, groups, M, out, groups);
 }
 
 void launch_finalize(const FinalizeArgs& a, hipStream_t s) {

@@ -61,7 +61,10 @@ void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, 
 int launch_combine(const CombineArgs& a, hipStream_t s);  // returns the per-batch block count
 int combine_blocks(int64_t N);
 void launch_ll_reduce(const double* ll_part, int count, double inv_total, float* out, hipStream_t s);
-void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s);
+// out = Σ over slices of part[slice][M], in a fixed order; tmp (optional, tmp_floats
+// long) lets many slices be summed in parallel groups first.
+void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s,
+                          float* tmp = nullptr, int64_t tmp_floats = 0);
 void launch_finalize(const FinalizeArgs& a, hipStream_t s);
 void launch_unpack(const UnpackArgs& a, int B, hipStream_t s);
 void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
