@@ -115,6 +115,8 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
     // ~6144 waves: two full rounds at three resident waves per SIMD.
     int64_t fs = std::max<int64_t>(1, (6144 + q.B - 1) / q.B);
     fs = std::min(fs, std::max<int64_t>(1, row_blocks / kMinBlocksPerSlice));
+    // The kernel addresses a slice with 32-bit buffer offsets: keep it under 1 GiB.
+    fs = std::max<int64_t>(fs, (q.N * q.D * 2 + (int64_t(1) << 30) - 1) >> 30);
     q.frows = ((q.N + fs - 1) / fs + kBN - 1) / kBN * kBN;
     q.fslices = (int)((q.N + q.frows - 1) / q.frows);
   }

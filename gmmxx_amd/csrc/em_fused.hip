@@ -1,18 +1,21 @@
 // Fused single-pass EM tile for small K (spherical, bf16 x, K <= 64, D <= 64).
 //
 // Every wave owns all K components and works through its own contiguous run of
-// 32-row blocks, independently of the other waves (no workgroup barriers).
-// Per block it
-//   1. loads the rows straight from HBM into the E-GEMM operand layout
-//      (lane (li, g) holds row 16h + li, columns 32ec + 8g .. +7: a wave reads
-//      16 whole rows per instruction) and builds ‖x‖² and the augmented chunk
-//      in registers;
-//   2. runs the E-GEMM C = W·φᵀ (components x rows) with the augmented k-chunk,
+// 32-row blocks, independently of the other waves of its workgroup (they share
+// only the staged component operands). The contractions use the 32x32x16 bf16
+// MFMA, whose accumulator gives lane l the values of column l % 32 for 16 of
+// the 32 rows of a tile: with components as rows and data rows as columns, a
+// lane holds 16 components of ONE data row per component tile and its partner
+// lane l ^ 32 holds the other 16, so each row reduction is in-lane work plus a
+// single lane swap. Per block of 32 rows it
+//   1. loads each row straight from HBM (lane l: row l % 32, contiguous columns
+//      of half l / 32), forms ‖x‖² and the augmented k-chunk in registers;
+//   2. runs the E-GEMM T = W'·φᵀ (components x rows) with the augmented chunk,
 //      which yields the log2 logits directly (see em_sph_bf16.hip);
-//   3. reduces each row in registers (in-lane over components, two lane swaps
-//      over the four lane groups): m = max_k l, e = 2^(l - m), s = Σ e, and
-//      r = e / s -- one exponential per (row, component);
-//   4. stages r (row-major) and the rows with their augmented columns in a
+//   3. takes the row maximum m, and subtracts it with one more rank-1 MFMA
+//      (m split into three bf16 parts, so the shift is exact) instead of one
+//      VALU subtraction per element; then e = 2^(l - m), s = Σ e, r = e / s;
+//   4. stages r (row-major) and the rows ψ = [x | augmented columns] in a
 //      wave-private LDS region and reads both back with the transposing LDS
 //      load as the operands of the M-GEMM acc += rᵀ·ψ.
 // Each wave writes one partial statistics tile and one partial log-likelihood
@@ -25,17 +28,26 @@ namespace gx {
 
 namespace {
 
-constexpr int kAug = 32;
+constexpr int kAug = 32;       // augmented constants per component in the w_aug buffer
 constexpr float kHuge = 1e30f;
-constexpr int kWaves = 4;  // waves per workgroup (independent)
+constexpr int kWaves = 4;      // waves per workgroup
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 template <typename T>
 __device__ __forceinline__ T ld16(const void* p) { return *reinterpret_cast<const T*>(p); }
 
-template <int OFF, bool MAX>
-__device__ __forceinline__ float lanes_op(float v) {
-  const auto t = (OFF == 16) ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false)
-                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// The value of the partner lane l ^ 32 combined with this lane's.
+template <bool MAX>
+__device__ __forceinline__ float half_op(float v) {
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   const float a = __uint_as_float(t[0]), b = __uint_as_float(t[1]);
   return MAX ? fmaxf(a, b) : a + b;
 }
@@ -51,8 +63,10 @@ __device__ __forceinline__ uint32_t pack2(__bf16 a, __bf16 b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-typedef short v4s __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// Two floats rounded to bf16 (nearest even) in one dword, a in the low half.
+__device__ __forceinline__ uint32_t cvt2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
 
 // Transposing LDS read: in each 16-lane group, lane L supplies the address of
 // an 8-byte chunk; lane i receives word (i % 4) of the chunks of lanes 4j + i/4.
@@ -60,222 +74,269 @@ __device__ __forceinline__ v4s tr16(const __bf16* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
 }
 
+__device__ __forceinline__ bf16x8 cat(v4s lo, v4s hi) {
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 }  // namespace
 
-template <int DP, int CT>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(DP * CT >= 256 ? 1 : 2)))
+// KT: 32-component tiles (K <= 32 * KT). VEC: x rows are 16-byte aligned and D == DP.
+template <int DP, int KT, bool VEC>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(DP * KT >= 128 ? 2 : 3)))
 void sph_bf16_fused_kernel(TileArgs a) {
-  constexpr int ECH = DP / 32;                  // x chunks of 32 columns
-  constexpr int KC = 16 * CT;                   // component slots
-  constexpr int JT = DP / 16 + 1;               // ψ = [x | augmented columns 0..15]
-  constexpr int JP = 16 * JT;
-  // LDS strides (bf16): s = stride/2 dwords ≡ 8 or 24 (mod 32) for the transposing reads.
-  constexpr int XS = DP <= 32 ? 80 : 112;
-  constexpr int RS = KC <= 32 ? 48 : 80;
-  static_assert(DP + 16 <= XS && KC <= RS, "staging strides");
+  constexpr int XK = DP / 16;                   // k-steps over the x columns
+  constexpr int XT = DP / 32;                   // 32-column tiles of x in ψ
+  constexpr int KC = 32 * KT;                   // component slots
+  constexpr int JP = DP + 16;                   // statistics columns
+  // LDS strides (bf16); s = stride / 2 dwords ≡ 8 or 24 (mod 32) keeps the
+  // 16-byte accesses and the transposing reads free of bank conflicts.
+  constexpr int WS = 2 * DP + 16;               // [W' hi | W' lo | augmented constants 0..15]
+  constexpr int XS = DP <= 32 ? 80 : 112;       // [x | augmented columns 0..31]
+  constexpr int RS = KC <= 32 ? 48 : 80;        // r row
+  static_assert(DP + 32 <= XS && KC <= RS, "staging strides");
 
+  __shared__ __align__(16) __bf16 ws[KC * WS];
   __shared__ __align__(16) __bf16 xs_all[kWaves * 32 * XS];
   __shared__ __align__(16) __bf16 rs_all[kWaves * 32 * RS];
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int g = lane / 16, li = lane % 16;
+  const int lr = lane % 32, hf = lane / 32;     // data row / component of the tile; k half
   const int b = blockIdx.y;
-  const int slice = blockIdx.x * kWaves + wave;
+
+  // Stage the component operands once per workgroup. Slots past K get W' = 0
+  // and C = -1e30 (augmented column 6), so their responsibilities are 0.
+  constexpr int WCH = WS / 8;
+  for (int i = threadIdx.x; i < KC * WCH; i += 64 * kWaves) {
+    const int kk = i / WCH, c = i % WCH;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (kk < a.K) {
+      const size_t bk = (size_t)b * a.K + kk;
+      const __bf16* src = c < DP / 8   ? reinterpret_cast<const __bf16*>(a.w_hi) + bk * DP + 8 * c
+                          : c < DP / 4 ? reinterpret_cast<const __bf16*>(a.w_lo) + bk * DP + 8 * (c - DP / 8)
+                                       : reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * (c - DP / 4);
+      v = ld16<uint4>(src);
+    } else if (c == DP / 4) {
+      v.w = pack2((__bf16)(-kHuge), (__bf16)0.f);   // augmented elements 6 and 7
+    }
+    *reinterpret_cast<uint4*>(ws + kk * WS + 8 * c) = v;
+  }
+  __syncthreads();
+
+  // Wave-uniform: keeps the row bookkeeping in scalar registers.
+  const int slice = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + wave);
   if (slice >= a.nslices) return;
   const int64_t N = a.N;
-  const int K = a.K, D = a.D;
+  const int D = a.D;
   const int64_t rbeg = (int64_t)slice * a.rows_per_slice;
   const int64_t rend = (rbeg + a.rows_per_slice < N) ? rbeg + a.rows_per_slice : N;
   __bf16* xw = xs_all + wave * 32 * XS;
   __bf16* rw = rs_all + wave * 32 * RS;
-  // r rows: the 4-element column chunk is XOR-swizzled by (row / 4) % 4 so that
-  // the 16 lanes writing one column of 16 rows, and the transposing reads of 4
-  // rows x 4 chunks, both touch 16 distinct bank pairs.
+  // r rows: the 4-element column chunk is XOR-swizzled by (row / 4) % 4, so that
+  // lanes writing one chunk of consecutive rows, and the transposing reads of
+  // 4 rows x 4 chunks, touch distinct bank pairs.
   auto rswz = [](int row, int col) { return col ^ (((row >> 2) & 3) << 2); };
 
-  // ---- components: lane (li, g) holds component 16ct + li, k-group g ----
-  bf16x8 whi[CT][ECH], wlo[CT][ECH], waug[CT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct) {
-    const int kk = 16 * ct + li;
-    if (kk < K) {
-      const size_t bk = (size_t)b * K + kk;
-#pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) {
-        whi[ct][ec] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_hi) + bk * DP + 32 * ec + 8 * g);
-        wlo[ct][ec] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_lo) + bk * DP + 32 * ec + 8 * g);
-      }
-      waug[ct] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * g);
-    } else {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-#pragma unroll
-        for (int ec = 0; ec < ECH; ++ec) { whi[ct][ec][s] = (__bf16)0.f; wlo[ct][ec][s] = (__bf16)0.f; }
-        waug[ct][s] = (__bf16)((8 * g + s) == 6 ? -kHuge : 0.f);   // C = -1e30: r = 0
-      }
-    }
-  }
-  f32x4 acc[CT][JT];
-#pragma unroll
-  for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-    for (int jt = 0; jt < JT; ++jt) acc[ct][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Constant augmented columns of the staged rows: 8..31 are zero.
+  for (int i = lane; i < 32 * 3; i += 64)
+    *reinterpret_cast<uint4*>(xw + (i / 3) * XS + DP + 8 + 8 * (i % 3)) = make_uint4(0u, 0u, 0u, 0u);
 
-  // Constant augmented columns 8..15 of the staged rows: [1 0 0 0 0 0 0 0].
-  for (int r = lane; r < 32; r += 64)
-    *reinterpret_cast<uint4*>(xw + r * XS + DP + 8) = make_uint4(pack2((__bf16)1.f, (__bf16)0.f), 0u, 0u, 0u);
+  // E-GEMM operands of this lane: component 32t + lr, k half hf; x k-step s
+  // covers columns 8 (hf XK + s) .. +7, so each lane's x columns are contiguous.
+  const __bf16* wl = ws + lr * WS;
+  // Rank-1 shift operand: ones in k slots 0..2 for every component.
+  const bf16x8 ones3 = __builtin_bit_cast(
+      bf16x8, hf == 0 ? make_uint4(pack2((__bf16)1.f, (__bf16)1.f), pack2((__bf16)1.f, (__bf16)0.f), 0u, 0u)
+                      : make_uint4(0u, 0u, 0u, 0u));
+
+  f32x16 accx[KT][XT], acca[KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    acca[t] = f32x16{};
+#pragma unroll
+    for (int xt = 0; xt < XT; ++xt) accx[t][xt] = f32x16{};
+  }
 
   const __bf16* xb = reinterpret_cast<const __bf16*>(a.x) + (size_t)b * N * D;
-  // Row 16h + li, columns 32ec + 8g .. +7 of the block at n0 (zero past the slice end).
-  auto load = [&](int64_t n0, uint4 (&v)[2][ECH]) {
-    const int last = (int)(rend - 1 - n0);
-    const __bf16* blk = xb + (size_t)n0 * D;
+  // Row lr of the block at n0, chunks hf XK + s. Rows past the slice end must be
+  // finite (their responsibilities and log-likelihood terms are masked to zero
+  // below): whole-chunk rows use buffer loads bounded by the slice, which return
+  // 0 there; padded rows re-read the slice's last row. Every call issues the same
+  // loads, so the prefetch below needs no branches.
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__bf16*>(xb + (size_t)rbeg * D), (short)0, (int)((rend - rbeg) * D * 2), 0x00020000);
+  const int voff = (lr * D + 8 * hf * XK) * 2;
+  auto load = [&](int64_t n0, uint4 (&v)[XK]) {
+    if constexpr (VEC) {
+      const int soff = (int)((n0 - rbeg) * D * 2);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = 16 * h + li;
-      const bool valid = r <= last;
+      for (int s = 0; s < XK; ++s)
+        v[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, voff + 16 * s, soff, 0));
+    } else {
+      const int64_t nb = n0 < rend ? n0 : n0 - 32;
+      const __bf16* blk = xb + (size_t)nb * D;
+      const int r = min(lr, (int)(rend - 1 - nb));
 #pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) {
-        const int c = 32 * ec + 8 * g;
-        if (a.vec_ok) {
-          const uint4 t = *reinterpret_cast<const uint4*>(blk + (valid ? r : last) * D + c);
-          v[h][ec] = valid ? t : make_uint4(0, 0, 0, 0);
-        } else {
-          union { uint4 u; __bf16 e[8]; } t;
+      for (int s = 0; s < XK; ++s) {
+        const int c = 8 * (hf * XK + s);
+        // Built as whole dwords so that the loop-carried rows stay in 32-bit registers.
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(blk) + (size_t)r * D + c;
+        uint32_t w4[4];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) t.e[j] = (valid && c + j < D) ? blk[r * D + c + j] : (__bf16)0.f;
-          v[h][ec] = t.u;
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = (c + 2 * j < D) ? src[2 * j] : 0u;
+          const uint32_t hi = (c + 2 * j + 1 < D) ? src[2 * j + 1] : 0u;
+          w4[j] = lo | (hi << 16);
         }
+        v[s] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
       }
     }
   };
 
   double ll = 0.0;
   const int nblk = (rend > rbeg) ? (int)((rend - rbeg + 31) / 32) : 0;
-  uint4 cur[2][ECH], nxt[2][ECH];
-  if (nblk > 0) load(rbeg, cur);
-  for (int ib = 0; ib < nblk; ++ib) {
-    const int64_t n0 = rbeg + (int64_t)ib * 32;
-    if (ib + 1 < nblk) load(n0 + 32, nxt);
-    const int last = (int)(rend - 1 - n0);
 
-    // ‖x‖² per row and the augmented operand (lane group 0: q parts and ones,
-    // group 1: the third constant column, groups 2-3: zero).
-    bf16x8 xa[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float q = 0.f;
-#pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) {
-        const uint4 u = cur[h][ec];
-        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x2 p = __builtin_bit_cast(bf16x2, w4[j]);
-          q = __builtin_amdgcn_fdot2_f32_bf16(p, p, q, false);
-        }
-      }
-      q = lanes_op<32, false>(lanes_op<16, false>(q));
-      __bf16 qh, qm, ql;
-      split3(q, qh, qm, ql);
-      const uint4 w0 = make_uint4(pack2(qh, qm), pack2(ql, qh), pack2(qm, qh), pack2((__bf16)1.f, (__bf16)1.f));
-      const uint4 w = (g == 0) ? w0 : (g == 1 ? make_uint4(pack2((__bf16)1.f, (__bf16)0.f), 0u, 0u, 0u)
-                                              : make_uint4(0u, 0u, 0u, 0u));
-      xa[h] = __builtin_bit_cast(bf16x8, w);
-      // stage the row (x and augmented columns 0..7) for the ψ operand
-      __bf16* row = xw + (16 * h + li) * XS;
-#pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) *reinterpret_cast<uint4*>(row + 32 * ec + 8 * g) = cur[h][ec];
-      if (g == 0) *reinterpret_cast<uint4*>(row + DP) = w0;
-    }
+  // Transposing-read addresses for the 32x32 operands: lane i of 16-lane group G
+  // reads rows 8 (G / 2) + i / 4 (+4) of a k-step and columns 16 (G % 2) + 4 (i % 4).
+  const int G = lane / 16, i16 = lane % 16;
+  const int trow = 8 * (G >> 1) + (i16 >> 2), tcol = 16 * (G & 1) + 4 * (i16 & 3);
 
-    // E-GEMM: T[ct][h] = W(16 comps) · φᵀ(16 rows); lane (li, g): components 16ct + 4g + v of row 16h + li.
-    f32x4 T[CT][2];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) T[ct][h] = mfma_bf16(waug[ct], xa[h], f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-    for (int ec = 0; ec < ECH; ++ec)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const bf16x8 xv = __builtin_bit_cast(bf16x8, cur[h][ec]);
-          T[ct][h] = mfma_bf16(whi[ct][ec], xv, T[ct][h]);
-          T[ct][h] = mfma_bf16(wlo[ct][ec], xv, T[ct][h]);
-        }
+  // One block: `cur` holds its rows; the next block's rows are loaded into
+  // `nxt`. Two blocks per loop trip, so the two register sets alternate without
+  // copies and the prefetch stays in flight while the current block is processed.
+  auto block = [&](int64_t n0, uint4 (&cur)[XK], uint4 (&nxt)[XK]) {
+    load(n0 + 32, nxt);
+    const bool valid = n0 + lr < rend;
 
-    // Row log-normaliser and responsibilities.
+    // ‖x‖² of row lr and the augmented operand: k 0..7 (half 0) = q_h q_m q_l q_h q_m q_h 1 1,
+    // k 8..15 (half 1) = 1 0 ... 0.
+    float q = 0.f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      float m = T[0][h][0];
+    for (int s = 0; s < XK; ++s) {
+      const uint32_t w4[4] = {cur[s].x, cur[s].y, cur[s].z, cur[s].w};
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) m = fmaxf(m, T[ct][h][v]);
-      m = lanes_op<32, true>(lanes_op<16, true>(m));
-      float s = 0.f;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          T[ct][h][v] = fast_exp2(T[ct][h][v] - m);
-          s += T[ct][h][v];
-        }
-      s = lanes_op<32, false>(lanes_op<16, false>(s));
-      const bool valid = 16 * h + li <= last;
-      if (g == 0 && valid) ll += (double)(m + __log2f(s));
-      const float inv = valid ? __builtin_amdgcn_rcpf(s) : 0.f;
-      const int rr = 16 * h + li;
-      __bf16* row = rw + rr * RS;
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const uint2 p = make_uint2(pack2((__bf16)(T[ct][h][0] * inv), (__bf16)(T[ct][h][1] * inv)),
-                                   pack2((__bf16)(T[ct][h][2] * inv), (__bf16)(T[ct][h][3] * inv)));
-        *reinterpret_cast<uint2*>(row + 16 * ct + rswz(rr, 4 * g)) = p;
+      for (int j = 0; j < 4; ++j) {
+        const bf16x2 p = __builtin_bit_cast(bf16x2, w4[j]);
+        q = __builtin_amdgcn_fdot2_f32_bf16(p, p, q, false);
       }
     }
+    q = half_op<false>(q);
+    __bf16 qh, qm, ql;
+    split3(q, qh, qm, ql);
+    const uint4 w0 = make_uint4(pack2(qh, qm), pack2(ql, qh), pack2(qm, qh), pack2((__bf16)1.f, (__bf16)1.f));
+    const uint4 w1 = make_uint4(pack2((__bf16)1.f, (__bf16)0.f), 0u, 0u, 0u);
+    const bf16x8 phia = __builtin_bit_cast(bf16x8, hf == 0 ? w0 : w1);
+    // Stage the row for the ψ operand: x, and augmented columns 0..7 = w0.
+    __bf16* row = xw + lr * XS;
+#pragma unroll
+    for (int s = 0; s < XK; ++s) *reinterpret_cast<uint4*>(row + 8 * (hf * XK + s)) = cur[s];
+    if (hf == 0) *reinterpret_cast<uint4*>(row + DP) = w0;
+
+    // E-GEMM: lane l, register v of tile t holds component 32t + 8(v/4) + 4hf + v%4 of row lr.
+    f32x16 T[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const __bf16* wt = wl + 32 * t * WS;
+      T[t] = mfma32(ld16<bf16x8>(wt + 2 * DP + 8 * hf), phia, f32x16{});
+#pragma unroll
+      for (int s = 0; s < XK; ++s) {
+        const bf16x8 xv = __builtin_bit_cast(bf16x8, cur[s]);
+        const int c = 8 * (hf * XK + s);
+        T[t] = mfma32(ld16<bf16x8>(wt + c), xv, T[t]);
+        T[t] = mfma32(ld16<bf16x8>(wt + DP + c), xv, T[t]);
+      }
+    }
+
+    // Row maximum, shifted out by the rank-1 MFMA: T += 1 · (-(m_h + m_m + m_l)).
+    float m = T[0][0];
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) m = fmaxf(m, T[t][v]);
+    m = half_op<true>(m);
+    __bf16 mh, mm, ml;
+    split3(-m, mh, mm, ml);
+    const bf16x8 phim = __builtin_bit_cast(
+        bf16x8, hf == 0 ? make_uint4(pack2(mh, mm), pack2(ml, (__bf16)0.f), 0u, 0u) : make_uint4(0u, 0u, 0u, 0u));
+#pragma unroll
+    for (int t = 0; t < KT; ++t) T[t] = mfma32(ones3, phim, T[t]);
+
+    // e = 2^(l - m), s = Σ e (pairwise), r = e / s.
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) T[t][v] = fast_exp2(T[t][v]);
+    float ps[4 * KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        ps[4 * t + u] = (T[t][4 * u] + T[t][4 * u + 1]) + (T[t][4 * u + 2] + T[t][4 * u + 3]);
+#pragma unroll
+    for (int w = 1; w < 4 * KT; w *= 2)
+#pragma unroll
+      for (int u = 0; u + w < 4 * KT; u += 2 * w) ps[u] += ps[u + w];
+    const float s = half_op<false>(ps[0]);
+    if (hf == 0 && valid) ll += (double)(m + __log2f(s));
+    const float inv = valid ? __builtin_amdgcn_rcpf(s) : 0.f;
+    __bf16* rrow = rw + lr * RS;
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint2 p = make_uint2(cvt2(T[t][4 * u] * inv, T[t][4 * u + 1] * inv),
+                                   cvt2(T[t][4 * u + 2] * inv, T[t][4 * u + 3] * inv));
+        *reinterpret_cast<uint2*>(rrow + rswz(lr, 32 * t + 8 * u + 4 * hf)) = p;
+      }
     // The staging writes above and the transposing reads below are LDS operations
     // of this wave only, executed in order; keep the compiler from reordering them.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // M-GEMM: k = data row; lane L of group g reads rows 8g + L/4 (+4), 4 columns at 4(L%4).
-    const int rrow = 8 * g + (li >> 2), rcol = 4 * (li & 3);
-    bf16x8 ar[CT];
+    // M-GEMM over the 32 rows in two k-steps of 16: acc[t][·] += rᵀ(components of t) · ψ.
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-      const v4s lo = tr16(rw + rrow * RS + 16 * ct + rswz(rrow, rcol));
-      const v4s hi = tr16(rw + (rrow + 4) * RS + 16 * ct + rswz(rrow + 4, rcol));
-      ar[ct] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int r0 = 16 * s2 + trow;
+      bf16x8 ar[KT];
 #pragma unroll
-    for (int jt = 0; jt < JT; ++jt) {
-      const v4s plo = tr16(xw + rrow * XS + 16 * jt + rcol);
-      const v4s phi = tr16(xw + (rrow + 4) * XS + 16 * jt + rcol);
-      const bf16x8 bq = __builtin_bit_cast(bf16x8, __builtin_shufflevector(plo, phi, 0, 1, 2, 3, 4, 5, 6, 7));
+      for (int t = 0; t < KT; ++t)
+        ar[t] = cat(tr16(rw + r0 * RS + rswz(r0, 32 * t + tcol)),
+                    tr16(rw + (r0 + 4) * RS + rswz(r0 + 4, 32 * t + tcol)));
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) acc[ct][jt] = mfma_bf16(ar[ct], bq, acc[ct][jt]);
+      for (int xt = 0; xt <= XT; ++xt) {
+        const bf16x8 bq = cat(tr16(xw + r0 * XS + 32 * xt + tcol), tr16(xw + (r0 + 4) * XS + 32 * xt + tcol));
+#pragma unroll
+        for (int t = 0; t < KT; ++t) {
+          if (xt < XT) accx[t][xt] = mfma32(ar[t], bq, accx[t][xt]);
+          else acca[t] = mfma32(ar[t], bq, acca[t]);
+        }
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) cur[h][ec] = nxt[h][ec];
+  };
+  uint4 xa_[XK], xb_[XK];
+  if (nblk > 0) load(rbeg, xa_);
+  for (int ib = 0; ib < nblk; ib += 2) {
+    const int64_t n0 = rbeg + (int64_t)ib * 32;
+    block(n0, xa_, xb_);
+    __builtin_amdgcn_sched_barrier(0);
+    if (ib + 1 < nblk) block(n0 + 32, xb_, xa_);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
-  // Partial statistics of this wave's rows: component 16ct + 4g + v, feature 16jt + li.
+  // Partial statistics of this wave's rows: lane l, register v of tile t is
+  // component 32t + 8(v/4) + 4hf + v%4 and column lr of an x tile / of the augmented block.
+  float* dst0 = a.part_stats + ((size_t)slice * a.B + b) * a.K * JP;
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct)
+  for (int t = 0; t < KT; ++t)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int kk = 16 * ct + 4 * g + v;
-      if (kk < K) {
-        float* dst = a.part_stats + (((size_t)slice * a.B + b) * K + kk) * JP;
+    for (int v = 0; v < 16; ++v) {
+      const int kk = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
+      if (kk < a.K) {
+        float* dst = dst0 + (size_t)kk * JP;
 #pragma unroll
-        for (int jt = 0; jt < JT; ++jt) dst[16 * jt + li] = acc[ct][jt][v];
+        for (int xt = 0; xt < XT; ++xt) dst[32 * xt + lr] = accx[t][xt][v];
+        if (lr < 16) dst[DP + lr] = acca[t][v];
       }
     }
   // Partial log-likelihood (natural log) of this wave's rows.
@@ -283,26 +344,24 @@ void sph_bf16_fused_kernel(TileArgs a) {
   if (lane == 0) a.ll_part[(size_t)b * a.nslices + slice] = ll * (double)kLn2;
 }
 
+template <int DP, int KT>
+static void launch_fused(const TileArgs& a, dim3 grid, dim3 block, hipStream_t s) {
+  if (a.vec_ok) sph_bf16_fused_kernel<DP, KT, true><<<grid, block, 0, s>>>(a);
+  else sph_bf16_fused_kernel<DP, KT, false><<<grid, block, 0, s>>>(a);
+}
+
 int launch_sph_bf16_fused(int dp, int k, const TileArgs& a, int slices, hipStream_t s) {
+  if (k < 1 || k > 64 || (dp != 32 && dp != 64)) return -1;
   const dim3 grid((slices + kWaves - 1) / kWaves, a.B), block(64 * kWaves);
-  const int ct = (k + 15) / 16;
+  const bool one = k <= 32;
   if (dp == 32) {
-    switch (ct) {
-      case 1: sph_bf16_fused_kernel<32, 1><<<grid, block, 0, s>>>(a); return 0;
-      case 2: sph_bf16_fused_kernel<32, 2><<<grid, block, 0, s>>>(a); return 0;
-      case 3: case 4: sph_bf16_fused_kernel<32, 4><<<grid, block, 0, s>>>(a); return 0;
-      default: return -1;
-    }
+    if (one) launch_fused<32, 1>(a, grid, block, s);
+    else launch_fused<32, 2>(a, grid, block, s);
+  } else {
+    if (one) launch_fused<64, 1>(a, grid, block, s);
+    else launch_fused<64, 2>(a, grid, block, s);
   }
-  if (dp == 64) {
-    switch (ct) {
-      case 1: sph_bf16_fused_kernel<64, 1><<<grid, block, 0, s>>>(a); return 0;
-      case 2: sph_bf16_fused_kernel<64, 2><<<grid, block, 0, s>>>(a); return 0;
-      case 3: case 4: sph_bf16_fused_kernel<64, 4><<<grid, block, 0, s>>>(a); return 0;
-      default: return -1;
-    }
-  }
-  return -1;
+  return 0;
 }
 
 }  // namespace gx

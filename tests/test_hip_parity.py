@@ -71,7 +71,10 @@ CASES = [
     ("spherical", 2, 6000, 32, 64, torch.float32),
     ("spherical", 1, 24000, 128, 300, torch.float32),     # two k-tiles, partial second tile
     ("spherical", 1, 30000, 128, 520, torch.bfloat16),    # three k-tiles
-    ("spherical", 2, 6000, 32, 64, torch.bfloat16),
+    ("spherical", 2, 6000, 32, 64, torch.bfloat16),        # fused single pass, whole-chunk rows
+    ("spherical", 1, 5000, 20, 10, torch.bfloat16),        # fused, padded rows, one component tile
+    ("spherical", 3, 4000, 50, 30, torch.bfloat16),        # fused, D 64 padded, two component tiles
+    ("spherical", 1, 9000, 64, 48, torch.bfloat16),        # fused, D 64, three component tiles
     ("spherical", 1, 777, 5, 3, torch.float32),           # D and N not multiples of the tile
     ("diag", 1, 30000, 64, 512, torch.float32),           # two k-tiles
     ("diag", 2, 3000, 20, 40, torch.float32),
