@@ -32,6 +32,7 @@ struct Plan {
   int lnw = 0, lktiles = 0;  // waves / component tiles of the plain log-normaliser pass (MODE_LSE)
   bool fused = false;        // EM iteration as one fused pass (small K; em_fused.hip)
   int fslices = 0;           // fused: one wave per row slice
+  int fparts = 0;            // fused: partial results (one per workgroup of kFusedWaves slices)
   int64_t frows = 0;
   int64_t rows_per_slice = 0;
   int gram_slices = 0;
@@ -119,6 +120,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
     fs = std::max<int64_t>(fs, (q.N * q.D * 2 + (int64_t(1) << 30) - 1) >> 30);
     q.frows = ((q.N + fs - 1) / fs + kBN - 1) / kBN * kBN;
     q.fslices = (int)((q.N + q.frows - 1) / q.frows);
+    q.fparts = (q.fslices + kFusedWaves - 1) / kFusedWaves;
   }
   int64_t gs = std::min<int64_t>(64, row_blocks);
   q.gram_rows = ((q.N + gs - 1) / gs + kBN - 1) / kBN * kBN;
@@ -213,12 +215,12 @@ int run_fused(const Plan& pl, const TileArgs& t, hipStream_t s) {
   u.rows_per_slice = pl.frows;
   return launch_sph_bf16_fused(pl.DP, pl.K, u, pl.fslices, s);
 }
-int stat_slices(const Plan& pl) { return pl.fused ? pl.fslices : pl.slices; }
+int stat_slices(const Plan& pl) { return pl.fused ? pl.fparts : pl.slices; }
 // The tile-partial buffer is free once the statistics are being reduced: it is
 // the scratch of the grouped slice reduction.
 float* red_tmp(const Plan& pl, void* ws) { return at<float>(ws, pl.o_pms); }
 int64_t red_tmp_floats(const Plan& pl) { return (int64_t)std::max(pl.ktiles, pl.lktiles) * pl.B * pl.N * 2; }
-int ll_parts(const Plan& pl) { return pl.B * (pl.fused ? pl.fslices : pl.cblocks); }
+int ll_parts(const Plan& pl) { return pl.B * (pl.fused ? pl.fparts : pl.cblocks); }
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
 int prepare(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights,
@@ -426,7 +428,7 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   if (pl.fused) {
     if (run_fused(pl, tile_args(pl, x, ws), s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
     launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0, ll_sum, s);
-    launch_reduce_slices(at<float>(ws, pl.o_pstats), pl.fslices, (int64_t)pl.B * pl.K * pl.JP,
+    launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                          at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
     if ((rc = check_hip("fused statistics pass"))) return rc;
   } else {

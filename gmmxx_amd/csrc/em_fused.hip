@@ -30,7 +30,7 @@ namespace {
 
 constexpr int kAug = 32;       // augmented constants per component in the w_aug buffer
 constexpr float kHuge = 1e30f;
-constexpr int kWaves = 4;      // waves per workgroup
+constexpr int kWaves = kFusedWaves;   // waves per workgroup
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short v4s __attribute__((ext_vector_type(4)));
@@ -95,9 +95,15 @@ void sph_bf16_fused_kernel(TileArgs a) {
   constexpr int RS = KC <= 32 ? 48 : 80;        // r row
   static_assert(DP + 32 <= XS && KC <= RS, "staging strides");
 
-  __shared__ __align__(16) __bf16 ws[KC * WS];
-  __shared__ __align__(16) __bf16 xs_all[kWaves * 32 * XS];
-  __shared__ __align__(16) __bf16 rs_all[kWaves * 32 * RS];
+  // One LDS pool: staged operands while the rows stream, then the workgroup's
+  // statistics while the waves' partial tiles are combined.
+  constexpr int kPool = KC * WS + kWaves * 32 * (XS + RS);
+  static_assert(KC * JP * 2 <= kPool, "combine buffer");
+  __shared__ __align__(16) __bf16 pool[kPool];
+  __shared__ double llw[kWaves];
+  __bf16* const ws = pool;
+  __bf16* const xs_all = pool + KC * WS;
+  __bf16* const rs_all = xs_all + kWaves * 32 * XS;
 
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int lr = lane % 32, hf = lane / 32;     // data row / component of the tile; k half
@@ -122,12 +128,12 @@ void sph_bf16_fused_kernel(TileArgs a) {
   }
   __syncthreads();
 
-  // Wave-uniform: keeps the row bookkeeping in scalar registers.
+  // Wave-uniform: keeps the row bookkeeping in scalar registers. A wave past the
+  // last slice gets an empty row range (it still takes part in the combine).
   const int slice = __builtin_amdgcn_readfirstlane(blockIdx.x * kWaves + wave);
-  if (slice >= a.nslices) return;
   const int64_t N = a.N;
   const int D = a.D;
-  const int64_t rbeg = (int64_t)slice * a.rows_per_slice;
+  const int64_t rbeg = slice < a.nslices ? (int64_t)slice * a.rows_per_slice : N;
   const int64_t rend = (rbeg + a.rows_per_slice < N) ? rbeg + a.rows_per_slice : N;
   __bf16* xw = xs_all + wave * 32 * XS;
   __bf16* rw = rs_all + wave * 32 * RS;
@@ -162,8 +168,16 @@ void sph_bf16_fused_kernel(TileArgs a) {
   // below): whole-chunk rows use buffer loads bounded by the slice, which return
   // 0 there; padded rows re-read the slice's last row. Every call issues the same
   // loads, so the prefetch below needs no branches.
+  // (readfirstlane: the descriptor must live in scalar registers. The builtin
+  // returns a signed int: each half is zero-extended through uint32_t, or a low
+  // word with bit 31 set would sign-extend into the high word.)
+  const uint64_t xaddr = reinterpret_cast<uint64_t>(xb + (size_t)rbeg * D);
+  const uint32_t xhi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(xaddr >> 32));
+  const uint32_t xlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)xaddr);
+  const uint64_t xbase = ((uint64_t)xhi << 32) | (uint64_t)xlo;
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<__bf16*>(xb + (size_t)rbeg * D), (short)0, (int)((rend - rbeg) * D * 2), 0x00020000);
+      reinterpret_cast<void*>(xbase), (short)0, __builtin_amdgcn_readfirstlane((int)((rend - rbeg) * D * 2)),
+      0x00020000);
   const int voff = (lr * D + 8 * hf * XK) * 2;
   auto load = [&](int64_t n0, uint4 (&v)[XK]) {
     if constexpr (VEC) {
@@ -324,24 +338,37 @@ void sph_bf16_fused_kernel(TileArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // Partial statistics of this wave's rows: lane l, register v of tile t is
-  // component 32t + 8(v/4) + 4hf + v%4 and column lr of an x tile / of the augmented block.
-  float* dst0 = a.part_stats + ((size_t)slice * a.B + b) * a.K * JP;
+  // Combine the waves' partial statistics in LDS in a fixed order (0 + w0 + w1 + ...),
+  // then write the workgroup's tile. Lane l, register v of tile t holds component
+  // 32t + 8(v/4) + 4hf + v%4 and column lr of an x tile / of the augmented block.
+  float* const red = reinterpret_cast<float*>(pool);
+  __syncthreads();   // every wave is done with the staging buffers
+  for (int i = threadIdx.x; i < KC * JP; i += 64 * kWaves) red[i] = 0.f;
+  for (int w = 0; w < kWaves; ++w) {
+    __syncthreads();
+    if (wave == w) {
 #pragma unroll
-  for (int t = 0; t < KT; ++t)
+      for (int t = 0; t < KT; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int kk = 32 * t + 8 * (v / 4) + 4 * hf + (v % 4);
-      if (kk < a.K) {
-        float* dst = dst0 + (size_t)kk * JP;
+        for (int v = 0; v < 16; ++v) {
+          float* dst = red + (32 * t + 8 * (v / 4) + 4 * hf + (v % 4)) * JP;
 #pragma unroll
-        for (int xt = 0; xt < XT; ++xt) dst[32 * xt + lr] = accx[t][xt][v];
-        if (lr < 16) dst[DP + lr] = acca[t][v];
-      }
+          for (int xt = 0; xt < XT; ++xt) dst[32 * xt + lr] += accx[t][xt][v];
+          if (lr < 16) dst[DP + lr] += acca[t][v];
+        }
     }
-  // Partial log-likelihood (natural log) of this wave's rows.
+  }
+  // Partial log-likelihood (natural log) of the workgroup's rows, same order.
   for (int off = 32; off >= 1; off /= 2) ll += __shfl_xor(ll, off);
-  if (lane == 0) a.ll_part[(size_t)b * a.nslices + slice] = ll * (double)kLn2;
+  if (lane == 0) llw[wave] = ll;
+  __syncthreads();
+  float* out = a.part_stats + ((size_t)blockIdx.x * a.B + b) * a.K * JP;
+  for (int i = threadIdx.x; i < a.K * JP; i += 64 * kWaves) out[i] = red[i];
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int w = 0; w < kWaves; ++w) sum += llw[w];
+    a.ll_part[(size_t)b * gridDim.x + blockIdx.x] = sum * (double)kLn2;
+  }
 }
 
 template <int DP, int KT>

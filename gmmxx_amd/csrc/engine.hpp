@@ -34,7 +34,10 @@ int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid,
 // dp 128 with nw 8 (and 16 for MODE_LSE).
 int launch_sph_bf16(int dp, int nw, int mode, const TileArgs& a, dim3 grid, hipStream_t s);
 // Fused single-pass kernel (em_fused.hip): spherical bf16, dp in {32, 64}, K <= 64;
-// one wave per row slice, `slices` slices.
+// one wave per row slice, `slices` slices, kFusedWaves waves per workgroup. Each
+// workgroup writes ONE partial statistics tile and ONE partial log-likelihood
+// (index blockIdx.x; a.nslices is the number of wave slices).
+constexpr int kFusedWaves = 4;
 int launch_sph_bf16_fused(int dp, int k, const TileArgs& a, int slices, hipStream_t s);
 
 }  // namespace gx
