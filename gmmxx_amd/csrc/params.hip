@@ -39,24 +39,32 @@ __device__ float weight_total(const float* w, int K, float floor_v, float* scrat
 }
 
 // ---------------------------------------------------------------------------
-// Prelude + E-step operand packing (one thread per component)
+// Prelude + E-step operand packing (one wave per component, lanes over features)
 // ---------------------------------------------------------------------------
 
-__global__ void prep_kernel(PrepArgs a) {
+constexpr int kMaxPrepD = 128;
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off >= 1; off /= 2) v += __shfl_xor(v, off);
+  return v;
+}
+
+__global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
   __shared__ float scratch[32];
-  const int b = blockIdx.y;
+  __shared__ float mus[kMaxPrepD];
+  const int b = blockIdx.y, k = blockIdx.x, lane = threadIdx.x;
   const int K = a.K, D = a.D, DP = a.DP, EP = a.EP;
   const float* wrow = a.weights + (size_t)b * K;
   // Iteration prelude (torch_fallback.py:2061-2066): w <- max(w, min_weight) / Σ.
   // Inference uses the weights as given (log w only).
   const float floor_v = a.prelude ? a.min_weight : -INFINITY;
   const float total = a.prelude ? weight_total(wrow, K, floor_v, scratch) : 1.f;
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= K) return;
   const size_t bk = (size_t)b * K + k;
   const float wk = a.prelude ? fmaxf(wrow[k], floor_v) / total : wrow[k];
   const float lw = logf(wk);
   const float* mu = a.means + bk * D;
+  for (int d = lane; d < D; d += 64) mus[d] = mu[d];
+  __syncthreads();
   float colq, ca, cb;
   const float log2pi_d = (float)(kLog2Pi * (double)D);
 
@@ -68,14 +76,14 @@ __global__ void prep_kernel(PrepArgs a) {
     reinterpret_cast<__bf16*>(a.w_hi)[bk * EP + e] = hi;
     reinterpret_cast<__bf16*>(a.w_lo)[bk * EP + e] = (__bf16)(v - (float)hi);
   };
-  auto put = [&](int e, float v) { if (a.bf) put_bf(e, v); else put_f32(e, v); };
 
   if (a.cov == SPH) {
     float var = a.covs[bk];
     if (a.prelude) var = fmaxf(var, a.reg_covar);
-    a.covs_used[bk] = var;
+    if (lane == 0) a.covs_used[bk] = var;
     float msq = 0.f;
-    for (int d = 0; d < D; ++d) msq = fmaf(mu[d], mu[d], msq);
+    for (int d = lane; d < D; d += 64) msq = fmaf(mus[d], mus[d], msq);
+    msq = wave_sum(msq);
     const float lognorm = (float)D * ((float)kLog2Pi + logf(var));
     colq = msq;
     ca = -0.5f * kLog2e / var;
@@ -83,8 +91,7 @@ __global__ void prep_kernel(PrepArgs a) {
     if (a.bf) {
       // bf16 kernel: W' = -2·ca·μ (hi/lo) and the augmented constants
       // [A_h A_h A_h A_m A_m A_l C_h C_m | C_l 0 ...] with A = ca, C = ca·‖μ‖² + cb.
-      for (int e = 0; e < EP; ++e) put_bf(e, e < D ? -2.f * ca * mu[e] : 0.f);
-      __bf16* aug = reinterpret_cast<__bf16*>(a.w_aug) + bk * 32;
+      for (int e = lane; e < EP; e += 64) put_bf(e, e < D ? -2.f * ca * mus[e] : 0.f);
       const float cy = fmaf(ca, colq, cb);
       const __bf16 ah = (__bf16)ca;
       const __bf16 am = (__bf16)(ca - (float)ah);
@@ -92,69 +99,70 @@ __global__ void prep_kernel(PrepArgs a) {
       const __bf16 ch = (__bf16)cy;
       const __bf16 cm = (__bf16)(cy - (float)ch);
       const __bf16 cl = (__bf16)(cy - (float)ch - (float)cm);
-      const __bf16 zero = (__bf16)0.f;
       const __bf16 vals[9] = {ah, ah, ah, am, am, al, ch, cm, cl};
-      for (int e = 0; e < 32; ++e) aug[e] = e < 9 ? vals[e] : zero;
+      if (lane < 32) reinterpret_cast<__bf16*>(a.w_aug)[bk * 32 + lane] = lane < 9 ? vals[lane] : (__bf16)0.f;
     } else {
-      for (int e = 0; e < EP; ++e) put(e, e < D ? mu[e] : 0.f);
+      for (int e = lane; e < EP; e += 64) put_f32(e, e < D ? mus[e] : 0.f);
     }
   } else if (a.cov == DIAG) {
     // torch_fallback.py:2491-2494
     const float* vr = a.covs + bk * D;
     float* vu = a.covs_used + bk * D;
     float logdet = 0.f, mpm = 0.f;
-    for (int d = 0; d < D; ++d) {
+    for (int d = lane; d < D; d += 64) {
       float v = vr[d];
       if (a.prelude) v = fmaxf(v, a.reg_covar);
       vu[d] = v;
       const float vc = fmaxf(v, 1e-30f);
       const float p = 1.f / vc;
-      const float wm = mu[d] * p;
+      const float wm = mus[d] * p;
       logdet += logf(vc);
-      mpm = fmaf(mu[d], wm, mpm);
+      mpm = fmaf(mus[d], wm, mpm);
       put_f32(d, p);
       put_f32(DP + d, -2.f * wm);
     }
-    for (int d = D; d < DP; ++d) { put_f32(d, 0.f); put_f32(DP + d, 0.f); }
-    for (int e = 2 * DP; e < EP; ++e) put_f32(e, 0.f);
-    colq = mpm;
+    for (int d = D + lane; d < DP; d += 64) { put_f32(d, 0.f); put_f32(DP + d, 0.f); }
+    for (int e = 2 * DP + lane; e < EP; e += 64) put_f32(e, 0.f);
+    logdet = wave_sum(logdet);
+    colq = wave_sum(mpm);
     ca = -0.5f * kLog2e;
     cb = (lw - 0.5f * (log2pi_d + logdet)) * kLog2e;
   } else if (a.cov == TIED) {
     // Pμ_k (torch_fallback.py:2873), μᵀPμ (:2874)
     const float* P = a.prec + (size_t)b * D * D;
     float mpm = 0.f;
-    for (int d = 0; d < D; ++d) {
+    for (int d = lane; d < D; d += 64) {
       float pm = 0.f;
-      for (int e = 0; e < D; ++e) pm = fmaf(mu[e], P[d * D + e], pm);
-      mpm = fmaf(mu[d], pm, mpm);
+      for (int e = 0; e < D; ++e) pm = fmaf(mus[e], P[d * D + e], pm);
+      mpm = fmaf(mus[d], pm, mpm);
       put_f32(d, pm);
     }
-    for (int e = D; e < EP; ++e) put_f32(e, 0.f);
-    colq = mpm;
+    for (int e = D + lane; e < EP; e += 64) put_f32(e, 0.f);
+    colq = wave_sum(mpm);
     ca = -0.5f * kLog2e;
     cb = (lw - 0.5f * (log2pi_d + a.logdet[b])) * kLog2e;
   } else {
     // FULL: W_k = [packed P_k with doubled off-diagonal | -2 P_k μ_k]  (torch_fallback.py:418-432)
     const float* P = a.prec + bk * D * D;
     const int S = DP * (DP + 1) / 2;
-    for (int e = 0; e < EP; ++e) put_f32(e, 0.f);
+    for (int e = lane; e < EP; e += 64) put_f32(e, 0.f);
+    __syncthreads();   // the zero fill lands before the packed entries below
     float mpm = 0.f;
-    for (int d = 0; d < D; ++d) {
+    for (int d = lane; d < D; d += 64) {
       float pm = 0.f;
-      for (int e = 0; e < D; ++e) pm = fmaf(P[d * D + e], mu[e], pm);
-      mpm = fmaf(mu[d], pm, mpm);
+      for (int e = 0; e < D; ++e) pm = fmaf(P[d * D + e], mus[e], pm);
+      mpm = fmaf(mus[d], pm, mpm);
       put_f32(S + d, -2.f * pm);
       for (int e = d; e < D; ++e)
         put_f32(sym_index(d, e, DP), d == e ? P[d * D + d] : P[d * D + e] + P[e * D + d]);
     }
-    colq = mpm;
+    colq = wave_sum(mpm);
     ca = -0.5f * kLog2e;
     cb = (lw - 0.5f * (log2pi_d + a.logdet[bk])) * kLog2e;
   }
   // l2 = ca * (rowq - 2S + colq) + cb (spherical, tied: S is the cross term x·μ / x·Pμ) or
   // ca * (S + colq) + cb (diag, full: W already carries the -2), stored as (ca, ca*colq + cb).
-  a.cconst[bk] = make_float4(ca, fmaf(ca, colq, cb), 0.f, 0.f);
+  if (lane == 0) a.cconst[bk] = make_float4(ca, fmaf(ca, colq, cb), 0.f, 0.f);
 }
 
 // ---------------------------------------------------------------------------
@@ -178,7 +186,23 @@ __device__ float jitter_of(int level) {
   return (float)j;
 }
 
-// Factorises sym(C) + jitter·I into Ls (lower triangle).  Returns success.
+// Dot product of length n of two LDS vectors with strides sa / sb, four
+// independent partial sums (the loads of consecutive terms overlap).
+__device__ __forceinline__ float lds_dot(const float* a, int sa, const float* b, int sb, int n) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int c = 0;
+  for (; c + 4 <= n; c += 4) {
+    s0 = fmaf(a[c * sa], b[c * sb], s0);
+    s1 = fmaf(a[(c + 1) * sa], b[(c + 1) * sb], s1);
+    s2 = fmaf(a[(c + 2) * sa], b[(c + 2) * sb], s2);
+    s3 = fmaf(a[(c + 3) * sa], b[(c + 3) * sb], s3);
+  }
+  for (; c < n; ++c) s0 = fmaf(a[c * sa], b[c * sb], s0);
+  return (s0 + s1) + (s2 + s3);
+}
+
+// Factorises sym(C) + jitter·I into Ls (lower triangle), left-looking: column j
+// is L_ij = (A_ij - Σ_{c<j} L_ic L_jc) / L_jj, one thread per row i.  Returns success.
 __device__ bool chol_factor(const float* C, int D, float jitter, float* Ls) {
   const int i = threadIdx.x;
   if (i < D) {
@@ -190,20 +214,17 @@ __device__ bool chol_factor(const float* C, int D, float jitter, float* Ls) {
   __syncthreads();
   bool ok = true;
   for (int j = 0; j < D; ++j) {
-    const float djj = Ls[j * kCS + j];
-    if (!(djj > 0.f)) { ok = false; break; }     // uniform across the block
+    // diagonal first (every thread computes it: the result is uniform)
+    const float djj = Ls[j * kCS + j] - lds_dot(Ls + j * kCS, 1, Ls + j * kCS, 1, j);
+    if (!(djj > 0.f)) { ok = false; break; }
     const float ljj = sqrtf(djj);
+    float lij = 0.f;
+    if (i > j && i < D) lij = (Ls[i * kCS + j] - lds_dot(Ls + i * kCS, 1, Ls + j * kCS, 1, j)) / ljj;
     __syncthreads();
     if (i == j) Ls[j * kCS + j] = ljj;
-    if (i > j && i < D) Ls[i * kCS + j] = Ls[i * kCS + j] / ljj;
-    __syncthreads();
-    if (i > j && i < D) {
-      const float lij = Ls[i * kCS + j];
-      for (int c = j + 1; c <= i; ++c) Ls[i * kCS + c] -= lij * Ls[c * kCS + j];
-    }
+    if (i > j && i < D) Ls[i * kCS + j] = lij;
     __syncthreads();
   }
-  __syncthreads();
   return ok;
 }
 
@@ -232,24 +253,22 @@ __global__ void chol_finish_kernel(const float* cov, int D, int M, const int* fi
   }
   __syncthreads();
   chol_factor(cov + (size_t)m * D * D, D, jitter_of(lvl_s), Ls);
-  // X = L^-1 (lower triangular), thread i computes column i by forward substitution.
+  // X = L^-1 (lower triangular), thread i computes column i by forward substitution:
+  // X_ri = -(Σ_{i<=c<r} L_rc X_ci) / L_rr.
   if (i < D) {
-    for (int r = 0; r < D; ++r) Xs[r * kCS + i] = 0.f;
+    for (int r = 0; r < i; ++r) Xs[r * kCS + i] = 0.f;
     Xs[i * kCS + i] = 1.f / Ls[i * kCS + i];
-    for (int r = i + 1; r < D; ++r) {
-      float s = 0.f;
-      for (int c = i; c < r; ++c) s = fmaf(Ls[r * kCS + c], Xs[c * kCS + i], s);
-      Xs[r * kCS + i] = -s / Ls[r * kCS + r];
-    }
+    for (int r = i + 1; r < D; ++r)
+      Xs[r * kCS + i] = -lds_dot(Ls + r * kCS + i, 1, Xs + i * kCS + i, kCS, r - i) / Ls[r * kCS + r];
   }
   __syncthreads();
-  // P = Xᵀ X: P[i][j] = Σ_{r >= max(i,j)} X[r][i] X[r][j]; symmetric by construction.
+  // P = Xᵀ X: P_ij = Σ_{r >= max(i,j)} X_ri X_rj, symmetric.  Thread i forms column i
+  // (P_ji for every j), so each store instruction writes one contiguous row of P.
   if (i < D) {
     float* Pm = prec + (size_t)m * D * D;
     for (int j = 0; j < D; ++j) {
-      float s = 0.f;
-      for (int r = (i > j ? i : j); r < D; ++r) s = fmaf(Xs[r * kCS + i], Xs[r * kCS + j], s);
-      Pm[i * D + j] = s;
+      const int r0 = i > j ? i : j;
+      Pm[j * D + i] = lds_dot(Xs + r0 * kCS + i, kCS, Xs + r0 * kCS + j, kCS, D - r0);
     }
   }
   if (i == 0) {
@@ -518,8 +537,7 @@ __global__ void canary_kernel(const int32_t* in, int32_t* out, int64_t n, int32_
 namespace gx {
 
 void launch_prep(const PrepArgs& a, hipStream_t s) {
-  dim3 grid((a.K + 255) / 256, a.B);
-  prep_kernel<<<grid, 256, 0, s>>>(a);
+  prep_kernel<<<dim3(a.K, a.B), 64, 0, s>>>(a);
 }
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, float* logdet, hipStream_t s) {
