@@ -146,7 +146,8 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_pidx = take((size_t)q.ktiles * BN * 4);
   q.o_pstats = take((size_t)std::max(q.slices, q.fslices) * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
-  q.o_ll = take((size_t)q.B * std::max(q.cblocks, q.fslices) * 8);
+  // (+B: the tied EM iteration's per-batch log-likelihood shift, after the row partials)
+  q.o_ll = take((size_t)q.B * (std::max(q.cblocks, q.fslices) + 1) * 8);
   q.o_first = take((size_t)q.chol_m * 4);
   q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
   q.o_logdet = take((size_t)q.chol_m * 4);
@@ -172,7 +173,10 @@ int check_hip(const char* what) {
   return GMMXX_OK;
 }
 
-TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
+// em: the EM iteration's passes, whose tied logits leave out the per-row xᵀPx
+// (a row constant: responsibilities and labels do not depend on it, and the
+// log-likelihood takes it back as -½ tr(P XᵀX) in the combine phase).
+TileArgs tile_args(const Plan& pl, const void* x, void* ws, bool em = false) {
   TileArgs a{};
   a.x = x;
   a.vec_ok = (pl.D == pl.DP) && ((uintptr_t)x % 16 == 0);
@@ -186,7 +190,7 @@ TileArgs tile_args(const Plan& pl, const void* x, void* ws) {
   a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
   a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
-  a.rowq = pl.cov == TIED ? at<float>(ws, pl.o_rowq) : nullptr;
+  a.rowq = (pl.cov == TIED && !em) ? at<float>(ws, pl.o_rowq) : nullptr;
   a.lse2 = at<float>(ws, pl.o_lse2);
   a.rowaux = (pl.bf && pl.cov == SPH && pl.DP >= 128) ? at<uint4>(ws, pl.o_rowaux) : nullptr;
   a.part_ms = at<float>(ws, pl.o_pms);
@@ -224,7 +228,7 @@ int ll_parts(const Plan& pl) { return pl.B * (pl.fused ? pl.fparts : pl.cblocks)
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
 int prepare(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights,
-            double reg, double minw, int prelude, void* ws, hipStream_t s) {
+            double reg, double minw, int prelude, void* ws, hipStream_t s, bool rowquad = true) {
   float* prec = nullptr;
   float* logdet = nullptr;
   if (pl.cov == TIED || pl.cov == FULL) {
@@ -254,7 +258,7 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
   launch_prep(a, s);
-  if (pl.cov == TIED)
+  if (pl.cov == TIED && rowquad)
     launch_rowquad(reinterpret_cast<const float*>(x), pl.B, pl.N, pl.D, prec, at<float>(ws, pl.o_rowq), s);
   return check_hip("parameter preparation");
 }
@@ -337,9 +341,9 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
   const hipStream_t s = (hipStream_t)stream;
   switch (phase) {
     case GMMXX_PHASE_PREPARE:
-      return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s);
+      return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s, /*rowquad=*/false);
     case GMMXX_PHASE_LSE_TILE: {
-      const TileArgs t = tile_args(pl, x, ws);
+      const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if ((pl.fused ? run_fused(pl, t, s) : run_tile(pl, MODE_LSE, t, s)) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip(pl.fused ? "fused tile kernel" : "log-normaliser tile kernel");
@@ -359,13 +363,17 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       c.lse2 = at<float>(ws, pl.o_lse2);
       c.ll_part = at<double>(ws, pl.o_ll);
       launch_combine(c, s);
-      launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0 / ((double)pl.B * (double)pl.N),
-                       lower_bound, s);
+      int parts = pl.B * pl.cblocks;
+      if (pl.cov == TIED) {   // -½ tr(P XᵀX) per batch after the row partials
+        launch_tied_ll_shift(at<float>(ws, pl.o_prec), gram, pl.B, pl.D, at<double>(ws, pl.o_ll) + parts, s);
+        parts += pl.B;
+      }
+      launch_ll_reduce(at<double>(ws, pl.o_ll), parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
       return check_hip("combine");
     }
     case GMMXX_PHASE_STATS_TILE: {
       if (pl.fused) return GMMXX_OK;  // statistics came out of the fused pass
-      const TileArgs t = tile_args(pl, x, ws);
+      const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if (run_tile(pl, MODE_STATS, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip("statistics tile kernel");

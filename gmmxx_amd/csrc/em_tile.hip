@@ -281,7 +281,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         q = group_sum<CPR>(q);
         if (cc == 0) rowq_s[buf * kBN + r] = q;
       } else if constexpr (COV == TIED) {
-        if (cc == 0) rowq_s[buf * kBN + r] = (n < rend) ? a.rowq[(size_t)b * N + n] : 0.f;
+        // (no rowq: the EM iteration's logits leave the row constant xᵀPx out)
+        if (cc == 0) rowq_s[buf * kBN + r] = (n < rend && a.rowq) ? a.rowq[(size_t)b * N + n] : 0.f;
       } else {
         if (cc == 0) rowq_s[buf * kBN + r] = 0.f;
       }

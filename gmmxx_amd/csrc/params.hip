@@ -342,6 +342,20 @@ __global__ void combine_kernel(CombineArgs a) {
   if (threadIdx.x == 0 && a.ll_part) a.ll_part[(size_t)b * gridDim.x + blockIdx.x] = t;
 }
 
+// Tied EM iteration: the logits leave out the per-row xᵀPx, so the row
+// log-normalisers are each too large by ½ xᵀPx; their sum is taken back here
+// as -½ Σ_n x_nᵀ P x_n = -½ Σ_ij P_ij (XᵀX)_ij.
+__global__ void tied_ll_shift_kernel(const float* prec, const float* gram, int D, double* out) {
+  __shared__ double scratch[32];
+  const int b = blockIdx.x;
+  const float* P = prec + (size_t)b * D * D;
+  const float* G = gram + (size_t)b * D * D;
+  double s = 0.0;
+  for (int i = threadIdx.x; i < D * D; i += blockDim.x) s += (double)P[i] * (double)G[i];
+  const double t = block_sum(s, scratch);
+  if (threadIdx.x == 0) out[b] = -0.5 * t;
+}
+
 // Mean log-likelihood over all B*N rows (lower bound of the iteration).
 __global__ void ll_reduce_kernel(const double* ll_part, int count, double inv_total, float* out) {
   __shared__ double scratch[32];
@@ -538,6 +552,10 @@ namespace gx {
 
 void launch_prep(const PrepArgs& a, hipStream_t s) {
   prep_kernel<<<dim3(a.K, a.B), 64, 0, s>>>(a);
+}
+
+void launch_tied_ll_shift(const float* prec, const float* gram, int B, int D, double* out, hipStream_t s) {
+  tied_ll_shift_kernel<<<B, 256, 0, s>>>(prec, gram, D, out);
 }
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, float* logdet, hipStream_t s) {
