@@ -173,7 +173,9 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
 // chol_finish: the batch-global level is the largest first level (all
 //              matrices factorise there); refactorise at it and form
 //              P = L^-T L^-1 and log det = 2 Σ log L_jj.
-// One workgroup of 64 threads per matrix, one thread per row, D <= 64.
+// One workgroup of 256 threads per matrix (D <= 64): the factorisation and the
+// triangular inverse run one thread per row / column, the staging of C and the
+// product P = XᵀX use every thread.
 // ---------------------------------------------------------------------------
 
 constexpr int kMaxCholD = 64;
@@ -203,13 +205,16 @@ __device__ __forceinline__ float lds_dot(const float* a, int sa, const float* b,
 
 // Factorises sym(C) + jitter·I into Ls (lower triangle), left-looking: column j
 // is L_ij = (A_ij - Σ_{c<j} L_ic L_jc) / L_jj, one thread per row i.  Returns success.
+// C is staged with coalesced loads by the whole block; the lower triangle is then
+// symmetrised in place (it reads only the untouched upper triangle).
 __device__ bool chol_factor(const float* C, int D, float jitter, float* Ls) {
   const int i = threadIdx.x;
-  if (i < D) {
-    for (int j = 0; j < D; ++j) {
-      const float s = 0.5f * (C[i * D + j] + C[j * D + i]);
-      Ls[i * kCS + j] = (i == j) ? s + jitter : s;
-    }
+  for (int o = i; o < D * D; o += blockDim.x) Ls[(o / D) * kCS + o % D] = C[o];
+  __syncthreads();
+  for (int o = i; o < D * D; o += blockDim.x) {
+    const int r = o / D, c = o % D;
+    if (c < r) Ls[r * kCS + c] = 0.5f * (Ls[r * kCS + c] + Ls[c * kCS + r]);
+    else if (c == r) Ls[r * kCS + r] += jitter;
   }
   __syncthreads();
   bool ok = true;
@@ -262,13 +267,14 @@ __global__ void chol_finish_kernel(const float* cov, int D, int M, const int* fi
       Xs[r * kCS + i] = -lds_dot(Ls + r * kCS + i, 1, Xs + i * kCS + i, kCS, r - i) / Ls[r * kCS + r];
   }
   __syncthreads();
-  // P = Xᵀ X: P_ij = Σ_{r >= max(i,j)} X_ri X_rj, symmetric.  Thread i forms column i
-  // (P_ji for every j), so each store instruction writes one contiguous row of P.
-  if (i < D) {
+  // P = Xᵀ X: P_ij = Σ_{r >= max(i,j)} X_ri X_rj, symmetric; every thread of the
+  // block forms entries, consecutive threads consecutive entries of one row.
+  {
     float* Pm = prec + (size_t)m * D * D;
-    for (int j = 0; j < D; ++j) {
-      const int r0 = i > j ? i : j;
-      Pm[j * D + i] = lds_dot(Xs + r0 * kCS + i, kCS, Xs + r0 * kCS + j, kCS, D - r0);
+    for (int o = i; o < D * D; o += blockDim.x) {
+      const int pi = o % D, pj = o / D;
+      const int r0 = pi > pj ? pi : pj;
+      Pm[pj * D + pi] = lds_dot(Xs + r0 * kCS + pi, kCS, Xs + r0 * kCS + pj, kCS, D - r0);
     }
   }
   if (i == 0) {
@@ -559,8 +565,8 @@ void launch_tied_ll_shift(const float* prec, const float* gram, int B, int D, do
 }
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, float* logdet, hipStream_t s) {
-  chol_try_kernel<<<M, 64, 0, s>>>(cov, D, first_ok);
-  chol_finish_kernel<<<M, 64, 0, s>>>(cov, D, M, first_ok, prec, logdet);
+  chol_try_kernel<<<M, 256, 0, s>>>(cov, D, first_ok);
+  chol_finish_kernel<<<M, 256, 0, s>>>(cov, D, M, first_ok, prec, logdet);
 }
 
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s) {
