@@ -219,6 +219,15 @@ def _traffic_from_profile(name, phase):
     return vals.get(key)
 
 
+def kernel_label(cfg, phase):
+    """Name of the kernel that runs in `phase` for this config (see gmmxx_amd/csrc)."""
+    if cfg["cov"] == "spherical" and cfg["dtype"] == "bf16":
+        if cfg["D"] <= 64 and cfg["K"] <= 64:
+            return "sph_bf16_fused_kernel (fused pass)"
+        return f"sph_bf16_kernel ({phase})"
+    return f"em_tile_kernel ({phase})"
+
+
 def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
     from gmmxx_amd import _hip
     cfg = CONFIGS[name]
@@ -283,7 +292,7 @@ def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
         "steps": steps, "warmup": warmup, "ms_per_iter": ms_per_step, "iter_per_s": 1e3 / ms_per_step,
         "gflop_per_s": fl["iteration"] / (ms_per_step * 1e-3) / 1e9,
         "roofline": {"bound": "hbm" if bound == "hbm" else "mfma", "peak_kind": bound,
-                     "kernel": f"em_tile ({dominant})", "achieved": achieved, "peak": peak, "unit": unit,
+                     "kernel": kernel_label(cfg, dominant), "achieved": achieved, "peak": peak, "unit": unit,
                      "frac": achieved / peak, "traffic": _traffic_from_profile(name, dominant)},
         "em_iteration": {"algorithmic_tflop": fl["iteration"] / 1e12, "achieved": it_rate, "unit": it_unit,
                          "frac": it_rate / peak, "phase_ms": phase_ms},

@@ -442,24 +442,29 @@ __global__ void finalize_kernel(FinalizeArgs a) {
 }
 
 // Tied: Σ = sym((XᵀX − Σ_k n_k μ_k μ_kᵀ) / N) + reg·I   (torch_fallback.py:3159-3162)
+// One block per (row d, batch b), one thread per column e; four partial sums
+// over the components keep the loads in flight.  s_de is formed with the same
+// products in the same order for (d, e) and (e, d), so the result is symmetric.
 __global__ void finalize_tied_kernel(FinalizeArgs a) {
-  const int b = blockIdx.y;
+  const int b = blockIdx.y, d = blockIdx.x, e = threadIdx.x;
   const int K = a.K, D = a.D, JP = a.JP;
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= D * D) return;
-  const int d = t / D, e = t % D;
-  const float* st = a.stats + (size_t)b * K * JP;
+  if (e >= D) return;
+  const float* st = a.stats + (size_t)b * K * JP + a.nk_col;
   const float* mu = a.means + (size_t)b * K * D;
-  float sde = 0.f, sed = 0.f;
-  for (int k = 0; k < K; ++k) {
-    const float nk = st[(size_t)k * JP + a.nk_col];
-    sde += nk * (mu[k * D + d] * mu[k * D + e]);
-    sed += nk * (mu[k * D + e] * mu[k * D + d]);
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int k = 0;
+  for (; k + 4 <= K; k += 4) {
+    s0 = fmaf(st[(size_t)k * JP], mu[k * D + d] * mu[k * D + e], s0);
+    s1 = fmaf(st[(size_t)(k + 1) * JP], mu[(k + 1) * D + d] * mu[(k + 1) * D + e], s1);
+    s2 = fmaf(st[(size_t)(k + 2) * JP], mu[(k + 2) * D + d] * mu[(k + 2) * D + e], s2);
+    s3 = fmaf(st[(size_t)(k + 3) * JP], mu[(k + 3) * D + d] * mu[(k + 3) * D + e], s3);
   }
+  for (; k < K; ++k) s0 = fmaf(st[(size_t)k * JP], mu[k * D + d] * mu[k * D + e], s0);
+  const float sde = (s0 + s1) + (s2 + s3);
   const float* G = a.gram + (size_t)b * D * D;
   const float ade = (G[d * D + e] - sde) / (float)a.N;
-  const float aed = (G[e * D + d] - sed) / (float)a.N;
-  a.covs[(size_t)b * D * D + t] = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
+  const float aed = (G[e * D + d] - sde) / (float)a.N;
+  a.covs[(size_t)b * D * D + d * D + e] = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
 }
 
 // Full: Σ_k = sym((Σ r xxᵀ − n_k μμᵀ) / max(n_k, floor)) + reg·I, kept if inactive (:3150-3158)
@@ -612,7 +617,7 @@ void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, 
 
 void launch_finalize(const FinalizeArgs& a, hipStream_t s) {
   finalize_kernel<<<dim3((a.K + 255) / 256, a.B), 256, 0, s>>>(a);
-  if (a.cov == TIED) finalize_tied_kernel<<<dim3((a.D * a.D + 255) / 256, a.B), 256, 0, s>>>(a);
+  if (a.cov == TIED) finalize_tied_kernel<<<dim3(a.D, a.B), 64, 0, s>>>(a);
   if (a.cov == FULL) finalize_full_kernel<<<dim3(a.K, a.B), 256, 0, s>>>(a);
 }
 
