@@ -79,7 +79,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   const int S = q.DP * (q.DP + 1) / 2;
   const int E = (q.cov == SPH || q.cov == TIED) ? q.DP : (q.cov == DIAG ? 2 * q.DP : S + q.DP);
   const int J = (q.cov == SPH) ? q.DP + 3 : (q.cov == DIAG ? 2 * q.DP + 1 : (q.cov == TIED ? q.DP + 1 : q.DP + S + 1));
-  q.EP = round_up(E, q.bf ? 32 : 16);
+  q.EP = round_up(E, 32);
   q.JP = round_up(J, 16);
   q.nk_col = (q.cov == SPH) ? q.DP : (q.cov == DIAG ? 2 * q.DP : (q.cov == TIED ? q.DP : q.DP + S));
   q.sq_col = q.DP + 1;

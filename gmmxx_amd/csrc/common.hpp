@@ -30,7 +30,7 @@ struct Dims {
   static constexpr int S = DP * (DP + 1) / 2;
   static constexpr int E = (COV == SPH || COV == TIED) ? DP : (COV == DIAG ? 2 * DP : S + DP);
   static constexpr int J = (COV == SPH) ? DP + 3 : (COV == DIAG ? 2 * DP + 1 : (COV == TIED ? DP + 1 : DP + S + 1));
-  static constexpr int EP = round_up(E, BF ? 32 : 16);
+  static constexpr int EP = round_up(E, 32);   // whole 32-deep bf16 MFMA k-steps
   static constexpr int JP = round_up(J, 16);
   // Column of N_k in the statistics row.
   static constexpr int NK_COL = (COV == SPH) ? DP : (COV == DIAG ? 2 * DP : (COV == TIED ? DP : DP + S));

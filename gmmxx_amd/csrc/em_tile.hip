@@ -48,6 +48,22 @@ __host__ __device__ constexpr int cw_for() {
 template <typename T>
 __device__ __forceinline__ T ld16(const void* p) { return *reinterpret_cast<const T*>(p); }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// (a, b) split into three bf16 parts each, v = v1 + v2 + v3 exactly; part p of
+// both values packed into qp (a in the low half).
+__device__ __forceinline__ void split3x2(float a, float b, uint32_t& q1, uint32_t& q2, uint32_t& q3) {
+  const f32x2 v = f32x2{a, b};
+  const bf16x2 h = __builtin_convertvector(v, bf16x2);
+  const f32x2 r = v - __builtin_convertvector(h, f32x2);
+  const bf16x2 m = __builtin_convertvector(r, bf16x2);
+  const bf16x2 l = __builtin_convertvector(r - __builtin_convertvector(m, f32x2), bf16x2);
+  q1 = __builtin_bit_cast(uint32_t, h);
+  q2 = __builtin_bit_cast(uint32_t, m);
+  q3 = __builtin_bit_cast(uint32_t, l);
+}
+
 // Lane maxima start at this floor instead of -inf so merges need no guards;
 // invalid components still contribute exp2(-inf - m) = 0.
 constexpr float kLogFloor = -1e30f;
@@ -129,7 +145,10 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr bool PSI_LDS = BF && MODE == MODE_STATS;     // materialised ψᵀ (bf16 spherical)
   // Block i+1's E-GEMM overlaps block i's epilogue (off where it would not fit
   // the LDS budget (full) or the register file (diag at D = 128)).
-  constexpr bool PIPE = COV != FULL && !(COV == DIAG && DP >= 128);
+  // The split-bf16 statistics pass keeps three W parts resident: no second
+  // accumulator set at E-step widths of 128 and more.
+  constexpr bool PIPE = COV != FULL && !(COV == DIAG && DP >= 128) &&
+                        !(!BF && MODE == MODE_STATS && Dims<COV, DP, BF>::EP >= 128);
   constexpr int PD = PIPE ? 2 : 1;                       // loader runs PD blocks ahead
   constexpr int NB = PD + 1;                             // staged-row buffers
   constexpr int XS = DP + (BF ? 8 : 4);                  // staged-row stride, elements
@@ -138,8 +157,24 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   using FT = typename std::conditional<BF, __bf16, float>::type;
   using WF = typename std::conditional<BF, bf16x8, f32x4>::type;
   static_assert(NCH % 64 == 0, "row block must split into whole waves of chunks");
+  // Split-bf16 E-GEMM (fp32 x, log-normaliser passes): the E-step features φ and W
+  // are each split into three bf16 parts (v = v1 + v2 + v3 exactly) and the
+  // product runs as six 16x16x32 bf16 MFMAs per 32-deep k-step, keeping every
+  // cross term down to 2^-24 relative -- fp32 accuracy at 6/16 of the cost of
+  // the fp32 MFMA.  φ parts are staged once per block for all waves.
+  // Every pass of a shape uses the same E-GEMM, so all of them see identical logits
+  // (off for diag at D = 128: its three staged φ parts would not fit the LDS).
+  constexpr bool X3 = !BF && COV != FULL && !(COV == DIAG && DP >= 128);
+  constexpr int X3K = EP / 32;                           // k-steps of the split E-GEMM
+  constexpr int EPS = EP + 16;                           // split-φ row stride (s ≡ 8 or 24 mod 32 dwords)
+  constexpr int X3P = NB * kBN * EPS;                    // one part, all buffers
+  // Wide statistics passes keep W's third part in LDS (per wave, in the exact
+  // per-lane fragment order) to stay within the register file.
+  constexpr bool W3L = X3 && MODE == MODE_STATS && EP >= 128;
 
-  __shared__ __align__(16) XT xs[COV == FULL ? 8 : NB * kBN * XS];
+  __shared__ __align__(16) XT xs[(COV == FULL || (X3 && LSE)) ? 8 : NB * kBN * XS];   // ψ source (fp32 rows)
+  __shared__ __align__(16) __bf16 phx[X3 ? 3 * X3P : 8];
+  __shared__ __align__(16) bf16x8 w3s[W3L ? 8 * (CW / 16) * X3K * 64 : 1];   // [wave][ct][ec][lane]
   __shared__ __align__(16) float phi[COV == FULL ? NB * kBN * PS : 4];
   __shared__ __align__(16) FT psiT[PSI_LDS ? 2 * JP * QS : 8];
   __shared__ float rowq_s[NB * kBN];
@@ -167,10 +202,38 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   const int64_t rend = (rbeg + a.rows_per_slice < N) ? rbeg + a.rows_per_slice : N;
 
   // ---- resident E-step operand and per-component constants ----
-  WF whi[CT][ECH];
+  // (split-bf16: w3[p][ct][ec] = part p of W[16ct + li][32ec + 8g .. +7])
+  bf16x8 w3[X3 ? (W3L ? 2 : 3) : 1][X3 ? CT : 1][X3 ? X3K : 1];
+  if constexpr (X3) {
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const int kk = kbase + 16 * ct + li;
+#pragma unroll
+      for (int ec = 0; ec < X3K; ++ec) {
+        f32x4 lo4 = f32x4{0.f, 0.f, 0.f, 0.f}, hi4 = lo4;
+        if (kk < K) {
+          const float* wp = reinterpret_cast<const float*>(a.w_hi) + ((size_t)b * K + kk) * EP + 32 * ec + 8 * g;
+          lo4 = ld16<f32x4>(wp);
+          hi4 = ld16<f32x4>(wp + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = j < 4 ? lo4[j] : hi4[j - 4];
+          const __bf16 p1 = (__bf16)v;
+          const float r1 = v - (float)p1;
+          const __bf16 p2 = (__bf16)r1;
+          w3[0][ct][ec][j] = p1;
+          w3[1][ct][ec][j] = p2;
+          if constexpr (W3L) w3s[((wave * CT + ct) * X3K + ec) * 64 + lane][j] = (__bf16)(r1 - (float)p2);
+          else w3[W3L ? 0 : 2][ct][ec][j] = (__bf16)(r1 - (float)p2);
+        }
+      }
+    }
+  }
+  WF whi[X3 ? 1 : CT][X3 ? 1 : ECH];
   WF wlo[BF ? CT : 1][BF ? ECH : 1];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) {
+  for (int ct = 0; ct < (X3 ? 0 : CT); ++ct) {
     const int kk = kbase + 16 * ct + li;
 #pragma unroll
     for (int ec = 0; ec < ECH; ++ec) {
@@ -231,6 +294,13 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       psiT[bufi * JP * QS + j * QS + rem % QS] = (FT)(j == DP ? 1.f : 0.f);
     }
   }
+  if constexpr (X3) {
+    constexpr int E = Dm::E;
+    for (int i = tid; i < 3 * NB * kBN * (EP - E); i += nthr) {
+      const int row = i / (EP - E), c = E + i % (EP - E);
+      phx[row * EPS + c] = (__bf16)0.f;   // row runs over every part and buffer
+    }
+  }
   if constexpr (COV == FULL) {
     for (int i = tid; i < NB * kBN * (EP - S - DP); i += nthr) {
       const int row = i / (EP - S - DP), c = i % (EP - S - DP);
@@ -271,7 +341,28 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       float v[VEC];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[j] = to_f32(t.e[j]);
-      if constexpr (COV != FULL) {
+      if constexpr (X3) {
+        // φ features of these VEC columns, split into three bf16 parts.
+        auto put3 = [&](int col, const float (&f)[VEC]) {
+          uint32_t q1[VEC / 2], q2[VEC / 2], q3[VEC / 2];
+#pragma unroll
+          for (int j = 0; j < VEC; j += 2) split3x2(f[j], f[j + 1], q1[j / 2], q2[j / 2], q3[j / 2]);
+          __bf16* base = phx + (buf * kBN + r) * EPS + col;
+          *reinterpret_cast<uint2*>(base) = make_uint2(q1[0], q1[1]);
+          *reinterpret_cast<uint2*>(base + X3P) = make_uint2(q2[0], q2[1]);
+          *reinterpret_cast<uint2*>(base + 2 * X3P) = make_uint2(q3[0], q3[1]);
+        };
+        if constexpr (COV == DIAG) {
+          float sq[VEC];
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) sq[j] = v[j] * v[j];
+          put3(cc, sq);
+          put3(DP + cc, v);
+        } else {
+          put3(cc, v);
+        }
+      }
+      if constexpr (COV != FULL && !(X3 && LSE)) {
         *reinterpret_cast<uint4*>(&xs[buf * kBN * XS + r * XS + cc]) = raw;
       }
       if constexpr (COV == SPH) {
@@ -407,6 +498,36 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     Acc A;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) { A.t[ct][0] = f32x4{0.f, 0.f, 0.f, 0.f}; A.t[ct][1] = A.t[ct][0]; }
+    if constexpr (X3) {
+      // Six products per k-step, the smallest first: W1φ3, W3φ1, W2φ2, W1φ2, W2φ1, W1φ1.
+#pragma unroll
+      for (int ec = 0; ec < X3K; ++ec) {
+        bf16x8 xv[3][2];
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            xv[p][h] = ld16<bf16x8>(&phx[p * X3P + (bx * kBN + 16 * h + li) * EPS + 32 * ec + 8 * g]);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            // LSE: C = W·φᵀ (lane: components 4g + v of row li); otherwise C = φ·Wᵀ
+            // (lane: rows 4g + v of component li), the M-GEMM's A-operand layout.
+            auto mm = [&](const bf16x8& w, const bf16x8& x, const f32x4& c) {
+              return LSE ? mfma_bf16(w, x, c) : mfma_bf16(x, w, c);
+            };
+            const bf16x8 wp3 = W3L ? w3s[((wave * CT + ct) * X3K + ec) * 64 + lane] : w3[W3L ? 0 : 2][ct][ec];
+            A.t[ct][h] = mm(w3[0][ct][ec], xv[2][h], A.t[ct][h]);
+            A.t[ct][h] = mm(wp3, xv[0][h], A.t[ct][h]);
+            A.t[ct][h] = mm(w3[1][ct][ec], xv[1][h], A.t[ct][h]);
+            A.t[ct][h] = mm(w3[0][ct][ec], xv[1][h], A.t[ct][h]);
+            A.t[ct][h] = mm(w3[1][ct][ec], xv[0][h], A.t[ct][h]);
+            A.t[ct][h] = mm(w3[0][ct][ec], xv[0][h], A.t[ct][h]);
+          }
+      }
+      return A;
+    } else {
 #pragma unroll
     for (int ec = 0; ec < ECH; ++ec) {
       if constexpr (BF) {
@@ -444,6 +565,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       }
     }
     return A;
+    }
   };
 
   auto epilogue = [&](const Acc& A, int bx, int pb, int64_t n0) {
