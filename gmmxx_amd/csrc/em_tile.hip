@@ -64,6 +64,17 @@ __device__ __forceinline__ void split3x2(float a, float b, uint32_t& q1, uint32_
   q3 = __builtin_bit_cast(uint32_t, l);
 }
 
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// Transposing LDS read: in each 16-lane group, lane L supplies the address of
+// an 8-byte chunk; lane i receives word (i % 4) of the chunks of lanes 4j + i/4.
+__device__ __forceinline__ v4s tr16(const __bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+}
+__device__ __forceinline__ bf16x8 cat_v4s(v4s lo, v4s hi) {
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Lane maxima start at this floor instead of -inf so merges need no guards;
 // invalid components still contribute exp2(-inf - m) = 0.
 constexpr float kLogFloor = -1e30f;
@@ -172,7 +183,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   // per-lane fragment order) to stay within the register file.
   constexpr bool W3L = X3 && MODE == MODE_STATS && EP >= 128;
 
-  __shared__ __align__(16) XT xs[(COV == FULL || (X3 && LSE)) ? 8 : NB * kBN * XS];   // ψ source (fp32 rows)
+  __shared__ __align__(16) XT xs[(COV == FULL || X3) ? 8 : NB * kBN * XS];
   __shared__ __align__(16) __bf16 phx[X3 ? 3 * X3P : 8];
   __shared__ __align__(16) bf16x8 w3s[W3L ? 8 * (CW / 16) * X3K * 64 : 1];   // [wave][ct][ec][lane]
   __shared__ __align__(16) float phi[COV == FULL ? NB * kBN * PS : 4];
@@ -300,6 +311,12 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       const int row = i / (EP - E), c = E + i % (EP - E);
       phx[row * EPS + c] = (__bf16)0.f;   // row runs over every part and buffer
     }
+    // Augmented ψ columns EP..EP+15 (statistics pass): part 1 = [1 0 ...], parts 2, 3 = 0
+    // (spherical rows put their ‖x‖² parts at EP+1 when staged).
+    for (int i = tid; i < 3 * NB * kBN * 16; i += nthr) {
+      const int row = i / 16, c = i % 16;
+      phx[row * EPS + EP + c] = (__bf16)((c == 0 && row < NB * kBN) ? 1.f : 0.f);
+    }
   }
   if constexpr (COV == FULL) {
     for (int i = tid; i < NB * kBN * (EP - S - DP); i += nthr) {
@@ -362,7 +379,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
           put3(cc, v);
         }
       }
-      if constexpr (COV != FULL && !(X3 && LSE)) {
+      if constexpr (COV != FULL && !X3) {
         *reinterpret_cast<uint4*>(&xs[buf * kBN * XS + r * XS + cc]) = raw;
       }
       if constexpr (COV == SPH) {
@@ -371,6 +388,16 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         for (int j = 0; j < VEC; ++j) q = fmaf(v[j], v[j], q);
         q = group_sum<CPR>(q);
         if (cc == 0) rowq_s[buf * kBN + r] = q;
+        if constexpr (X3 && MODE == MODE_STATS) {
+          if (cc == 0) {
+            uint32_t q1, q2, q3;
+            split3x2(q, 0.f, q1, q2, q3);
+            __bf16* at = phx + (buf * kBN + r) * EPS + EP + 1;
+            *at = __builtin_bit_cast(__bf16, (uint16_t)q1);
+            at[X3P] = __builtin_bit_cast(__bf16, (uint16_t)q2);
+            at[2 * X3P] = __builtin_bit_cast(__bf16, (uint16_t)q3);
+          }
+        }
       } else if constexpr (COV == TIED) {
         // (no rowq: the EM iteration's logits leave the row constant xᵀPx out)
         if (cc == 0) rowq_s[buf * kBN + r] = (n < rend && a.rowq) ? a.rowq[(size_t)b * N + n] : 0.f;
@@ -622,7 +649,49 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
             const float l2 = logit(cS[ct], A.t[ct][rt][v], rowq_s[bx * kBN + r]);
             rr[ct][rt][v] = fast_exp2(l2 - lse_s[bx * kBN + r]);
           }
-      if constexpr (MODE == MODE_STATS) {
+      if constexpr (MODE == MODE_STATS && X3) {
+        // M-GEMM on split bf16 operands: r in three parts (A element j = 4rt + v is
+        // data row 16rt + 4g + v), ψ tiles read from the staged split φ rows with the
+        // transposing load (rows 4g..4g+3 and 16+4g..16+4g+3, the same order).
+        bf16x8 ra[3][CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          uint32_t q[3][4];
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; v += 2)
+              split3x2(rr[ct][rt][v], rr[ct][rt][v + 1], q[0][2 * rt + v / 2], q[1][2 * rt + v / 2],
+                       q[2][2 * rt + v / 2]);
+#pragma unroll
+          for (int p = 0; p < 3; ++p) ra[p][ct] = __builtin_bit_cast(bf16x8, make_uint4(q[p][0], q[p][1], q[p][2], q[p][3]));
+        }
+        // ψ tile jt = 16 consecutive φ columns (diag: x then x², spherical/tied: x) or the
+        // augmented columns at EP.
+        auto psi_col = [](int jt) {
+          constexpr int XT16 = DP / 16;
+          if constexpr (COV == DIAG) return jt < XT16 ? DP + 16 * jt : (jt < 2 * XT16 ? 16 * (jt - XT16) : EP);
+          else return jt < XT16 ? 16 * jt : EP;
+        };
+        const __bf16* tb = phx + (bx * kBN + 4 * g + (li >> 2)) * EPS + 4 * (li & 3);
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt) {
+          const int c0 = psi_col(jt);
+          bf16x8 bq[3];
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+            bq[p] = cat_v4s(tr16(tb + p * X3P + c0), tr16(tb + p * X3P + 16 * EPS + c0));
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[2], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[2][ct], bq[0], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[1][ct], bq[1], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[1], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[1][ct], bq[0], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[0], acc[ct][jt]);
+          }
+        }
+      } else if constexpr (MODE == MODE_STATS) {
         // M-GEMM: each ψ fragment is loaded once and used by every component tile.
         if constexpr (BF) {
           bf16x8 ar[CT];
