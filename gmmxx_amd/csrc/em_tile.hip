@@ -154,12 +154,11 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr int NCH = kBN * CPR;                         // chunks per row block
   constexpr int PF = (NCH + 511) / 512;                  // prefetched chunks per thread at 512 threads
   constexpr bool PSI_LDS = BF && MODE == MODE_STATS;     // materialised ψᵀ (bf16 spherical)
-  // Block i+1's E-GEMM overlaps block i's epilogue (off where it would not fit
-  // the LDS budget (full) or the register file (diag at D = 128)).
-  // The split-bf16 statistics pass keeps three W parts resident: no second
-  // accumulator set at E-step widths of 128 and more.
-  constexpr bool PIPE = COV != FULL && !(COV == DIAG && DP >= 128) &&
-                        !(!BF && MODE == MODE_STATS && Dims<COV, DP, BF>::EP >= 128);
+  // Block i+1's E-GEMM issued ahead of block i's epilogue: kept for the bf16
+  // path only.  The fp32 (split-bf16) passes measured equal or faster without
+  // it (C3 3.45 vs 3.47 ms, C4 0.87 vs 0.93 ms): MFMA and VALU time add up on
+  // this machine, and the second accumulator set only costs registers.
+  constexpr bool PIPE = BF && COV != FULL;
   constexpr int PD = PIPE ? 2 : 1;                       // loader runs PD blocks ahead
   constexpr int NB = PD + 1;                             // staged-row buffers
   constexpr int XS = DP + (BF ? 8 : 4);                  // staged-row stride, elements
