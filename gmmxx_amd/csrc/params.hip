@@ -174,8 +174,8 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
 //              matrices factorise there); refactorise at it and form
 //              P = L^-T L^-1 and log det = 2 Σ log L_jj.
 // One workgroup of 256 threads per matrix (D <= 64): the factorisation and the
-// triangular inverse run one thread per row / column, the staging of C and the
-// product P = XᵀX use every thread.
+// triangular inverse run four threads per row / column (quad reductions), the
+// staging of C and the product P = XᵀX use every thread.
 // ---------------------------------------------------------------------------
 
 constexpr int kMaxCholD = 64;
@@ -203,31 +203,45 @@ __device__ __forceinline__ float lds_dot(const float* a, int sa, const float* b,
   return (s0 + s1) + (s2 + s3);
 }
 
+// Sum over the 4 lanes of a quad (lanes 4i .. 4i+3), result in every lane.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // lane ^ 1
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // lane ^ 2
+  return v;
+}
+
 // Factorises sym(C) + jitter·I into Ls (lower triangle), left-looking: column j
-// is L_ij = (A_ij - Σ_{c<j} L_ic L_jc) / L_jj, one thread per row i.  Returns success.
-// C is staged with coalesced loads by the whole block; the lower triangle is then
-// symmetrised in place (it reads only the untouched upper triangle).
-__device__ bool chol_factor(const float* C, int D, float jitter, float* Ls) {
-  const int i = threadIdx.x;
-  for (int o = i; o < D * D; o += blockDim.x) Ls[(o / D) * kCS + o % D] = C[o];
+// is L_ij = (A_ij - Σ_{c<j} L_ic L_jc) / L_jj.  Four threads per row i (t = 4i + p)
+// each take the terms c ≡ p (mod 4) and a quad reduction joins them; tmp (LDS,
+// D floats) carries the column's numerators.  Returns success.  C is staged with
+// coalesced loads by the whole block; the lower triangle is then symmetrised in
+// place (it reads only the untouched upper triangle).
+__device__ bool chol_factor(const float* C, int D, float jitter, float* Ls, float* tmp) {
+  const int t = threadIdx.x, i = t >> 2, p = t & 3;
+  for (int o = t; o < D * D; o += blockDim.x) Ls[(o / D) * kCS + o % D] = C[o];
   __syncthreads();
-  for (int o = i; o < D * D; o += blockDim.x) {
+  for (int o = t; o < D * D; o += blockDim.x) {
     const int r = o / D, c = o % D;
     if (c < r) Ls[r * kCS + c] = 0.5f * (Ls[r * kCS + c] + Ls[c * kCS + r]);
     else if (c == r) Ls[r * kCS + r] += jitter;
   }
   __syncthreads();
   bool ok = true;
+  const bool row = i < D;
   for (int j = 0; j < D; ++j) {
-    // diagonal first (every thread computes it: the result is uniform)
-    const float djj = Ls[j * kCS + j] - lds_dot(Ls + j * kCS, 1, Ls + j * kCS, 1, j);
-    if (!(djj > 0.f)) { ok = false; break; }
-    const float ljj = sqrtf(djj);
-    float lij = 0.f;
-    if (i > j && i < D) lij = (Ls[i * kCS + j] - lds_dot(Ls + i * kCS, 1, Ls + j * kCS, 1, j)) / ljj;
+    float part = 0.f;
+    if (row && i >= j)
+      for (int c = p; c < j; c += 4) part = fmaf(Ls[i * kCS + c], Ls[j * kCS + c], part);
+    const float sum = quad_sum(part);
+    if (row && i >= j && p == 0) tmp[i] = Ls[i * kCS + j] - sum;
     __syncthreads();
-    if (i == j) Ls[j * kCS + j] = ljj;
-    if (i > j && i < D) Ls[i * kCS + j] = lij;
+    const float djj = tmp[j];
+    if (!(djj > 0.f)) { ok = false; break; }     // uniform across the block
+    const float ljj = sqrtf(djj);
+    if (row && p == 0) {
+      if (i == j) Ls[j * kCS + j] = ljj;
+      else if (i > j) Ls[i * kCS + j] = tmp[i] / ljj;
+    }
     __syncthreads();
   }
   return ok;
@@ -235,11 +249,12 @@ __device__ bool chol_factor(const float* C, int D, float jitter, float* Ls) {
 
 __global__ void chol_try_kernel(const float* cov, int D, int* first_ok) {
   __shared__ float Ls[kMaxCholD * kCS];
+  __shared__ float tmp[kMaxCholD];
   const int m = blockIdx.x;
   const float* C = cov + (size_t)m * D * D;
   int level = 7;
   for (int l = 0; l < 7; ++l) {
-    if (chol_factor(C, D, jitter_of(l), Ls)) { level = l; break; }
+    if (chol_factor(C, D, jitter_of(l), Ls, tmp)) { level = l; break; }
   }
   if (threadIdx.x == 0) first_ok[m] = level;
 }
@@ -248,6 +263,7 @@ __global__ void chol_finish_kernel(const float* cov, int D, int M, const int* fi
                                    float* prec, float* logdet) {
   __shared__ float Ls[kMaxCholD * kCS];
   __shared__ float Xs[kMaxCholD * kCS];
+  __shared__ float tmp[kMaxCholD];
   __shared__ int lvl_s;
   const int m = blockIdx.x;
   const int i = threadIdx.x;
@@ -257,14 +273,22 @@ __global__ void chol_finish_kernel(const float* cov, int D, int M, const int* fi
     lvl_s = lv > 6 ? 6 : lv;
   }
   __syncthreads();
-  chol_factor(cov + (size_t)m * D * D, D, jitter_of(lvl_s), Ls);
-  // X = L^-1 (lower triangular), thread i computes column i by forward substitution:
-  // X_ri = -(Σ_{i<=c<r} L_rc X_ci) / L_rr.
-  if (i < D) {
-    for (int r = 0; r < i; ++r) Xs[r * kCS + i] = 0.f;
-    Xs[i * kCS + i] = 1.f / Ls[i * kCS + i];
-    for (int r = i + 1; r < D; ++r)
-      Xs[r * kCS + i] = -lds_dot(Ls + r * kCS + i, 1, Xs + i * kCS + i, kCS, r - i) / Ls[r * kCS + r];
+  chol_factor(cov + (size_t)m * D * D, D, jitter_of(lvl_s), Ls, tmp);
+  // X = L^-1 (lower triangular) by forward substitution, X_ri = -(Σ_{i<=c<r} L_rc X_ci) / L_rr:
+  // column ci = i / 4 by a quad of threads, each taking the terms c ≡ ci + p (mod 4).
+  // The four lanes of a quad run the same trip counts and all store the same X_ri
+  // (one wave: the stores land before the next step's loads).
+  {
+    const int ci = i >> 2, p = i & 3;
+    if (ci < D) {
+      for (int r = p; r < ci; r += 4) Xs[r * kCS + ci] = 0.f;
+      Xs[ci * kCS + ci] = 1.f / Ls[ci * kCS + ci];
+      for (int r = ci + 1; r < D; ++r) {
+        float part = 0.f;
+        for (int c = ci + p; c < r; c += 4) part = fmaf(Ls[r * kCS + c], Xs[c * kCS + ci], part);
+        Xs[r * kCS + ci] = -quad_sum(part) / Ls[r * kCS + r];
+      }
+    }
   }
   __syncthreads();
   // P = Xᵀ X: P_ij = Σ_{r >= max(i,j)} X_ri X_rj, symmetric; every thread of the
