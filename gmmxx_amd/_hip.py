@@ -161,7 +161,10 @@ def _device_tensor(t: torch.Tensor, name: str, dtype: Optional[torch.dtype] = No
         raise ValueError(f"{name}: must be on a GPU device, got {t.device}")
     if dtype is not None and t.dtype != dtype:
         raise ValueError(f"{name}: dtype must be {dtype}, got {t.dtype}")
-    return t.contiguous()
+    t = t.contiguous()
+    # The library reads rows with 16-byte loads (and requires it for spherical bf16 at
+    # D = 128): a view that starts mid-allocation is copied to an aligned buffer.
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 class Workspace:

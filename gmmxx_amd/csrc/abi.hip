@@ -6,6 +6,8 @@
 
 #include <stdint.h>
 
+#include <stdlib.h>
+
 #include <algorithm>
 #include <string>
 
@@ -31,6 +33,9 @@ struct Plan {
   int DP = 0, EP = 0, JP = 0, nk_col = 0, sq_col = 0, sq_n = 0, CW = 0, nw = 0, ktiles = 0, slices = 0, cblocks = 0;
   int lnw = 0, lktiles = 0;  // waves / component tiles of the plain log-normaliser pass (MODE_LSE)
   bool fused = false;        // EM iteration as one fused pass (small K; em_fused.hip)
+  bool coop = false;         // EM iteration as one cooperative pass (spherical bf16, D = 128; em_coop.hip)
+  int cG = 0, cNG = 0, cspb = 0;   // coop: workgroups per group, groups, row items per batch
+  int64_t crows = 0;         // coop: rows per item
   int fslices = 0;           // fused: one wave per row slice
   int fparts = 0;            // fused: partial results (one per workgroup of kFusedWaves slices)
   int64_t frows = 0;
@@ -39,6 +44,7 @@ struct Plan {
   int64_t gram_rows = 0;
   int chol_m = 0;
   size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
+  size_t o_xch = 0, o_flags = 0;
   size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_prec = 0, o_logdet = 0, o_gram = 0, total = 0;
 };
 
@@ -122,6 +128,30 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
     q.fslices = (int)((q.N + q.frows - 1) / q.frows);
     q.fparts = (q.fslices + kFusedWaves - 1) / kFusedWaves;
   }
+  // Cooperative single pass: spherical bf16 at D = 128 with 256 < K <= 1024
+  // (groups of 2..4 workgroups; at one group member and at eight the two-pass
+  // kernels measured faster).  Group members must be co-resident, so the grid is
+  // the device's resident capacity rounded to whole groups (multiples of 8
+  // groups keep each group on one XCD).  GMMXX_HIP_NO_COOP=1 selects the
+  // two-pass kernels instead.
+  const char* no_coop = getenv("GMMXX_HIP_NO_COOP");
+  q.coop = sph_bf && q.DP == 128 && q.D == 128 && q.K > kCoopComps && q.K <= kCoopComps * kMaxCoopGroup &&
+           !(no_coop && no_coop[0] == '1');
+  if (q.coop) {
+    q.cG = (q.K + kCoopComps - 1) / kCoopComps;
+    int ng = coop_capacity() / q.cG;
+    if (ng >= 8) ng -= ng % 8;
+    q.cNG = ng;
+    q.coop = ng >= 1;
+  }
+  if (q.coop) {
+    int64_t spb = std::max<int64_t>(1, q.cNG / q.B);
+    spb = std::min(spb, std::max<int64_t>(1, row_blocks / kMinBlocksPerSlice));
+    // An item is addressed with 32-bit offsets: keep it under 2^30 bytes of x.
+    spb = std::max<int64_t>(spb, (q.N * q.DP * 2 + (int64_t(1) << 30) - 1) >> 30);
+    q.crows = ((q.N + spb - 1) / spb + kBN - 1) / kBN * kBN;
+    q.cspb = (int)((q.N + q.crows - 1) / q.crows);
+  }
   int64_t gs = std::min<int64_t>(64, row_blocks);
   q.gram_rows = ((q.N + gs - 1) / gs + kBN - 1) / kBN * kBN;
   q.gram_slices = (int)((q.N + q.gram_rows - 1) / q.gram_rows);
@@ -144,10 +174,12 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_rowaux = take(sph_bf && q.DP >= 128 ? BN * 16 : 0);
   q.o_pms = take((size_t)std::max(q.ktiles, q.lktiles) * BN * 8);
   q.o_pidx = take((size_t)q.ktiles * BN * 4);
-  q.o_pstats = take((size_t)std::max(q.slices, q.fslices) * BK * q.JP * 4);
+  q.o_pstats = take((size_t)std::max({q.slices, q.fslices, q.cspb}) * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
   // (+B: the tied EM iteration's per-batch log-likelihood shift, after the row partials)
-  q.o_ll = take((size_t)q.B * (std::max(q.cblocks, q.fslices) + 1) * 8);
+  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb}) + 1) * 8);
+  q.o_xch = take(q.coop ? (size_t)q.cNG * kRing * q.cG * kBN * 8 : 0);
+  q.o_flags = take(q.coop ? 4 : 0);   // status word of the cooperative pass
   q.o_first = take((size_t)q.chol_m * 4);
   q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
   q.o_logdet = take((size_t)q.chol_m * 4);
@@ -219,12 +251,41 @@ int run_fused(const Plan& pl, const TileArgs& t, hipStream_t s) {
   u.rows_per_slice = pl.frows;
   return launch_sph_bf16_fused(pl.DP, pl.K, u, pl.fslices, s);
 }
-int stat_slices(const Plan& pl) { return pl.fused ? pl.fparts : pl.slices; }
+// Cooperative single pass: partial statistics per row item and partial log-likelihoods.
+int run_coop(const Plan& pl, const void* x, void* ws, hipStream_t s) {
+  if ((uintptr_t)x % 16 != 0)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned for spherical bf16 at D = 128");
+  CoopArgs c{};
+  c.x = x;
+  c.vec_ok = 1;
+  c.N = pl.N;
+  c.D = pl.D;
+  c.K = pl.K;
+  c.B = pl.B;
+  c.w_hi = at<void>(ws, pl.o_whi);
+  c.w_lo = at<void>(ws, pl.o_wlo);
+  c.w_aug = at<void>(ws, pl.o_waug);
+  c.G = pl.cG;
+  c.NG = pl.cNG;
+  c.spb = pl.cspb;
+  c.rows_per_item = pl.crows;
+  c.part_stats = at<float>(ws, pl.o_pstats);
+  c.ll_part = at<double>(ws, pl.o_ll);
+  c.xch = at<uint64_t>(ws, pl.o_xch);
+  c.status = at<unsigned>(ws, pl.o_flags);
+  c.spin_limit = 1 << 20;
+  const int rc = launch_sph_bf16_coop(pl.DP, c, s);
+  if (rc == -2) return fail(GMMXX_ERR_HIP, "cooperative launch of the single-pass kernel failed");
+  if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no cooperative kernel for this shape");
+  return check_hip("cooperative single-pass kernel");
+}
+const unsigned* coop_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags); }
+int stat_slices(const Plan& pl) { return pl.fused ? pl.fparts : (pl.coop ? pl.cspb : pl.slices); }
 // The tile-partial buffer is free once the statistics are being reduced: it is
 // the scratch of the grouped slice reduction.
 float* red_tmp(const Plan& pl, void* ws) { return at<float>(ws, pl.o_pms); }
 int64_t red_tmp_floats(const Plan& pl) { return (int64_t)std::max(pl.ktiles, pl.lktiles) * pl.B * pl.N * 2; }
-int ll_parts(const Plan& pl) { return pl.B * (pl.fused ? pl.fparts : pl.cblocks); }
+int ll_parts(const Plan& pl) { return pl.B * (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : pl.cblocks)); }
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
 int prepare(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights,
@@ -343,15 +404,17 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     case GMMXX_PHASE_PREPARE:
       return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s, /*rowquad=*/false);
     case GMMXX_PHASE_LSE_TILE: {
+      if (pl.coop) return run_coop(pl, x, ws, s);
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if ((pl.fused ? run_fused(pl, t, s) : run_tile(pl, MODE_LSE, t, s)) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip(pl.fused ? "fused tile kernel" : "log-normaliser tile kernel");
     }
     case GMMXX_PHASE_COMBINE: {
-      if (pl.fused) {  // the fused pass already produced per-slice log-likelihoods
+      if (pl.fused || pl.coop) {  // the single pass already produced per-slice log-likelihoods
         launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0 / ((double)pl.B * (double)pl.N),
                          lower_bound, s);
+        if (pl.coop) launch_coop_check(coop_status(pl, ws), lower_bound, s);
         return check_hip("log-likelihood reduction");
       }
       CombineArgs c{};
@@ -372,7 +435,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip("combine");
     }
     case GMMXX_PHASE_STATS_TILE: {
-      if (pl.fused) return GMMXX_OK;  // statistics came out of the fused pass
+      if (pl.fused || pl.coop) return GMMXX_OK;  // statistics came out of the single pass
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if (run_tile(pl, MODE_STATS, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
@@ -433,9 +496,14 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
-  if (pl.fused) {
-    if (run_fused(pl, tile_args(pl, x, ws), s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
+  if (pl.fused || pl.coop) {
+    if (pl.coop) {
+      if ((rc = run_coop(pl, x, ws, s))) return rc;
+    } else if (run_fused(pl, tile_args(pl, x, ws), s) != 0) {
+      return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
+    }
     launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0, ll_sum, s);
+    if (pl.coop) launch_coop_check(coop_status(pl, ws), ll_sum, s);
     launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                          at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
     if ((rc = check_hip("fused statistics pass"))) return rc;

@@ -40,4 +40,35 @@ int launch_sph_bf16(int dp, int nw, int mode, const TileArgs& a, dim3 grid, hipS
 constexpr int kFusedWaves = 4;
 int launch_sph_bf16_fused(int dp, int k, const TileArgs& a, int slices, hipStream_t s);
 
+// Single-pass cooperative kernel (em_coop.hip): spherical bf16 at D = 128 with
+// G = ceil(K / 256) workgroups per group of rows, 2 <= G <= kMaxCoopGroup
+// (256 < K <= 1024, where it measured faster than the two-pass kernels).
+constexpr int kCoopComps = 256;      // components per workgroup
+constexpr int kMaxCoopGroup = 4;
+constexpr int kRing = 4;             // exchange slots per group
+
+struct CoopArgs {
+  const void* x;               // [B][N][D] bf16
+  int vec_ok;
+  int64_t N;
+  int D, K, B;
+  const void* w_hi;            // [B][K][DP] bf16
+  const void* w_lo;
+  const void* w_aug;           // [B][K][32] bf16
+  int G;                       // workgroups per group
+  int NG;                      // groups (grid = NG * G)
+  int spb;                     // row items per batch
+  int64_t rows_per_item;       // multiple of 32
+  float* part_stats;           // [spb][B][K][JP]
+  double* ll_part;             // [B][spb] natural-log partial sums
+  uint64_t* xch;               // [NG][kRing][G][32] exchanged (max, ±sum) words, zeroed by the launcher
+  unsigned* status;            // nonzero after a timed-out wait (zeroed by the launcher)
+  int spin_limit;
+};
+// Resident workgroups of the cooperative kernel on the current device.
+int coop_capacity();
+int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s);
+// *value = NaN when the cooperative pass reported a timed-out wait (status != 0).
+void launch_coop_check(const unsigned* status, float* value, hipStream_t s);
+
 }  // namespace gx

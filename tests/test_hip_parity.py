@@ -70,7 +70,10 @@ CASES = [
     # cov, B, N, D, K, dtype  -- at least ~50 rows per component (well conditioned)
     ("spherical", 2, 6000, 32, 64, torch.float32),
     ("spherical", 1, 24000, 128, 300, torch.float32),     # two k-tiles, partial second tile
-    ("spherical", 1, 30000, 128, 520, torch.bfloat16),    # three k-tiles
+    ("spherical", 1, 30000, 128, 520, torch.bfloat16),    # single pass, groups of three workgroups
+    ("spherical", 1, 20000, 128, 256, torch.bfloat16),    # single pass, one workgroup per group (no exchange)
+    ("spherical", 2, 12345, 128, 1000, torch.bfloat16),   # single pass, groups of four, padded rows and components
+    ("spherical", 1, 40000, 128, 2048, torch.bfloat16),   # single pass, groups of eight (largest)
     ("spherical", 2, 6000, 32, 64, torch.bfloat16),        # fused single pass, whole-chunk rows
     ("spherical", 1, 5000, 20, 10, torch.bfloat16),        # fused, padded rows, one component tile
     ("spherical", 3, 4000, 50, 30, torch.bfloat16),        # fused, D 64 padded, two component tiles
@@ -231,6 +234,34 @@ def test_em_step_degenerate_accuracy(hip, case):
         print(f"  it {it}: truth {truth:.6f} hip {float(lb):.6f} oracle {e_lb:.6f}", flush=True)
         assert err_hip <= max(4.0 * err_ref, 1e-5 * abs(truth)), (it, truth, float(lb), e_lb)
         means, covs, w = e_m, e_c, e_w
+
+
+@pytest.mark.parametrize("k", [300, 1000])
+def test_single_pass_matches_two_pass(hip, monkeypatch, k):
+    """Spherical bf16 at D = 128: the cooperative single pass and the two-pass
+    tile kernels (GMMXX_HIP_NO_COOP=1) compute the same EM iteration; they differ
+    only in the order of the log-normaliser merge and in where r is rounded to
+    bf16, so parameters agree to 2e-3 relative and the lower bound to 1e-5."""
+    print(f"[single-vs-two-pass] K={k}", flush=True)
+    x, means, covs, w = make_problem("spherical", 1, 16000, 128, k, seed=21, dtype=torch.bfloat16)
+    xd = to_dev(x, torch.bfloat16)
+    out = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("GMMXX_HIP_NO_COOP", mode)
+        m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
+        lbs = []
+        for _ in range(3):
+            lb = torch.zeros(1, device=DEV)
+            hip.em_step("spherical", xd, m_d, c_d, w_d, lb)
+            lbs.append(float(lb))
+        torch.cuda.synchronize()
+        out[mode] = (m_d.cpu(), c_d.cpu(), w_d.cpu(), lbs)
+    (m1, c1, w1, l1), (m2, c2, w2, l2) = out["0"], out["1"]
+    for a, e in zip(l1, l2):
+        assert a == pytest.approx(e, rel=1e-5)
+    torch.testing.assert_close(m1, m2, rtol=2e-3, atol=2e-3 * float(m2.abs().max()))
+    torch.testing.assert_close(c1, c2, rtol=2e-3, atol=0)
+    torch.testing.assert_close(w1, w2, rtol=2e-3, atol=2e-3 * float(w2.abs().max()))
 
 
 def test_canary(hip):
