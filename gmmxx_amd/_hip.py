@@ -63,6 +63,7 @@ def _declare(lib):
         "gmmxx_hip_score": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_predict_proba": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_gram": (ctypes.c_int, [P, vp, vp, vp, i64, vp]),
+        "gmmxx_hip_finalize_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, i64, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -75,7 +76,7 @@ def exported_symbols() -> Tuple[str, ...]:
     return ("gmmxx_hip_abi_version", "gmmxx_hip_last_error", "gmmxx_hip_canary",
             "gmmxx_hip_supported", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_phase",
             "gmmxx_hip_estep_stats", "gmmxx_hip_score", "gmmxx_hip_predict_proba",
-            "gmmxx_hip_gram")
+            "gmmxx_hip_gram", "gmmxx_hip_finalize_stats")
 
 
 def load_library(path: Optional[str] = None):
@@ -291,6 +292,32 @@ def estep_stats(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs
                                       float(reg_covar), float(min_weight), _ptr(nk), _ptr(sum_x), _ptr(sum_q),
                                       _ptr(ll), ws.ptr, ws.nbytes, _stream(dev)), "gmmxx_hip_estep_stats")
     return nk, sum_x, sum_q, ll
+
+
+def finalize_stats(covariance_type: str, nk: torch.Tensor, sum_x: torch.Tensor, sum_q: Optional[torch.Tensor],
+                   means: torch.Tensor, covs: torch.Tensor, weights: torch.Tensor, n_rows: int, *,
+                   gram_xx: Optional[torch.Tensor] = None, reg_covar: float = 1e-6,
+                   min_weight: float = 1e-8, ws: Optional[Workspace] = None) -> None:
+    """M-step in place on (means, covs, weights) from sufficient statistics summed
+    over row chunks (``estep_stats`` layout); ``n_rows`` is the total row count."""
+    require_hip()
+    for t, nm in ((means, "means"), (covs, "covariances"), (weights, "weights")):
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise ValueError(f"{nm} must be a contiguous float32 GPU tensor")
+    B, K, D = int(means.shape[0]), int(means.shape[1]), int(means.shape[2])
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    nk = _device_tensor(nk, "nk", torch.float32)
+    sum_x = _device_tensor(sum_x, "sum_x", torch.float32)
+    if sum_q is not None:
+        sum_q = _device_tensor(sum_q, "sum_q", torch.float32)
+    if gram_xx is not None:
+        gram_xx = _device_tensor(gram_xx, "gram_xx", torch.float32)
+    prob = problem(covariance_type, torch.float32, B, int(n_rows), D, K)
+    ws = ws or Workspace(problem(covariance_type, torch.float32, B, 1, D, K), means.device)
+    _check(_lib.gmmxx_hip_finalize_stats(ctypes.byref(prob), _ptr(nk), _ptr(sum_x), _ptr(sum_q), _ptr(gram_xx),
+                                         float(reg_covar), float(min_weight), _ptr(means), _ptr(covs),
+                                         _ptr(weights), ws.ptr, ws.nbytes, _stream(means.device)),
+           "gmmxx_hip_finalize_stats")
 
 
 def score(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,

@@ -353,6 +353,32 @@ int stats_pass(const Plan& pl, const void* x, void* ws, hipStream_t s) {
   return check_hip("statistics pass");
 }
 
+// M-step parameter update from the statistics rows in the workspace; n_rows is
+// the row count per batch that divides N_k into the weights.
+void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, double min_weight, int64_t n_rows,
+              float* means, float* covs, float* weights, hipStream_t s) {
+  FinalizeArgs f{};
+  f.cov = pl.cov;
+  f.B = pl.B;
+  f.K = pl.K;
+  f.D = pl.D;
+  f.DP = pl.DP;
+  f.JP = pl.JP;
+  f.nk_col = pl.nk_col;
+  f.sq_col = pl.sq_col;
+  f.sq_n = pl.sq_n;
+  f.N = n_rows;
+  f.reg_covar = (float)reg_covar;
+  f.min_weight = (float)min_weight;
+  f.stats = at<float>(ws, pl.o_stats);
+  f.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
+  f.gram = gram;
+  f.means = means;
+  f.covs = covs;
+  f.weights = weights;
+  launch_finalize(f, s);
+}
+
 int begin(const gmmxx_problem* p, Plan* pl, const void* x, void* ws, int64_t ws_bytes) {
   int rc = plan_problem(p, pl);
   if (rc) return rc;
@@ -445,29 +471,9 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                            at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
       return check_hip("statistics reduction");
-    case GMMXX_PHASE_FINALIZE: {
-      FinalizeArgs f{};
-      f.cov = pl.cov;
-      f.B = pl.B;
-      f.K = pl.K;
-      f.D = pl.D;
-      f.DP = pl.DP;
-      f.JP = pl.JP;
-      f.nk_col = pl.nk_col;
-      f.sq_col = pl.sq_col;
-      f.sq_n = pl.sq_n;
-      f.N = pl.N;
-      f.reg_covar = (float)reg_covar;
-      f.min_weight = (float)min_weight;
-      f.stats = at<float>(ws, pl.o_stats);
-      f.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
-      f.gram = gram;
-      f.means = means;
-      f.covs = covs;
-      f.weights = weights;
-      launch_finalize(f, s);
+    case GMMXX_PHASE_FINALIZE:
+      finalize(pl, ws, gram, reg_covar, min_weight, pl.N, means, covs, weights, s);
       return check_hip("finalize");
-    }
     default:
       return fail(GMMXX_ERR_INVALID_ARGUMENT, "unknown phase");
   }
@@ -527,6 +533,41 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   u.sum_q = pl.cov == TIED ? nullptr : sum_q;
   launch_unpack(u, pl.B, s);
   return check_hip("statistics unpack");
+}
+
+int gmmxx_hip_finalize_stats(const gmmxx_problem* p, const float* nk, const float* sum_x, const float* sum_q,
+                             const float* gram, double reg_covar, double min_weight, float* means, float* covs,
+                             float* weights, void* ws, int64_t ws_bytes, void* stream) {
+  if (!p) return fail(GMMXX_ERR_INVALID_ARGUMENT, "problem descriptor is NULL");
+  gmmxx_problem one = *p;   // the statistics rows do not depend on N: plan for one row
+  one.N = 1;
+  Plan pl;
+  int rc = plan_problem(&one, &pl);
+  if (rc) return rc;
+  if ((rc = check_ws(pl, ws, ws_bytes))) return rc;
+  if (!nk || !sum_x || !means || !covs || !weights) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  if (pl.cov != TIED && !sum_q) return fail(GMMXX_ERR_INVALID_ARGUMENT, "sum_q is required for this covariance type");
+  if (pl.cov == TIED && !gram) return fail(GMMXX_ERR_INVALID_ARGUMENT, "tied finalize needs the XᵀX buffer");
+  if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
+  const hipStream_t s = (hipStream_t)stream;
+  PackArgs k{};
+  k.cov = pl.cov;
+  k.K = pl.K;
+  k.D = pl.D;
+  k.DP = pl.DP;
+  k.JP = pl.JP;
+  k.nk_col = pl.nk_col;
+  k.sq_col = pl.sq_col;
+  k.reg_covar = (float)reg_covar;
+  k.nk = nk;
+  k.sum_x = sum_x;
+  k.sum_q = sum_q;
+  k.covs = covs;
+  k.stats = at<float>(ws, pl.o_stats);
+  k.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
+  launch_pack(k, pl.B, s);
+  finalize(pl, ws, gram, reg_covar, min_weight, p->N, means, covs, weights, s);
+  return check_hip("finalize from statistics");
 }
 
 int gmmxx_hip_score(const gmmxx_problem* p, const void* x, const float* means, const float* covs,

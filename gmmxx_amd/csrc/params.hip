@@ -536,6 +536,32 @@ __global__ void unpack_stats_kernel(UnpackArgs a) {
   }
 }
 
+// Packs caller statistics into the rows the finalize kernels read (one thread per
+// component); the spherical Σ r‖x‖² goes to the first of the sq columns.
+__global__ void pack_stats_kernel(PackArgs a) {
+  const int b = blockIdx.y;
+  const int k = blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= a.K) return;
+  const size_t bk = (size_t)b * a.K + k;
+  float* sk = a.stats + bk * a.JP;
+  const int D = a.D, DP = a.DP;
+  for (int j = 0; j < a.JP; ++j) sk[j] = 0.f;
+  sk[a.nk_col] = a.nk[bk];
+  for (int d = 0; d < D; ++d) sk[d] = a.sum_x[bk * D + d];
+  if (a.cov == SPH) {
+    sk[a.sq_col] = a.sum_q[bk];
+    a.covs_used[bk] = fmaxf(a.covs[bk], a.reg_covar);
+  } else if (a.cov == DIAG) {
+    for (int d = 0; d < D; ++d) {
+      sk[DP + d] = a.sum_q[bk * D + d];
+      a.covs_used[bk * D + d] = fmaxf(a.covs[bk * D + d], a.reg_covar);
+    }
+  } else if (a.cov == FULL) {
+    for (int d = 0; d < D; ++d)
+      for (int e = d; e < D; ++e) sk[DP + sym_index(d, e, DP)] = a.sum_q[(bk * D + d) * D + e];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // XᵀX per batch (tied, once per fit; torch_fallback.py:2856-2862)
 // ---------------------------------------------------------------------------
@@ -647,6 +673,10 @@ void launch_finalize(const FinalizeArgs& a, hipStream_t s) {
 
 void launch_unpack(const UnpackArgs& a, int B, hipStream_t s) {
   unpack_stats_kernel<<<dim3((a.K + 255) / 256, B), 256, 0, s>>>(a);
+}
+
+void launch_pack(const PackArgs& a, int B, hipStream_t s) {
+  pack_stats_kernel<<<dim3((a.K + 255) / 256, B), 256, 0, s>>>(a);
 }
 
 void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,

@@ -55,6 +55,21 @@ struct UnpackArgs {
   float* sum_q;
 };
 
+// Inverse of UnpackArgs: caller-side statistics (N_k, Σ r x, Σ r q(x)) packed into
+// the statistics rows, plus the variances an inactive component keeps
+// (spherical/diag: max(covariance, reg_covar), the iteration prelude's clamp).
+struct PackArgs {
+  int cov, K, D, DP, JP, nk_col;
+  int sq_col;
+  float reg_covar;
+  const float* nk;
+  const float* sum_x;
+  const float* sum_q;
+  const float* covs;
+  float* stats;
+  float* covs_used;
+};
+
 void launch_prep(const PrepArgs& a, hipStream_t s);
 void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, float* logdet, hipStream_t s);
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s);
@@ -69,6 +84,7 @@ void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, 
                           float* tmp = nullptr, int64_t tmp_floats = 0);
 void launch_finalize(const FinalizeArgs& a, hipStream_t s);
 void launch_unpack(const UnpackArgs& a, int B, hipStream_t s);
+void launch_pack(const PackArgs& a, int B, hipStream_t s);
 void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
                  hipStream_t s);
 void launch_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, hipStream_t s);

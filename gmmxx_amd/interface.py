@@ -28,7 +28,7 @@ from typing import Any, Optional
 
 import torch
 
-from . import _dispatch, _hip, em
+from . import _dispatch, _hip, em, large_n
 
 _VALID_COVARIANCE_TYPES = {"spherical", "diag", "tied", "full"}
 _COVARIANCE_ALIASES = {"diagonal": "diag"}
@@ -255,6 +255,12 @@ class GMMXX:
             target = torch.float32
         return x_b.to(device=self.device, dtype=target).contiguous()
 
+    def _is_large_cpu_stream_input(self, x_b: torch.Tensor) -> bool:
+        """Host data longer than chunk_size_data_cpu rows streams through HBM in
+        chunks instead of being copied whole (gmmxx/interface.py:434-439)."""
+        return (x_b.device.type == "cpu" and self.device.type == "cuda"
+                and x_b.shape[1] > self.chunk_size_data_cpu)
+
     def _resolve(self, x_b: torch.Tensor, k: int) -> str:
         if self.approx_top_k is not None:
             raise NotImplementedError("approximate top-k EM is not provided by the hip backend")
@@ -274,11 +280,22 @@ class GMMXX:
         torch.manual_seed(self.seed)
         if torch.cuda.is_available():
             torch.cuda.manual_seed_all(self.seed)
-        x_b = self._engine_tensor(x_b)
-        self.last_backend_used_ = self._resolve(x_b, self.k)
-        labels_b, means_b, covs_b, weights_b, info = em.fit(
-            x_b, self.k, self.covariance_type, max_iters=self.niter, tol=self.tol, verbose=self.verbose,
-            init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit)
+        streaming = self._is_large_cpu_stream_input(x_b)
+        if streaming:
+            # gmmxx/interface.py:452-490: host data streams through HBM (B = 1).
+            self.last_backend_used_ = self._resolve(x_b, self.k)
+            x_host = x_b if self.dtype is None else x_b.to(self.dtype)
+            labels_b, means_b, covs_b, weights_b, info = large_n.fit_large_n(
+                x_host, self.k, self.covariance_type, device=self.device, max_iters=self.niter, tol=self.tol,
+                verbose=self.verbose, init_params=self.init_params, reg_covar=self.reg_covar,
+                chunk_size_N=self.chunk_size_data_cpu, compute_labels=self.compute_labels_on_fit,
+                seed=self.seed)
+        else:
+            x_b = self._engine_tensor(x_b)
+            self.last_backend_used_ = self._resolve(x_b, self.k)
+            labels_b, means_b, covs_b, weights_b, info = em.fit(
+                x_b, self.k, self.covariance_type, max_iters=self.niter, tol=self.tol, verbose=self.verbose,
+                init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit)
         self.cluster_ids_b = labels_b
         self.means_b = means_b
         self.variances_b = covs_b
@@ -298,7 +315,7 @@ class GMMXX:
         self.triton_estep_enabled_ = self.triton_fused_update_enabled_ = False
         self.triton_approx_topk_enabled_ = self.triton_streaming_update_enabled_ = False
         self.triton_labels_enabled_ = self.approximate_em_enabled_ = False
-        self.large_n_streaming_enabled_ = self.copy_stream_prefetch_enabled_ = False
+        self.large_n_streaming_enabled_ = self.copy_stream_prefetch_enabled_ = streaming
         self.cuda_estep_enabled_ = self.cuda_fused_update_enabled_ = self.cuda_approx_topk_enabled_ = False
         self.last_backend_used_ = "hip"
 
@@ -384,15 +401,18 @@ class GMMXX:
         if self.means_b is None or self.variances_b is None or self.weights_b is None:
             raise RuntimeError("Model not trained. Call train() or fit() first.")
 
-    def _prepare_predict_input(self, data: torch.Tensor) -> tuple[torch.Tensor, Optional[int]]:
+    def _prepare_predict_input(self, data: torch.Tensor) -> tuple[torch.Tensor, Optional[int], bool]:
+        """(x, batch size, streamed): host data longer than chunk_size_data_cpu rows
+        stays on the host and is streamed (gmmxx/interface.py:1758-1769)."""
         self._require_trained()
         x_b, batch_size = self._normalize_input(data)
         if batch_size != self._batch_size:
             raise ValueError(f"Model was trained with batch size B={self._batch_size}, "
                              f"but received B={batch_size}.")
-        x_b = self._engine_tensor(x_b)
         self.last_backend_used_ = self._resolve(x_b, int(self.means_b.shape[1]))
-        return x_b, batch_size
+        if self._is_large_cpu_stream_input(x_b):
+            return (x_b if self.dtype is None else x_b.to(self.dtype)), batch_size, True
+        return self._engine_tensor(x_b), batch_size, False
 
     def _params(self):
         return self.means_b.contiguous(), self.variances_b.contiguous(), self.weights_b.contiguous()
@@ -400,26 +420,38 @@ class GMMXX:
     def predict(self, data: torch.Tensor) -> torch.Tensor:
         """First-max component index per sample, int64 (gmmxx/interface.py:1753-1971)."""
         with self._matmul_precision_scope():
-            x_b, batch_size = self._prepare_predict_input(data)
+            x_b, batch_size, streamed = self._prepare_predict_input(data)
             means, covs, weights = self._params()
-            _, labels = _hip.score(self.covariance_type, x_b, means, covs, weights, want_scores=False)
+            if streamed:
+                labels = large_n.predict_large_n(x_b, means, covs, weights, self.covariance_type,
+                                                 device=self.device, chunk_size_N=self.chunk_size_data_cpu)
+            else:
+                _, labels = _hip.score(self.covariance_type, x_b, means, covs, weights, want_scores=False)
             return labels.squeeze(0) if batch_size is None else labels
 
     def predict_proba(self, data: torch.Tensor) -> torch.Tensor:
         """Responsibilities (B, N, K) fp32 (gmmxx/interface.py:1973-2268)."""
         with self._matmul_precision_scope():
-            x_b, batch_size = self._prepare_predict_input(data)
+            x_b, batch_size, streamed = self._prepare_predict_input(data)
             means, covs, weights = self._params()
-            probs = _hip.predict_proba(self.covariance_type, x_b, means, covs, weights)
+            if streamed:
+                probs = large_n.predict_proba_large_n(x_b, means, covs, weights, self.covariance_type,
+                                                      device=self.device, chunk_size_N=self.chunk_size_data_cpu)
+            else:
+                probs = _hip.predict_proba(self.covariance_type, x_b, means, covs, weights)
             return probs.squeeze(0) if batch_size is None else probs
 
     def score_samples(self, data: torch.Tensor) -> torch.Tensor:
         """Per-sample log-likelihood log Σ_k w_k N(x | μ_k, Σ_k), fp32
         (gmmxx/interface.py:2270-2521)."""
         with self._matmul_precision_scope():
-            x_b, batch_size = self._prepare_predict_input(data)
+            x_b, batch_size, streamed = self._prepare_predict_input(data)
             means, covs, weights = self._params()
-            scores, _ = _hip.score(self.covariance_type, x_b, means, covs, weights, want_labels=False)
+            if streamed:
+                scores = large_n.score_samples_large_n(x_b, means, covs, weights, self.covariance_type,
+                                                       device=self.device, chunk_size_N=self.chunk_size_data_cpu)
+            else:
+                scores, _ = _hip.score(self.covariance_type, x_b, means, covs, weights, want_labels=False)
             return scores.squeeze(0) if batch_size is None else scores
 
     def score(self, data: torch.Tensor, y: Any = None) -> float:

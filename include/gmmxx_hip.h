@@ -113,6 +113,23 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
                           double min_weight, float* nk, float* sum_x, float* sum_q, float* ll_sum,
                           void* workspace, int64_t workspace_bytes, void* stream);
 
+/* M-step finalize from sufficient statistics, in place on (means, covariances,
+ * weights): nk (B, K), sum_x (B, K, D) and sum_q as gmmxx_hip_estep_stats returns
+ * them (spherical Σ r‖x‖² (B, K), diag Σ r x² (B, K, D), full Σ r xxᵀ (B, K, D, D),
+ * tied NULL and gram = XᵀX (B, D, D) instead), summed over any number of row
+ * chunks; p->N is the total row count per batch (the weights' denominator).
+ * Components with N_k <= min_weight keep their mean and (clamped) covariance.
+ * The workspace needs gmmxx_hip_workspace_bytes of p with N = 1 (any larger N
+ * also serves).  Used by the large-N streaming fit, which accumulates the chunk
+ * statistics itself.  Replaces the finalize ops finalize_spherical(_soft) /
+ * finalize_diag (gmmxx/csrc/bindings.cpp:124-146, :170; gmmxx/_cuda.py:758,
+ * :1029), tied_finalize / full_finalize (gmmxx/_cuda.py:1204-1238, :1355-1416)
+ * and the finalize block of the large-N loop (gmmxx/large_n.py:1496-1537). */
+int gmmxx_hip_finalize_stats(const gmmxx_problem* p, const float* nk, const float* sum_x, const float* sum_q,
+                             const float* gram, double reg_covar, double min_weight, float* means,
+                             float* covariances, float* weights, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
 /* Inference under fixed parameters (no prelude): per-sample log-likelihood
  * `scores` (B, N) and/or first-maximum labels (B, N) int64; either may be NULL.
  * Replaces spherical/diag/full assign + logsumexp (gmmxx/csrc/bindings.cpp:19-58,

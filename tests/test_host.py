@@ -303,3 +303,37 @@ def test_n_parameters_batched():
     rng = np.random.default_rng(0)
     est = _fitted("diag", 3, 4, 5, rng)
     assert est._n_parameters(3) == 3 * (4 * 5 + 4 * 5 + 3)
+
+
+# --- large-N streaming: input validation (gmmxx/large_n.py:468-478), no GPU needed ---
+
+def test_large_n_rejects_bad_input():
+    from gmmxx_amd import large_n
+    dev = torch.device("cuda")
+    with pytest.raises(NotImplementedError):
+        large_n.fit_large_n(torch.zeros((2, 10, 3)), 2, "spherical", device=dev)
+    with pytest.raises(ValueError):
+        large_n.fit_large_n(torch.zeros((10, 3)), 2, "spherical", device=dev)
+    with pytest.raises(ValueError):
+        large_n.fit_large_n(torch.zeros((1, 10, 3)), 2, "spherical", device=torch.device("cpu"))
+    with pytest.raises(TypeError):
+        large_n.fit_large_n(torch.zeros((1, 10, 3), dtype=torch.int32), 2, "spherical", device=dev)
+    with pytest.raises(ValueError):
+        large_n.fit_large_n(torch.zeros((1, 10, 3)), 2, "bogus", device=dev)
+    with pytest.raises(ValueError):
+        large_n.fit_large_n(torch.zeros((1, 10, 3)), 2, "diag", device=dev, chunk_size_N=0)
+
+
+def test_large_n_engine_dtype():
+    from gmmxx_amd import large_n
+    x = torch.zeros((1, 4, 3), dtype=torch.bfloat16)
+    assert large_n._engine_dtype(x, "spherical") == torch.bfloat16
+    assert large_n._engine_dtype(x, "diag") == torch.float32
+    assert large_n._engine_dtype(x.double(), "spherical") == torch.float32
+
+
+def test_estimator_routes_long_host_input_to_streaming():
+    from gmmxx_amd import GMMXX
+    gm = GMMXX(n_components=3, backend="hip", device="cuda", chunk_size_data_cpu=100)
+    assert gm._is_large_cpu_stream_input(torch.zeros((1, 101, 2)))
+    assert not gm._is_large_cpu_stream_input(torch.zeros((1, 100, 2)))
