@@ -64,6 +64,9 @@ def _declare(lib):
         "gmmxx_hip_predict_proba": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_gram": (ctypes.c_int, [P, vp, vp, vp, i64, vp]),
         "gmmxx_hip_finalize_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, i64, vp]),
+        "gmmxx_hip_topk_workspace_bytes": (i64, [P]),
+        "gmmxx_hip_estep_stats_topk": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, ctypes.c_int, vp, vp, vp,
+                                                      vp, vp, i64, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -76,7 +79,8 @@ def exported_symbols() -> Tuple[str, ...]:
     return ("gmmxx_hip_abi_version", "gmmxx_hip_last_error", "gmmxx_hip_canary",
             "gmmxx_hip_supported", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_phase",
             "gmmxx_hip_estep_stats", "gmmxx_hip_score", "gmmxx_hip_predict_proba",
-            "gmmxx_hip_gram", "gmmxx_hip_finalize_stats")
+            "gmmxx_hip_gram", "gmmxx_hip_finalize_stats", "gmmxx_hip_topk_workspace_bytes",
+            "gmmxx_hip_estep_stats_topk")
 
 
 def load_library(path: Optional[str] = None):
@@ -171,9 +175,10 @@ def _device_tensor(t: torch.Tensor, name: str, dtype: Optional[torch.dtype] = No
 class Workspace:
     """Device scratch for one problem shape, sized by the library (256-byte aligned)."""
 
-    def __init__(self, prob: _Problem, device: torch.device):
+    def __init__(self, prob: _Problem, device: torch.device, *, topk: bool = False):
         lib = load_library()
-        nbytes = int(lib.gmmxx_hip_workspace_bytes(ctypes.byref(prob)))
+        query = lib.gmmxx_hip_topk_workspace_bytes if topk else lib.gmmxx_hip_workspace_bytes
+        nbytes = int(query(ctypes.byref(prob)))
         if nbytes < 0:
             raise HipRuntimeError("problem not supported by the HIP engine: "
                                   + lib.gmmxx_hip_last_error().decode(errors="replace"))
@@ -291,6 +296,38 @@ def estep_stats(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs
     _check(_lib.gmmxx_hip_estep_stats(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
                                       float(reg_covar), float(min_weight), _ptr(nk), _ptr(sum_x), _ptr(sum_q),
                                       _ptr(ll), ws.ptr, ws.nbytes, _stream(dev)), "gmmxx_hip_estep_stats")
+    return nk, sum_x, sum_q, ll
+
+
+def estep_stats_topk(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+                     weights: torch.Tensor, top_k: int, *, reg_covar: float = 1e-6, min_weight: float = 1e-8,
+                     ws: Optional[Workspace] = None):
+    """Approximate top-k E-step statistics (nk, sum_x, sum_q, ll_sum): each row's
+    responsibility mass is spread over its ``top_k`` largest logits only (ties by
+    lower component index), normalised over them; ``ll_sum`` sums the top-k
+    log-normalisers.  ``1 <= top_k < K``.  The workspace holds the (B, N, K)
+    logits, so callers pass row chunks (gmmxx/torch_fallback.py:667-777)."""
+    require_hip()
+    x = _device_tensor(x, "x")
+    means = _device_tensor(means, "means", torch.float32)
+    covs = _device_tensor(covs, "covariances", torch.float32)
+    weights = _device_tensor(weights, "weights", torch.float32)
+    B, N, D, K = _shape(x, means)
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    if not 1 <= int(top_k) < K:
+        raise ValueError(f"top_k must satisfy 1 <= top_k < K={K}, got {top_k}")
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    ws = ws or Workspace(prob, x.device, topk=True)
+    dev = x.device
+    nk = torch.empty((B, K), dtype=torch.float32, device=dev)
+    sum_x = torch.empty((B, K, D), dtype=torch.float32, device=dev)
+    q_shape = {"spherical": (B, K), "diag": (B, K, D), "full": (B, K, D, D)}.get(covariance_type)
+    sum_q = torch.empty(q_shape, dtype=torch.float32, device=dev) if q_shape else None
+    ll = torch.empty((1,), dtype=torch.float32, device=dev)
+    _check(_lib.gmmxx_hip_estep_stats_topk(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
+                                           float(reg_covar), float(min_weight), int(top_k), _ptr(nk),
+                                           _ptr(sum_x), _ptr(sum_q), _ptr(ll), ws.ptr, ws.nbytes, _stream(dev)),
+           "gmmxx_hip_estep_stats_topk")
     return nk, sum_x, sum_q, ll
 
 

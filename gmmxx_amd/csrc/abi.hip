@@ -379,6 +379,28 @@ void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, dou
   launch_finalize(f, s);
 }
 
+// Approximate top-k EM: the (B, N, K) log2 logits, each row's threshold logit
+// and index, and per-block log-likelihood sums, after the plan's workspace.
+struct TopkLayout {
+  size_t o_logits = 0, o_thr = 0, o_thri = 0, o_ll = 0, total = 0;
+};
+TopkLayout topk_layout(const Plan& pl) {
+  TopkLayout t;
+  size_t off = pl.total;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  const size_t BN = (size_t)pl.B * pl.N;
+  t.o_logits = take(BN * pl.K * 4);
+  t.o_thr = take(BN * 4);
+  t.o_thri = take(BN * 4);
+  t.o_ll = take((size_t)pl.B * topk_select_blocks(pl.N) * 8);
+  t.total = off;
+  return t;
+}
+
 int begin(const gmmxx_problem* p, Plan* pl, const void* x, void* ws, int64_t ws_bytes) {
   int rc = plan_problem(p, pl);
   if (rc) return rc;
@@ -532,6 +554,74 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   u.sum_x = sum_x;
   u.sum_q = pl.cov == TIED ? nullptr : sum_q;
   launch_unpack(u, pl.B, s);
+  return check_hip("statistics unpack");
+}
+
+int64_t gmmxx_hip_topk_workspace_bytes(const gmmxx_problem* p) {
+  Plan pl;
+  if (plan_problem(p, &pl) != GMMXX_OK) return -1;
+  return (int64_t)topk_layout(pl).total;
+}
+
+int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
+                               const float* weights, double reg_covar, double min_weight, int top_k, float* nk,
+                               float* sum_x, float* sum_q, float* ll_sum, void* ws, int64_t ws_bytes,
+                               void* stream) {
+  Plan pl;
+  int rc = plan_problem(p, &pl);
+  if (rc) return rc;
+  if (!x) return fail(GMMXX_ERR_INVALID_ARGUMENT, "x is NULL");
+  const TopkLayout tl = topk_layout(pl);
+  if (!ws) return fail(GMMXX_ERR_WORKSPACE, "workspace is NULL");
+  if (ws_bytes < 0 || (uint64_t)ws_bytes < tl.total)
+    return fail(GMMXX_ERR_WORKSPACE, "workspace too small: need " + std::to_string(tl.total) + " bytes");
+  if ((uintptr_t)ws % 256 != 0) return fail(GMMXX_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  if (!means || !covs || !weights || !nk || !sum_x || !ll_sum) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  if (pl.cov != TIED && !sum_q) return fail(GMMXX_ERR_INVALID_ARGUMENT, "sum_q is required for this covariance type");
+  if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
+  if (top_k < 1 || top_k >= pl.K)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "top_k must be in [1, K-1] (top_k >= K is exact EM)");
+  const hipStream_t s = (hipStream_t)stream;
+  // Parameters with the iteration prelude; tied rows get xᵀPx, so the logits
+  // (and the log-normalisers) are complete.
+  if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
+  // spherical bf16 at D = 128: the later passes read the augmented row chunk
+  // that the log-normaliser pass stores.
+  if (pl.bf && pl.cov == SPH && pl.DP >= 128) {
+    if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, false, s))) return rc;
+  }
+  float* logits = at<float>(ws, tl.o_logits);
+  float* thr = at<float>(ws, tl.o_thr);
+  int* thri = at<int>(ws, tl.o_thri);
+  double* tll = at<double>(ws, tl.o_ll);
+  TileArgs t = tile_args(pl, x, ws);
+  t.proba = logits;
+  t.raw_logits = 1;
+  if (run_tile(pl, MODE_PROBA, t, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+  const int sel_blocks = topk_select_blocks(pl.N);
+  launch_topk_select(logits, pl.B, pl.N, pl.K, top_k, at<float>(ws, pl.o_lse2), thr, thri, tll, sel_blocks, s);
+  TileArgs u = tile_args(pl, x, ws);
+  u.thr2 = thr;
+  u.thr_idx = thri;
+  if (run_tile(pl, MODE_STATS_TOPK, u, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+  launch_reduce_slices(u.part_stats, pl.slices, (int64_t)pl.B * pl.K * pl.JP, at<float>(ws, pl.o_stats), s,
+                       red_tmp(pl, ws), red_tmp_floats(pl));
+  launch_ll_reduce(tll, pl.B * sel_blocks, 1.0, ll_sum, s);
+  if ((rc = check_hip("approximate top-k statistics"))) return rc;
+  UnpackArgs k{};
+  k.cov = pl.cov;
+  k.K = pl.K;
+  k.D = pl.D;
+  k.DP = pl.DP;
+  k.JP = pl.JP;
+  k.nk_col = pl.nk_col;
+  k.sq_col = pl.sq_col;
+  k.sq_n = pl.sq_n;
+  k.stats = at<float>(ws, pl.o_stats);
+  k.nk = nk;
+  k.sum_x = sum_x;
+  k.sum_q = pl.cov == TIED ? nullptr : sum_q;
+  launch_unpack(k, pl.B, s);
   return check_hip("statistics unpack");
 }
 

@@ -10,7 +10,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 enum Cov { SPH = 0, DIAG = 1, TIED = 2, FULL = 3 };
-enum Mode { MODE_LSE = 0, MODE_STATS = 1, MODE_PROBA = 2, MODE_LSE_IDX = 3 };
+// MODE_STATS_TOPK: the statistics pass of approximate top-k EM -- responsibilities
+// only for each row's top-k components (ranked by logit, then lower index), the
+// rest zero, against the top-k log-normaliser.
+enum Mode { MODE_LSE = 0, MODE_STATS = 1, MODE_PROBA = 2, MODE_LSE_IDX = 3, MODE_STATS_TOPK = 4 };
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;

@@ -101,7 +101,8 @@ template <int DP, int NW, int MODE>
 __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
   constexpr bool LSE = (MODE == MODE_LSE || MODE == MODE_LSE_IDX);
   constexpr bool WANT_IDX = MODE == MODE_LSE_IDX;
-  constexpr bool STATS = MODE == MODE_STATS;
+  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK;
+  constexpr bool TOPK = MODE == MODE_STATS_TOPK;
   constexpr int CW = 32, CT = 2;                 // components per wave, 16-wide tiles
   constexpr int ECH = DP / 32;                   // x chunks of the E-GEMM
   // Staged row stride (bf16): s = XS/2 dwords ≡ 8 or 24 (mod 32) measured fastest for
@@ -124,6 +125,8 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
 
   __shared__ __align__(16) __bf16 xs[NB * kBN * XS];
   __shared__ __align__(16) float lse_s[LSE ? 4 : NB * kBN];
+  __shared__ __align__(16) float thr_s[TOPK ? NB * kBN : 4];   // top-k threshold logit and index per row
+  __shared__ __align__(16) int thri_s[TOPK ? NB * kBN : 4];
   constexpr int RS = kBN + 1;                    // red_* stride per wave (conflict-free reads)
   __shared__ float red_m[LSE ? 2 * NW * RS : 1];   // [parity][wave][row]
   __shared__ float red_s[LSE ? 2 * NW * RS : 1];
@@ -218,6 +221,8 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
   // log-normaliser pass (rowaux) and the row's lse2.
   uint4 pa[PF];
   float pl[PF];
+  float pt[TOPK ? PF : 1];
+  int pti[TOPK ? PF : 1];
   auto fetch = [&](int64_t n0) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
@@ -230,6 +235,10 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
           if (c % CPR == 0) {
             if constexpr (AUX) pa[i] = a.rowaux[o];
             pl[i] = (n < rend) ? a.lse2[o] : kHuge;
+            if constexpr (TOPK) {
+              pt[i] = (n < rend) ? a.thr2[o] : kHuge;
+              pti[i] = (n < rend) ? a.thr_idx[o] : -1;
+            }
           }
         }
       }
@@ -271,6 +280,12 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
         }
         if constexpr (!LSE) {
           if (cc == 0) lse_s[buf * kBN + r] = pl[i];
+        }
+        if constexpr (TOPK) {
+          if (cc == 0) {
+            thr_s[buf * kBN + r] = pt[i];
+            thri_s[buf * kBN + r] = pti[i];
+          }
         }
       }
     }
@@ -417,13 +432,35 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
       }
     } else if constexpr (STATS) {
       bf16x8 ar[CT];
+      if constexpr (TOPK) {
+        // Only each row's top k (logit descending, then lower index) get mass;
+        // lane (li, g) holds component kbase + 16ct + li of rows 4g + v and 16 + 4g + v.
+        const f32x4 t0 = ld16<f32x4>(&thr_s[bx * kBN + 4 * g]);
+        const f32x4 t1 = ld16<f32x4>(&thr_s[bx * kBN + 16 + 4 * g]);
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        const i32x4 i0 = ld16<i32x4>(&thri_s[bx * kBN + 4 * g]);
+        const i32x4 i1 = ld16<i32x4>(&thri_s[bx * kBN + 16 + 4 * g]);
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
+        for (int ct = 0; ct < CT; ++ct) {
+          const int kk = kbase + 16 * ct + li;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          ar[ct][v] = (__bf16)fast_exp2(A.t[ct][0][v] - ls0[v]);
-          ar[ct][4 + v] = (__bf16)fast_exp2(A.t[ct][1][v] - ls1[v]);
+          for (int v = 0; v < 4; ++v) {
+            const float l0 = A.t[ct][0][v], l1 = A.t[ct][1][v];
+            const bool k0 = l0 > t0[v] || (l0 == t0[v] && kk <= i0[v]);
+            const bool k1 = l1 > t1[v] || (l1 == t1[v] && kk <= i1[v]);
+            ar[ct][v] = (__bf16)(k0 ? fast_exp2(l0 - ls0[v]) : 0.f);
+            ar[ct][4 + v] = (__bf16)(k1 ? fast_exp2(l1 - ls1[v]) : 0.f);
+          }
         }
+      } else {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            ar[ct][v] = (__bf16)fast_exp2(A.t[ct][0][v] - ls0[v]);
+            ar[ct][4 + v] = (__bf16)fast_exp2(A.t[ct][1][v] - ls1[v]);
+          }
+      }
       // M-GEMM B operand ψ[k][feature 16jt + li] for k = 8g + 4h + j (data row
       // 16h + 4g + j) straight from the staged rows with the transposing LDS
       // read: in each 16-lane group, lane L supplies the 8-byte chunk of row
@@ -451,7 +488,9 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int64_t n = n0 + 16 * h + 4 * g + v;
-              if (n < rend) a.proba[((size_t)b * N + n) * K + kk] = fast_exp2(A.t[ct][h][v] - (h ? ls1[v] : ls0[v]));
+              if (n < rend)
+                a.proba[((size_t)b * N + n) * K + kk] =
+                    a.raw_logits ? A.t[ct][h][v] : fast_exp2(A.t[ct][h][v] - (h ? ls1[v] : ls0[v]));
             }
         }
       }
@@ -488,7 +527,7 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
   // With 16 waves there are no registers for a second accumulator set: the
   // E-GEMM and epilogue of a block run back to back, and the other waves of
   // the SIMD fill the gaps.
-  constexpr bool PIPE = NW < 16;
+  constexpr bool PIPE = NW < 16 && !TOPK;   // (the approximate pass skips the pipeline: fewer registers)
   Acc cur;
   if (PIPE && nblk > 0) cur = egemm(load_frags(0));
   int bx = 0;
@@ -541,6 +580,7 @@ static int launch_sph_bf16_nw(int mode, const TileArgs& a, dim3 grid, hipStream_
     case MODE_LSE_IDX: sph_bf16_kernel<DP, NW, MODE_LSE_IDX><<<grid, block, 0, s>>>(a); break;
     case MODE_STATS: sph_bf16_kernel<DP, NW, MODE_STATS><<<grid, block, 0, s>>>(a); break;
     case MODE_PROBA: sph_bf16_kernel<DP, NW, MODE_PROBA><<<grid, block, 0, s>>>(a); break;
+    case MODE_STATS_TOPK: sph_bf16_kernel<DP, NW, MODE_STATS_TOPK><<<grid, block, 0, s>>>(a); break;
     default: return -1;
   }
   return 0;

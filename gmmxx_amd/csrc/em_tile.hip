@@ -22,7 +22,14 @@
 //               feeds them directly as the A operand of the M-GEMM acc += rᵀ·ψ,
 //               so the (B, N, K) responsibility matrix never exists.  Each
 //               workgroup writes one partial statistics tile.
-//   MODE_PROBA  Same epilogue; r is written out (predict_proba needs it).
+//   MODE_PROBA  Same epilogue; r is written out (predict_proba needs it), or
+//               with raw_logits the log2 logits themselves (approximate EM).
+//   MODE_STATS_TOPK
+//               MODE_STATS restricted to each row's top k components: a
+//               logit keeps its responsibility iff it ranks above the row's
+//               threshold (value, then lower index), else contributes 0.  The
+//               E-GEMM and logit arithmetic are those of MODE_PROBA, so the
+//               recomputed logits equal the ones the threshold was chosen from.
 //
 // Logits are kept in log2 units (l2 = l·log2 e) so exp2 maps to v_exp_f32:
 //   l2 = A_k·S + (a_k·rowq_n + C_k)
@@ -144,6 +151,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr bool BF = sizeof(XT) == 2;
   constexpr bool LSE = (MODE == MODE_LSE || MODE == MODE_LSE_IDX);
   constexpr bool WANT_IDX = MODE == MODE_LSE_IDX;
+  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK;
+  constexpr bool TOPK = MODE == MODE_STATS_TOPK;
   using Dm = Dims<COV, DP, BF>;
   constexpr int EP = Dm::EP, JP = Dm::JP, J = Dm::J, S = Dm::S;
   constexpr int CT = CW / 16;
@@ -153,7 +162,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr int CPR = DP / VEC;                          // chunks per row
   constexpr int NCH = kBN * CPR;                         // chunks per row block
   constexpr int PF = (NCH + 511) / 512;                  // prefetched chunks per thread at 512 threads
-  constexpr bool PSI_LDS = BF && MODE == MODE_STATS;     // materialised ψᵀ (bf16 spherical)
+  constexpr bool PSI_LDS = BF && (MODE == MODE_STATS || MODE == MODE_STATS_TOPK);  // materialised ψᵀ (bf16 spherical)
   // Block i+1's E-GEMM issued ahead of block i's epilogue: kept for the bf16
   // path only.  The fp32 (split-bf16) passes measured equal or faster without
   // it (C3 3.45 vs 3.47 ms, C4 0.87 vs 0.93 ms): MFMA and VALU time add up on
@@ -180,7 +189,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr int X3P = NB * kBN * EPS;                    // one part, all buffers
   // Wide statistics passes keep W's third part in LDS (per wave, in the exact
   // per-lane fragment order) to stay within the register file.
-  constexpr bool W3L = X3 && MODE == MODE_STATS && EP >= 128;
+  constexpr bool W3L = X3 && STATS && EP >= 128;
 
   __shared__ __align__(16) XT xs[(COV == FULL || X3) ? 8 : NB * kBN * XS];
   __shared__ __align__(16) __bf16 phx[X3 ? 3 * X3P : 8];
@@ -189,6 +198,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   __shared__ __align__(16) FT psiT[PSI_LDS ? 2 * JP * QS : 8];
   __shared__ float rowq_s[NB * kBN];
   __shared__ float lse_s[NB * kBN];
+  __shared__ float thr_s[TOPK ? NB * kBN : 1];     // top-k threshold logit and index per row
+  __shared__ int thri_s[TOPK ? NB * kBN : 1];
   __shared__ float red_m[LSE ? 2 * kBN * 8 : 1];   // [parity][row][wave]
   __shared__ float red_s[LSE ? 2 * kBN * 8 : 1];
   __shared__ int red_i[WANT_IDX ? 2 * kBN * 8 : 1];
@@ -289,8 +300,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     else return fmaf(c.x, S, c.y);
   };
 
-  f32x4 acc[MODE == MODE_STATS ? CT : 1][MODE == MODE_STATS ? JT : 1];
-  if constexpr (MODE == MODE_STATS) {
+  f32x4 acc[STATS ? CT : 1][STATS ? JT : 1];
+  if constexpr (STATS) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -387,7 +398,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         for (int j = 0; j < VEC; ++j) q = fmaf(v[j], v[j], q);
         q = group_sum<CPR>(q);
         if (cc == 0) rowq_s[buf * kBN + r] = q;
-        if constexpr (X3 && MODE == MODE_STATS) {
+        if constexpr (X3 && STATS) {
           if (cc == 0) {
             uint32_t q1, q2, q3;
             split3x2(q, 0.f, q1, q2, q3);
@@ -423,6 +434,12 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       }
       if constexpr (!LSE) {
         if (cc == 0) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
+      }
+      if constexpr (TOPK) {
+        if (cc == 0) {
+          thr_s[buf * kBN + r] = (n < rend) ? a.thr2[(size_t)b * N + n] : INFINITY;
+          thri_s[buf * kBN + r] = (n < rend) ? a.thr_idx[(size_t)b * N + n] : -1;
+        }
       }
     }
   };
@@ -646,9 +663,18 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
           for (int v = 0; v < 4; ++v) {
             const int r = BF ? 8 * g + 4 * rt + v : 16 * rt + 4 * g + v;
             const float l2 = logit(cS[ct], A.t[ct][rt][v], rowq_s[bx * kBN + r]);
-            rr[ct][rt][v] = fast_exp2(l2 - lse_s[bx * kBN + r]);
+            if constexpr (MODE == MODE_PROBA) {
+              rr[ct][rt][v] = a.raw_logits ? l2 : fast_exp2(l2 - lse_s[bx * kBN + r]);
+            } else if constexpr (TOPK) {
+              // Only the row's top k (logit descending, then lower index) get mass.
+              const float t = thr_s[bx * kBN + r];
+              const bool keep = l2 > t || (l2 == t && kbase + 16 * ct + li <= thri_s[bx * kBN + r]);
+              rr[ct][rt][v] = keep ? fast_exp2(l2 - lse_s[bx * kBN + r]) : 0.f;
+            } else {
+              rr[ct][rt][v] = fast_exp2(l2 - lse_s[bx * kBN + r]);
+            }
           }
-      if constexpr (MODE == MODE_STATS && X3) {
+      if constexpr (STATS && X3) {
         // M-GEMM on split bf16 operands: r in three parts (A element j = 4rt + v is
         // data row 16rt + 4g + v), ψ tiles read from the staged split φ rows with the
         // transposing load (rows 4g..4g+3 and 16+4g..16+4g+3, the same order).
@@ -690,7 +716,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
             acc[ct][jt] = mfma_bf16(ra[0][ct], bq[0], acc[ct][jt]);
           }
         }
-      } else if constexpr (MODE == MODE_STATS) {
+      } else if constexpr (STATS) {
         // M-GEMM: each ψ fragment is loaded once and used by every component tile.
         if constexpr (BF) {
           bf16x8 ar[CT];
@@ -785,7 +811,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     if (nblk > 0) combine_out((int)((nblk - 1) & 1), rbeg + (nblk - 1) * kBN);
   }
 
-  if constexpr (MODE == MODE_STATS) {
+  if constexpr (STATS) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -809,6 +835,7 @@ static int launch_tile_t(int mode, const TileArgs& a, dim3 grid, int nw, hipStre
     case MODE_LSE_IDX: em_tile_kernel<COV, XT, DP, CW, MODE_LSE_IDX><<<grid, block, 0, s>>>(a); break;
     case MODE_STATS: em_tile_kernel<COV, XT, DP, CW, MODE_STATS><<<grid, block, 0, s>>>(a); break;
     case MODE_PROBA: em_tile_kernel<COV, XT, DP, CW, MODE_PROBA><<<grid, block, 0, s>>>(a); break;
+    case MODE_STATS_TOPK: em_tile_kernel<COV, XT, DP, CW, MODE_STATS_TOPK><<<grid, block, 0, s>>>(a); break;
     default: return -1;
   }
   return 0;

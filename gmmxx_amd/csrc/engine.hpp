@@ -26,7 +26,18 @@ struct TileArgs {
   float* proba;                // [B][N][K]                             (PROBA)
   int nslices;                 // row slices of the fused kernel
   double* ll_part;             // [B][nslices] partial log-likelihood   (fused)
+  int raw_logits;              // PROBA: write the log2-domain logits instead of responsibilities
+  const float* thr2;           // [B][N] STATS_TOPK: each row's k-th largest logit (log2)
+  const int* thr_idx;          // [B][N] STATS_TOPK: its component index (ties: lower index first)
 };
+
+// Approximate top-k EM (params.hip): per row of the (B, N, K) log2 logits, the
+// k-th largest logit and its index (order: logit descending, then index
+// ascending), the log-normaliser over the top k (written to lse2), and per-block
+// sums of the natural-log normalisers.
+void launch_topk_select(const float* logits, int B, int64_t N, int K, int top_k, float* lse2, float* thr2,
+                        int* thr_idx, double* ll_part, int ll_blocks, hipStream_t s);
+int topk_select_blocks(int64_t N);
 
 int tile_cw(int cov, int dp, int bf);
 int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s);

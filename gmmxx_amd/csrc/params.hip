@@ -9,6 +9,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "engine.hpp"
 #include "params.hpp"
 
 namespace gx {
@@ -370,6 +371,74 @@ __global__ void combine_kernel(CombineArgs a) {
   }
   const double t = block_sum(contrib, scratch);
   if (threadIdx.x == 0 && a.ll_part) a.ll_part[(size_t)b * gridDim.x + blockIdx.x] = t;
+}
+
+// ---------------------------------------------------------------------------
+// Approximate top-k EM: per-row top-k selection over the materialised logits
+// (torch_fallback.py:667-716 _topk_logits_for_chunk, :719-777 _accumulate_topk_stats)
+// ---------------------------------------------------------------------------
+
+constexpr int kSelWaves = 4;   // rows (waves) per block
+
+int topk_select_blocks(int64_t N) { return (int)((N + kSelWaves - 1) / kSelWaves); }
+
+// One wave per row.  Round j finds the largest logit that comes after round
+// j-1's pick in the order (logit descending, index ascending): a lane scans
+// its strided share of the row, then the wave reduces (max logit, min index).
+// After top_k rounds: threshold = the k-th pick, lse2 = m + log2 Σ_j 2^(v_j - m)
+// over the picks (m = the first); the block sums lse2·ln2 in a fixed order.
+__global__ __launch_bounds__(64 * kSelWaves) void topk_select_kernel(const float* __restrict__ logits, int64_t N,
+                                                                     int K, int top_k, float* lse2, float* thr2,
+                                                                     int* thr_idx, double* ll_part) {
+  __shared__ double llw[kSelWaves];
+  const int b = blockIdx.y, wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int64_t n = (int64_t)blockIdx.x * kSelWaves + wave;
+  double contrib = 0.0;
+  if (n < N) {
+    const float* row = logits + ((size_t)b * N + n) * K;
+    float pv = INFINITY;   // previous pick (value, index)
+    int pi = -1;
+    float m = 0.f, sum = 0.f;
+    for (int j = 0; j < top_k; ++j) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int k = lane; k < K; k += 64) {
+        const float v = row[k];
+        const bool after = v < pv || (v == pv && k > pi);
+        if (after && (v > bv || (v == bv && k < bi))) { bv = v; bi = k; }
+      }
+      for (int off = 32; off >= 1; off /= 2) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if (j == 0) m = bv;
+      sum += fast_exp2(bv - m);
+      pv = bv;
+      pi = bi;
+    }
+    const float l2 = m + __log2f(sum);
+    if (lane == 0) {
+      const size_t o = (size_t)b * N + n;
+      lse2[o] = l2;
+      thr2[o] = pv;
+      thr_idx[o] = pi;
+    }
+    contrib = (double)l2 * (double)kLn2;
+  }
+  if (lane == 0) llw[wave] = contrib;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < kSelWaves; ++w) t += llw[w];
+    ll_part[(size_t)b * gridDim.x + blockIdx.x] = t;
+  }
+}
+
+void launch_topk_select(const float* logits, int B, int64_t N, int K, int top_k, float* lse2, float* thr2,
+                        int* thr_idx, double* ll_part, int ll_blocks, hipStream_t s) {
+  topk_select_kernel<<<dim3(ll_blocks, B), 64 * kSelWaves, 0, s>>>(logits, N, K, top_k, lse2, thr2, thr_idx,
+                                                                     ll_part);
 }
 
 // Tied EM iteration: the logits leave out the per-row xᵀPx, so the row

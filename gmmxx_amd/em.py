@@ -131,13 +131,82 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
     return means.contiguous(), covs.contiguous(), weights, source
 
 
+def resolve_approx_top_k(approx_top_k: Optional[int], n_components: int) -> Optional[int]:
+    """None for exact EM; ``approx_top_k >= K`` is exact EM too
+    (gmmxx/torch_fallback.py:598-606)."""
+    if approx_top_k is None:
+        return None
+    top_k = int(approx_top_k)
+    if top_k <= 0:
+        raise ValueError("approx_top_k must be positive or None")
+    return None if top_k >= n_components else top_k
+
+
+# The approximate E-step keeps the (B, rows, K) fp32 logits of one row chunk in
+# its workspace; chunks are sized to hold at most this many logit bytes.
+_TOPK_LOGIT_BYTES = 1 << 30
+
+
+def topk_chunk_rows(bsz: int, n: int, k: int) -> int:
+    rows = max(4096, _TOPK_LOGIT_BYTES // (4 * bsz * k)) // 32 * 32
+    return min(n, rows)
+
+
+class _TopkStep:
+    """One approximate-EM iteration over row chunks: per chunk the top-k
+    statistics (``gmmxx_hip_estep_stats_topk``), summed, then one M-step from
+    the totals (``gmmxx_hip_finalize_stats``).  Follows the approximate
+    branches of the reference's EM loops (gmmxx/torch_fallback.py:2097-2145,
+    :2500-2526, :2911-2936), which likewise accumulate over row chunks."""
+
+    def __init__(self, x, covariance_type, k, top_k):
+        self.x, self.cov, self.k, self.top_k = x, covariance_type, k, top_k
+        bsz, n, d = x.shape
+        self.n = n
+        self.rows = topk_chunk_rows(bsz, n, k)
+        self.ws: Dict[int, _hip.Workspace] = {}
+        self.fin_ws = _hip.Workspace(_hip.problem(covariance_type, torch.float32, bsz, 1, d, k), x.device)
+
+    def chunks(self):
+        for n0 in range(0, self.n, self.rows):
+            xc = self.x[:, n0:min(n0 + self.rows, self.n), :]
+            rows = int(xc.shape[1])
+            ws = self.ws.get(rows)
+            if ws is None:
+                ws = _hip.Workspace(_hip.problem(self.cov, xc.dtype, xc.shape[0], rows, xc.shape[2], self.k),
+                                    xc.device, topk=True)
+                self.ws[rows] = ws
+            yield xc, ws
+
+    def gram(self):
+        total = None
+        for xc, ws in self.chunks():
+            g = _hip.gram(xc, ws)
+            total = g if total is None else total + g
+        return total
+
+    def step(self, means, covs, weights, lb_out, gram, reg_covar, min_weight):
+        tot = None
+        for xc, ws in self.chunks():
+            part = _hip.estep_stats_topk(self.cov, xc, means, covs, weights, self.top_k, reg_covar=reg_covar,
+                                         min_weight=min_weight, ws=ws)
+            tot = list(part) if tot is None else [a if a is None else a + b for a, b in zip(tot, part)]
+        nk, sum_x, sum_q, ll = tot
+        _hip.finalize_stats(self.cov, nk, sum_x, sum_q, means, covs, weights, self.n, gram_xx=gram,
+                            reg_covar=reg_covar, min_weight=min_weight, ws=self.fin_ws)
+        torch.div(ll, float(self.x.shape[0] * self.n), out=lb_out)
+
+
 @torch.no_grad()
 def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: int = 100,
         tol: float = 1e-4, init_means=None, init_covs=None, init_weights=None, verbose: bool = False,
         init_params: str = "kmeans", reg_covar: float = 1e-6, min_weight: float = 1e-8,
         compute_labels: bool = True, generator: Optional[torch.Generator] = None,
+        approx_top_k: Optional[int] = None,
         ) -> Tuple[Optional[torch.Tensor], torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, object]]:
-    """Soft EM on the HIP engine; see the module docstring."""
+    """Soft EM on the HIP engine; see the module docstring.  ``approx_top_k``
+    (1 <= k < K) restricts each row's responsibilities to its k largest logits,
+    renormalised over them, as the reference's approximate EM does."""
     if covariance_type not in _COVS:
         raise ValueError("covariance_type must be 'spherical', 'diag', 'tied' or 'full'")
     if n_components <= 0:
@@ -158,17 +227,27 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
     if not _hip.supported(covariance_type, x.dtype, bsz, n, d, k):
         raise _hip.HipRuntimeError(
             f"shape not supported by the hip backend: {covariance_type} B={bsz} N={n} D={d} K={k} {x.dtype}")
-    prob = _hip.problem(covariance_type, x.dtype, bsz, n, d, k)
-    ws = _hip.Workspace(prob, x.device)
-    gram = _hip.gram(x, ws) if covariance_type == "tied" else None
+    top_k = resolve_approx_top_k(approx_top_k, k)
+    topk_step = None
+    if top_k is None:
+        prob = _hip.problem(covariance_type, x.dtype, bsz, n, d, k)
+        ws = _hip.Workspace(prob, x.device)
+        gram = _hip.gram(x, ws) if covariance_type == "tied" else None
+    else:
+        ws = None
+        topk_step = _TopkStep(x, covariance_type, k, top_k)
+        gram = topk_step.gram() if covariance_type == "tied" else None
     lb = torch.zeros((max_iters,), dtype=torch.float32, device=x.device)
     spherical = covariance_type == "spherical"
     sync_each = bool(verbose or tol > 0.0)
     prev = None
     n_iter = 0
     for it in range(max_iters):
-        _hip.em_step(covariance_type, x, means, covs, weights, lb[it:it + 1], reg_covar=reg_covar,
-                     min_weight=min_weight, gram_xx=gram, ws=ws)
+        if topk_step is None:
+            _hip.em_step(covariance_type, x, means, covs, weights, lb[it:it + 1], reg_covar=reg_covar,
+                         min_weight=min_weight, gram_xx=gram, ws=ws)
+        else:
+            topk_step.step(means, covs, weights, lb[it:it + 1], gram, reg_covar, min_weight)
         n_iter = it + 1
         if not sync_each:
             continue
@@ -201,8 +280,8 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         "triton_fused_update_enabled": False,
         "triton_streaming_update_enabled": False,
         "triton_labels_enabled": False,
-        "approximate_em_enabled": False,
-        "approx_top_k": None,
+        "approximate_em_enabled": top_k is not None,
+        "approx_top_k": top_k,
         "backend_breakdown": {"hip": n_iter},
     }
     return labels, means, covs, weights, info
@@ -211,18 +290,16 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
 def _api(covariance_type):
     def run(x, n_components, max_iters=100, tol=1e-4, init_means=None, init_variances=None,
             init_weights=None, verbose=False, *, init_params="kmeans", reg_covar=1e-6,
-            min_weight=1e-8, compute_labels=True, generator=None, **unused):
+            min_weight=1e-8, compute_labels=True, generator=None, approx_top_k=None, **unused):
         for key in unused:
             if key not in {"chunk_size_N", "chunk_size_K", "kmeans_init_iters", "kmeans_init_tol",
                            "kmeans_use_triton", "gmm_use_triton", "gmm_use_triton_estep",
-                           "gmm_use_triton_streaming_update", "approx_top_k"}:
+                           "gmm_use_triton_streaming_update"}:
                 raise TypeError(f"unexpected keyword argument {key!r}")
-        if unused.get("approx_top_k") is not None:
-            raise NotImplementedError("approximate top-k EM is not part of the hip backend")
         return fit(x, n_components, covariance_type, max_iters=max_iters, tol=tol, init_means=init_means,
                    init_covs=init_variances, init_weights=init_weights, verbose=verbose,
                    init_params=init_params, reg_covar=reg_covar, min_weight=min_weight,
-                   compute_labels=compute_labels, generator=generator)
+                   compute_labels=compute_labels, generator=generator, approx_top_k=approx_top_k)
     run.__name__ = f"batch_gmm_{covariance_type.capitalize()}_hip"
     run.__doc__ = (f"{covariance_type} soft EM on the HIP engine; signature and return value of "
                    f"the reference's batch_gmm_*_torch_native (chunk/Triton knobs are accepted and ignored).")

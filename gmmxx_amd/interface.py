@@ -80,8 +80,9 @@ class GMMXX:
     ``covariance_type`` is ``spherical``, ``diag``/``diagonal``, ``tied`` or
     ``full``.  Supported shapes: D <= 128 (spherical, diag), D <= 64 (tied),
     D <= 16 (full); any N, K <= 65536, B <= 65535.  bf16 input is kept in bf16
-    for spherical.  ``approx_top_k`` (the reference's opt-in approximate EM)
-    is not provided and raises.
+    for spherical.  ``approx_top_k`` (1 <= k < K) opts into the reference's
+    approximate EM: each row's responsibilities cover only its k largest
+    logits; prediction stays exact.
     """
 
     def __init__(
@@ -262,8 +263,6 @@ class GMMXX:
                 and x_b.shape[1] > self.chunk_size_data_cpu)
 
     def _resolve(self, x_b: torch.Tensor, k: int) -> str:
-        if self.approx_top_k is not None:
-            raise NotImplementedError("approximate top-k EM is not provided by the hip backend")
         shape = (x_b.shape[0], x_b.shape[1], x_b.shape[2], k)
         return _dispatch.resolve_backend_with_env(self.backend, self.covariance_type, shape, x_b.dtype,
                                                   legacy_no_triton=self._legacy_no_triton)
@@ -289,13 +288,14 @@ class GMMXX:
                 x_host, self.k, self.covariance_type, device=self.device, max_iters=self.niter, tol=self.tol,
                 verbose=self.verbose, init_params=self.init_params, reg_covar=self.reg_covar,
                 chunk_size_N=self.chunk_size_data_cpu, compute_labels=self.compute_labels_on_fit,
-                seed=self.seed)
+                seed=self.seed, approx_top_k=self.approx_top_k)
         else:
             x_b = self._engine_tensor(x_b)
             self.last_backend_used_ = self._resolve(x_b, self.k)
             labels_b, means_b, covs_b, weights_b, info = em.fit(
                 x_b, self.k, self.covariance_type, max_iters=self.niter, tol=self.tol, verbose=self.verbose,
-                init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit)
+                init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit,
+                approx_top_k=self.approx_top_k)
         self.cluster_ids_b = labels_b
         self.means_b = means_b
         self.variances_b = covs_b
@@ -314,7 +314,10 @@ class GMMXX:
         self.hip_estep_enabled_ = True
         self.triton_estep_enabled_ = self.triton_fused_update_enabled_ = False
         self.triton_approx_topk_enabled_ = self.triton_streaming_update_enabled_ = False
-        self.triton_labels_enabled_ = self.approximate_em_enabled_ = False
+        self.triton_labels_enabled_ = False
+        # gmmxx/interface.py:391-392: approximation in use and its effective k
+        self.approximate_em_enabled_ = bool(info.get("approximate_em_enabled", False))
+        self.approx_top_k_ = info.get("approx_top_k")
         self.large_n_streaming_enabled_ = self.copy_stream_prefetch_enabled_ = streaming
         self.cuda_estep_enabled_ = self.cuda_fused_update_enabled_ = self.cuda_approx_topk_enabled_ = False
         self.last_backend_used_ = "hip"

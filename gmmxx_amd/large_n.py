@@ -142,8 +142,9 @@ def _sample_init(x_cpu, n_components, covariance_type, device, dtype, *, init_pa
 class _Workspaces:
     """One workspace per chunk shape (the full chunk and the last, shorter one)."""
 
-    def __init__(self, covariance_type, dtype, d, k, device):
+    def __init__(self, covariance_type, dtype, d, k, device, topk=False):
         self.cov, self.dtype, self.d, self.k, self.device = covariance_type, dtype, d, k, device
+        self.topk = topk
         self.cache: Dict[int, _hip.Workspace] = {}
 
     def get(self, rows: int) -> _hip.Workspace:
@@ -152,7 +153,8 @@ class _Workspaces:
             if not _hip.supported(self.cov, self.dtype, 1, rows, self.d, self.k):
                 raise _hip.HipRuntimeError(
                     f"shape not supported by the hip backend: {self.cov} N={rows} D={self.d} K={self.k}")
-            ws = _hip.Workspace(_hip.problem(self.cov, self.dtype, 1, rows, self.d, self.k), self.device)
+            ws = _hip.Workspace(_hip.problem(self.cov, self.dtype, 1, rows, self.d, self.k), self.device,
+                                topk=self.topk)
             self.cache[rows] = ws
         return ws
 
@@ -163,9 +165,11 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
                 verbose: bool = False, init_params: str = "kmeans", reg_covar: float = 1e-6,
                 chunk_size_N: int = 1 << 20, min_weight: float = 1e-8, compute_labels: bool = True,
                 max_init_samples: int = 65536, init_means=None, init_covs=None, init_weights=None,
-                seed: int = 0):
+                seed: int = 0, approx_top_k: Optional[int] = None):
     """Soft EM with x (1, N, D) in host memory; returns (labels, means, covariances,
-    weights, info) like gmmxx/large_n.py:866-1595 (labels on the host)."""
+    weights, info) like gmmxx/large_n.py:866-1595 (labels on the host).
+    ``approx_top_k`` selects the approximate top-k E-step per chunk, as the
+    reference's streamed loop does (gmmxx/large_n.py:1325-1370)."""
     device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     if covariance_type not in _COVS:
         raise ValueError("covariance_type must be 'spherical', 'diag', 'tied', or 'full'")
@@ -192,8 +196,12 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
             x_cpu, n_components, covariance_type, device, dtype, init_params=init_params,
             reg_covar=reg_covar, max_init_samples=max_init_samples, seed=seed)
     k = int(means.shape[1])
+    top_k = em.resolve_approx_top_k(approx_top_k, k)
     stream = ChunkStream(x_cpu, device, dtype, chunk_size_N)
     wss = _Workspaces(covariance_type, dtype, d, k, device)
+    # the top-k E-step holds a chunk's logits: sub-chunks bound that buffer
+    sub_rows = em.topk_chunk_rows(1, min(n, chunk_size_N), k) if top_k is not None else 0
+    topk_wss = _Workspaces(covariance_type, dtype, d, k, device, topk=True) if top_k is not None else None
     fin_ws = _hip.Workspace(_hip.problem(covariance_type, torch.float32, 1, 1, d, k), device)
 
     gram = None
@@ -212,14 +220,23 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
         sq = torch.zeros(q_shape, dtype=torch.float32, device=device) if q_shape else None
         ll = torch.zeros((), dtype=torch.float64, device=device)
         for _, _, xc in stream:
-            c_nk, c_sx, c_sq, c_ll = _hip.estep_stats(covariance_type, xc, means, covs, weights,
-                                                      reg_covar=reg_covar, min_weight=min_weight,
-                                                      ws=wss.get(int(xc.shape[1])))
-            nk += c_nk
-            sx += c_sx
-            if sq is not None:
-                sq += c_sq
-            ll += c_ll[0].double()
+            parts = ((xc,) if top_k is None else
+                     tuple(xc[:, r0:r0 + sub_rows] for r0 in range(0, int(xc.shape[1]), sub_rows)))
+            for xp in parts:
+                rows = int(xp.shape[1])
+                if top_k is None:
+                    c_nk, c_sx, c_sq, c_ll = _hip.estep_stats(covariance_type, xp, means, covs, weights,
+                                                              reg_covar=reg_covar, min_weight=min_weight,
+                                                              ws=wss.get(rows))
+                else:
+                    c_nk, c_sx, c_sq, c_ll = _hip.estep_stats_topk(covariance_type, xp, means, covs, weights,
+                                                                   top_k, reg_covar=reg_covar,
+                                                                   min_weight=min_weight, ws=topk_wss.get(rows))
+                nk += c_nk
+                sx += c_sx
+                if sq is not None:
+                    sq += c_sq
+                ll += c_ll[0].double()
         _hip.finalize_stats(covariance_type, nk, sx, sq, means, covs, weights, n, gram_xx=gram,
                             reg_covar=reg_covar, min_weight=min_weight, ws=fin_ws)
         value = float(ll.item()) / float(n)
@@ -247,8 +264,8 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
         "triton_approx_topk_enabled": False,
         "triton_streaming_update_enabled": False,
         "triton_labels_enabled": False,
-        "approximate_em_enabled": False,
-        "approx_top_k": None,
+        "approximate_em_enabled": top_k is not None,
+        "approx_top_k": top_k,
         "fallback_reason": None,
         "backend_breakdown": {"hip": n_iter},
     }

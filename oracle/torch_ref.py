@@ -8,8 +8,9 @@ identical seeded inputs and initial parameters.  It is never imported by the
 product package; only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` call it.
 
-Scope: the exact (non-approximate) EM path with Triton/CUDA disabled, i.e. the
-branch a CPU tensor takes through the reference.  Every function cites the
+Scope: the EM path with Triton/CUDA disabled, i.e. the branch a CPU tensor
+takes through the reference, exact and with approximate top-k responsibilities
+(``approx_top_k``).  Every function cites the
 reference lines it follows.  The arithmetic order (chunking over N and K,
 clamps, casts, the logits formulas) follows the reference op for op, because
 that order is what defines parity at fp32 rounding level.
@@ -21,7 +22,11 @@ How each part is pinned (checked independently of this restatement):
     lower-bound bookkeeping: golden vectors written by the reference's own
     torch fallback (tests/golden/make_golden.py) and closed-form known answers
     restated from the reference's tests;
-  * EM trajectory: sklearn's M-step and the golden trajectories.
+  * EM trajectory: sklearn's M-step and the golden trajectories;
+  * approximate top-k statistics: top_k = 1 equals hard-assignment group-by
+    sums over the float64 argmax, top_k = K - 1 with one unreachable component
+    equals the exact statistics, and a float64 brute force (sorted logits, then
+    scatter) on tiny inputs (tests/test_oracle_pinned.py).
 
 Difference from the reference that is deliberate: the reference records the
 lower bound of non-final iterations as 0.0 for diag/tied/full when ``tol == 0``
@@ -424,6 +429,74 @@ def _accumulate(x, x_sq_all, mdl, covariance_type, chunk_n, chunk_size_K, collec
     return nk, sum_x, sum_q, total_ll
 
 
+def _topk_logits(mdl, xc, xs, k, chunk_size_K, top_k):
+    """Running top-k over component tiles (torch_fallback.py:667-716): the
+    kept logits and their component indices, per row."""
+    bsz, n_chunk = xc.shape[0], xc.shape[1]
+    top_k = min(int(top_k), k)
+    best = torch.full((bsz, n_chunk, top_k), -torch.inf, dtype=torch.float32)
+    best_idx = torch.zeros((bsz, n_chunk, top_k), dtype=torch.long)
+    for k0 in range(0, k, chunk_size_K):
+        k1 = min(k0 + chunk_size_K, k)
+        logits = mdl.logits(xc, xs, k0, k1).to(torch.float32)
+        idx = torch.arange(k0, k1, dtype=torch.long).view(1, 1, k1 - k0).expand(bsz, n_chunk, k1 - k0)
+        cand = torch.cat((best, logits), dim=-1)
+        cand_idx = torch.cat((best_idx, idx), dim=-1)
+        best, pos = cand.topk(top_k, dim=-1)
+        best_idx = cand_idx.gather(-1, pos)
+    return best, best_idx
+
+
+def _accumulate_topk(x, x_sq_all, mdl, covariance_type, chunk_n, chunk_size_K, top_k):
+    """Approximate top-k sufficient statistics (torch_fallback.py:719-777):
+    responsibilities over each row's top-k components only, scattered into the
+    statistics; the log-likelihood sums the top-k log-normalisers."""
+    bsz, n, d = x.shape
+    k = mdl.k
+    spherical = covariance_type == "spherical"
+    nk = torch.zeros((bsz, k), dtype=torch.float32)
+    sum_x = torch.zeros((bsz, k, d), dtype=torch.float32)
+    sum_q = {"spherical": lambda: torch.zeros((bsz, k), dtype=torch.float32),
+             "diag": lambda: torch.zeros((bsz, k, d), dtype=torch.float32),
+             "full": lambda: torch.zeros((bsz, k, d, d), dtype=torch.float32)}.get(covariance_type, lambda: None)()
+    total_ll = torch.zeros((), dtype=torch.float32)
+    for n0 in range(0, n, chunk_n):
+        n1 = min(n0 + chunk_n, n)
+        xc = x[:, n0:n1, :]
+        xcf = xc.to(torch.float32)
+        xs = x_sq_all[:, n0:n1] if spherical else None
+        tl, ti = _topk_logits(mdl, xc, xs, k, chunk_size_K, top_k)
+        lse = torch.logsumexp(tl, dim=-1)
+        resp = torch.exp(tl - lse.unsqueeze(-1))
+        total_ll = total_ll + lse.sum()
+        for j in range(tl.shape[-1]):
+            idx, r = ti[:, :, j], resp[:, :, j]
+            nk.scatter_add_(1, idx, r)
+            sum_x.scatter_add_(1, idx.unsqueeze(-1).expand(-1, -1, d), r.unsqueeze(-1) * xcf)
+            if spherical:
+                sum_q.scatter_add_(1, idx, r * xs)
+            elif covariance_type == "diag":
+                sum_q.scatter_add_(1, idx.unsqueeze(-1).expand(-1, -1, d), r.unsqueeze(-1) * xcf.square())
+            elif covariance_type == "full":
+                outer = xcf.unsqueeze(-1) * xcf.unsqueeze(-2)
+                sum_q.scatter_add_(1, idx[:, :, None, None].expand(-1, -1, d, d), r[:, :, None, None] * outer)
+    return nk, sum_x, sum_q, total_ll
+
+
+@torch.no_grad()
+def estep_stats_topk(x, covariance_type, means, covs, weights, top_k, *, reg_covar=1e-6, min_weight=1e-8,
+                     chunk_size_N=DEFAULT_CHUNK_N, chunk_size_K=DEFAULT_CHUNK_K):
+    """estep_stats with approximate top-k responsibilities (1 <= top_k < K)."""
+    spherical = covariance_type == "spherical"
+    if covariance_type in ("spherical", "diag"):
+        covs = covs.clamp_min(reg_covar)
+    weights = weights.clamp_min(min_weight)
+    weights = weights / weights.sum(dim=-1, keepdim=True)
+    mdl = _Model(covariance_type, means, covs, weights)
+    x_sq_all = (x.to(torch.float32) ** 2).sum(dim=-1) if spherical else None
+    return _accumulate_topk(x, x_sq_all, mdl, covariance_type, chunk_size_N, chunk_size_K, top_k)
+
+
 @torch.no_grad()
 def estep_stats(x, covariance_type, means, covs, weights, *, reg_covar=1e-6, min_weight=1e-8,
                 chunk_size_N=DEFAULT_CHUNK_N, chunk_size_K=DEFAULT_CHUNK_K):
@@ -489,6 +562,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         reg_covar: float = 1e-6, min_weight: float = 1e-8,
         chunk_size_N: int = DEFAULT_CHUNK_N, chunk_size_K: int = DEFAULT_CHUNK_K,
         compute_labels: bool = True, record_all_lower_bounds: bool = True,
+        approx_top_k: Optional[int] = None,
         ) -> Tuple[Optional[torch.Tensor], torch.Tensor, torch.Tensor, torch.Tensor, Dict]:
     """Soft EM with explicit initial parameters, for one covariance type.
 
@@ -516,6 +590,10 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
     means, covs, weights = init_user_parameters(x, covariance_type, init_means, init_covs,
                                                 init_weights, reg_covar, x_sq=x_sq_all)
     chunk_n = _spherical_chunk_n(n, d, k, chunk_size_N) if spherical else chunk_size_N
+    # _resolve_approx_top_k (torch_fallback.py:598-606): top_k >= K is exact EM.
+    if approx_top_k is not None and int(approx_top_k) <= 0:
+        raise ValueError("approx_top_k must be positive or None")
+    top_k = int(approx_top_k) if approx_top_k is not None and int(approx_top_k) < k else None
 
     total_xx = None
     if covariance_type == "tied":                                   # :2856-2862
@@ -536,8 +614,12 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         weights = weights / weights.sum(dim=-1, keepdim=True)
         mdl = _Model(covariance_type, means, covs, weights)
 
-        nk, sum_x, sum_q, total_ll = _accumulate(x, x_sq_all, mdl, covariance_type, chunk_n,
-                                                 chunk_size_K, collect)
+        if top_k is not None:
+            nk, sum_x, sum_q, total_ll = _accumulate_topk(x, x_sq_all, mdl, covariance_type, chunk_n,
+                                                          chunk_size_K, top_k)
+        else:
+            nk, sum_x, sum_q, total_ll = _accumulate(x, x_sq_all, mdl, covariance_type, chunk_n,
+                                                     chunk_size_K, collect)
 
         means_new, covs_new, weights_new = finalize(
             covariance_type, nk, sum_x, sum_q, means, covs, n=n, reg_covar=reg_covar,
@@ -565,7 +647,8 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
                         chunk_size_N=chunk_n if covariance_type == "tied" else chunk_size_N,
                         chunk_size_K=chunk_size_K)
     info = {"n_iter": iteration + 1, "lower_bound": history[-1],
-            "lower_bound_history": history, "init_source": "user"}
+            "lower_bound_history": history, "init_source": "user",
+            "approximate_em_enabled": top_k is not None, "approx_top_k": top_k}
     return labels, means, covs, weights, info
 
 

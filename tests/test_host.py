@@ -242,10 +242,19 @@ def test_fit_on_cpu_device_refuses():
         est.fit(torch.randn(16, 3))
 
 
-def test_approx_top_k_not_provided(monkeypatch):
-    est = GMMXX(k=2, approx_top_k=1)
-    with pytest.raises(NotImplementedError):
-        est._resolve(torch.zeros(1, 4, 2), 2)
+def test_approx_top_k_resolution():
+    """gmmxx/torch_fallback.py:598-606: None and k >= K are exact EM."""
+    from gmmxx_amd import em
+    assert em.resolve_approx_top_k(None, 4) is None
+    assert em.resolve_approx_top_k(4, 4) is None and em.resolve_approx_top_k(9, 4) is None
+    assert em.resolve_approx_top_k(3, 4) == 3
+    with pytest.raises(ValueError):
+        em.resolve_approx_top_k(0, 4)
+    assert em.topk_chunk_rows(1, 100, 8) == 100
+    rows = em.topk_chunk_rows(2, 10 ** 9, 1024)
+    assert rows % 32 == 0 and 2 * rows * 1024 * 4 <= 1 << 30
+    with pytest.raises(ValueError):
+        GMMXX(k=2, approx_top_k=0)
 
 
 def _fitted(cov, b, k, d, rng):

@@ -11,7 +11,10 @@
   (tests/test_cuda_spherical_safe.py:151-179, tests/test_cuda_diag_safe.py:153-189,
   tests/test_cuda_soft_em_non_spherical.py:95-132) under the torch-fallback
   conventions (weight floor 1e-8 and renormalisation instead of w=0);
-* invariants: EM never decreases the log-likelihood, responsibilities sum to 1.
+* invariants: EM never decreases the log-likelihood, responsibilities sum to 1;
+* approximate top-k statistics: a float64 brute force over sorted scipy logits,
+  hard assignment at top_k = 1, exact EM at top_k = K - 1 when the dropped
+  component is unreachable.
 """
 
 import math
@@ -212,3 +215,87 @@ def test_em_invariants(cov):
     torch.testing.assert_close(wt.sum(-1), torch.ones(2), atol=1e-6, rtol=0)
     p = torch_ref.predict_proba(x, m, c, wt, cov)
     torch.testing.assert_close(p.sum(-1), torch.ones(2, 300), atol=1e-5, rtol=0)
+
+
+def _topk_stats64(cov, x, logits64, top_k):
+    """Brute force in float64: per row, sort the logits (value descending, then
+    index ascending), keep the first top_k, normalise over them and scatter."""
+    b, n, d = x.shape
+    k = logits64.shape[-1]
+    xn = x.double().numpy()
+    nk, sx = np.zeros((b, k)), np.zeros((b, k, d))
+    sq = {"spherical": np.zeros((b, k)), "diag": np.zeros((b, k, d)), "full": np.zeros((b, k, d, d))}.get(cov)
+    ll = 0.0
+    for bi in range(b):
+        for i in range(n):
+            keep = sorted(range(k), key=lambda j: (-logits64[bi, i, j], j))[:top_k]
+            v = logits64[bi, i, keep]
+            lse = float(logsumexp(v))
+            ll += lse
+            row = xn[bi, i]
+            for j, val in zip(keep, v):
+                r = math.exp(val - lse)
+                nk[bi, j] += r
+                sx[bi, j] += r * row
+                if cov == "spherical":
+                    sq[bi, j] += r * float(row @ row)
+                elif cov == "diag":
+                    sq[bi, j] += r * row * row
+                elif cov == "full":
+                    sq[bi, j] += r * np.outer(row, row)
+    return nk, sx, sq, ll
+
+
+@pytest.mark.parametrize("cov", COVS)
+@pytest.mark.parametrize("top_k", [1, 2, 4])
+def test_topk_stats_vs_float64_brute_force(cov, top_k):
+    x, means, covs, w = _problem(cov, b=2, n=50, d=3, k=5, seed=11)
+    nk, sx, sq, ll = torch_ref.estep_stats_topk(x, cov, means, covs, w, top_k)
+    e_nk, e_sx, e_sq, e_ll = _topk_stats64(cov, x, _ref_logits64(cov, x, means, covs, w), top_k)
+    np.testing.assert_allclose(nk.double().numpy(), e_nk, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(sx.double().numpy(), e_sx, rtol=1e-4, atol=1e-4)
+    if sq is not None:
+        np.testing.assert_allclose(sq.double().numpy(), e_sq, rtol=1e-4, atol=1e-4)
+    assert float(ll) == pytest.approx(e_ll, rel=1e-5)
+
+
+@pytest.mark.parametrize("cov", COVS)
+def test_topk_one_is_hard_assignment(cov):
+    """top_k = 1: every row's whole mass goes to its argmax, so the statistics
+    are group-by sums over the float64 labels and the log-likelihood sums the
+    maximum logits."""
+    x, means, covs, w = _problem(cov, b=1, n=80, d=3, k=4, seed=12)
+    ref = _ref_logits64(cov, x, means, covs, w)
+    lab = ref.argmax(-1)[0]
+    nk, sx, sq, ll = torch_ref.estep_stats_topk(x, cov, means, covs, w, 1)
+    xn = x[0].double().numpy()
+    np.testing.assert_allclose(nk[0].double().numpy(), np.bincount(lab, minlength=4), rtol=0, atol=1e-6)
+    for j in range(4):
+        np.testing.assert_allclose(sx[0, j].double().numpy(), xn[lab == j].sum(0), rtol=1e-5, atol=1e-4)
+    assert float(ll) == pytest.approx(ref.max(-1).sum(), rel=1e-5)
+
+
+@pytest.mark.parametrize("cov", COVS)
+def test_topk_all_but_unreachable_equals_exact(cov):
+    """top_k = K - 1 with one component no row can reach: the dropped logit is
+    always that component's and its responsibility underflows to zero in exact
+    EM, so the approximate statistics equal the exact ones."""
+    x, means, covs, w = _problem(cov, b=1, n=80, d=3, k=4, seed=13)
+    means = means.clone()
+    means[0, 2] = 500.0
+    approx = torch_ref.estep_stats_topk(x, cov, means, covs, w, 3)
+    exact = torch_ref.estep_stats(x, cov, means, covs, w)
+    for a, e in zip(approx, exact):
+        if e is not None:
+            torch.testing.assert_close(a, e, rtol=1e-5, atol=1e-5)
+    # and a fit with approx_top_k = K - 1 follows exact EM
+    _, m1, c1, w1, i1 = torch_ref.fit(x, 4, cov, max_iters=3, tol=0.0, init_means=means, init_covs=covs,
+                                      init_weights=w, approx_top_k=3)
+    _, m2, c2, w2, i2 = torch_ref.fit(x, 4, cov, max_iters=3, tol=0.0, init_means=means, init_covs=covs,
+                                      init_weights=w)
+    assert i1["approximate_em_enabled"] and i1["approx_top_k"] == 3 and not i2["approximate_em_enabled"]
+    torch.testing.assert_close(m1, m2, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(i1["lower_bound_history"], i2["lower_bound_history"], rtol=1e-6)
+    # top_k >= K resolves to exact EM (gmmxx/torch_fallback.py:598-606)
+    assert torch_ref.fit(x, 4, cov, max_iters=1, init_means=means, init_covs=covs, init_weights=w,
+                         approx_top_k=4)[4]["approximate_em_enabled"] is False
