@@ -64,6 +64,8 @@ def _declare(lib):
         "gmmxx_hip_predict_proba": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_gram": (ctypes.c_int, [P, vp, vp, vp, i64, vp]),
         "gmmxx_hip_finalize_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, i64, vp]),
+        "gmmxx_hip_kmeans_pp_workspace_bytes": (i64, [i64, i64, i64, i64, ctypes.c_int]),
+        "gmmxx_hip_kmeans_pp": (ctypes.c_int, [vp, i64, i64, i64, i64, ctypes.c_int, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_topk_workspace_bytes": (i64, [P]),
         "gmmxx_hip_estep_stats_topk": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, ctypes.c_int, vp, vp, vp,
                                                       vp, vp, i64, vp]),
@@ -80,7 +82,7 @@ def exported_symbols() -> Tuple[str, ...]:
             "gmmxx_hip_supported", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_phase",
             "gmmxx_hip_estep_stats", "gmmxx_hip_score", "gmmxx_hip_predict_proba",
             "gmmxx_hip_gram", "gmmxx_hip_finalize_stats", "gmmxx_hip_topk_workspace_bytes",
-            "gmmxx_hip_estep_stats_topk")
+            "gmmxx_hip_estep_stats_topk", "gmmxx_hip_kmeans_pp_workspace_bytes", "gmmxx_hip_kmeans_pp")
 
 
 def load_library(path: Optional[str] = None):
@@ -329,6 +331,36 @@ def estep_stats_topk(covariance_type: str, x: torch.Tensor, means: torch.Tensor,
                                            _ptr(sum_x), _ptr(sum_q), _ptr(ll), ws.ptr, ws.nbytes, _stream(dev)),
            "gmmxx_hip_estep_stats_topk")
     return nk, sum_x, sum_q, ll
+
+
+def kmeans_pp(sample: torch.Tensor, n_components: int, first_idx: torch.Tensor, draws: torch.Tensor) -> torch.Tensor:
+    """Greedy k-means++ centres (B, K, D) fp32 from a row sample (B, S, D), with the
+    random numbers given: ``first_idx`` (B,) int64 and ``draws`` (B, K-1, T) uniform
+    in [0, 1), T candidates per step (gmmxx/torch_fallback.py:1390-1451)."""
+    require_hip()
+    sample = _device_tensor(sample, "sample", torch.float32)
+    if sample.ndim != 3:
+        raise ValueError("sample must have shape (B, S, D)")
+    B, S, D = (int(v) for v in sample.shape)
+    K = int(n_components)
+    dev = sample.device
+    first_idx = first_idx.to(device=dev, dtype=torch.int64).contiguous()
+    draws = draws.to(device=dev, dtype=torch.float32).contiguous()
+    if tuple(first_idx.shape) != (B,):
+        raise ValueError("first_idx must have shape (B,)")
+    if draws.ndim != 3 or draws.shape[0] != B or draws.shape[1] != K - 1:
+        raise ValueError("draws must have shape (B, K-1, trials)")
+    trials = int(draws.shape[2]) if K > 1 else 1
+    need = int(_lib.gmmxx_hip_kmeans_pp_workspace_bytes(B, S, D, K, trials))
+    if need < 0:
+        raise ValueError("k-means++ needs 1 <= K <= S <= 65536, D <= 1024 and 1 <= trials <= 16")
+    buf = torch.empty(need + 256, dtype=torch.uint8, device=dev)
+    base = buf.data_ptr()
+    centers = torch.empty((B, K, D), dtype=torch.float32, device=dev)
+    _check(_lib.gmmxx_hip_kmeans_pp(_ptr(sample), B, S, D, K, trials, _ptr(first_idx), _ptr(draws),
+                                    _ptr(centers), ctypes.c_void_p(base + (-base) % 256), need, _stream(dev)),
+           "gmmxx_hip_kmeans_pp")
+    return centers
 
 
 def finalize_stats(covariance_type: str, nk: torch.Tensor, sum_x: torch.Tensor, sum_q: Optional[torch.Tensor],

@@ -701,4 +701,38 @@ int gmmxx_hip_gram(const gmmxx_problem* p, const void* x, float* out, void* ws, 
   return check_hip("gram");
 }
 
+int64_t gmmxx_hip_kmeans_pp_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t K, int trials) {
+  if (B < 1 || B > 65535 || S < 1 || S > kKppMaxRows || D < 1 || D > 1024 || K < 1 || K > S || trials < 1 ||
+      trials > kKppMaxTrials)
+    return -1;
+  return kpp_workspace_bytes((int)B, (int)S, (int)K, trials);
+}
+
+int gmmxx_hip_kmeans_pp(const float* sample, int64_t B, int64_t S, int64_t D, int64_t K, int trials,
+                        const int64_t* first_idx, const float* draws, float* centers, void* ws, int64_t ws_bytes,
+                        void* stream) {
+  const int64_t need = gmmxx_hip_kmeans_pp_workspace_bytes(B, S, D, K, trials);
+  if (need < 0)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT,
+                "k-means++ needs 1 <= B <= 65535, 1 <= K <= S <= 65536, 1 <= D <= 1024, 1 <= trials <= 16");
+  if (!sample || !first_idx || !centers || (K > 1 && !draws)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  if (!ws) return fail(GMMXX_ERR_WORKSPACE, "workspace is NULL");
+  if (ws_bytes < need) return fail(GMMXX_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
+  if ((uintptr_t)ws % 256 != 0) return fail(GMMXX_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  KppArgs a{};
+  a.sample = sample;
+  a.B = (int)B;
+  a.S = (int)S;
+  a.D = (int)D;
+  a.K = (int)K;
+  a.T = trials;
+  a.vec = (D % 4 == 0) && ((uintptr_t)sample % 16 == 0);
+  a.first = first_idx;
+  a.draws = draws;
+  a.centers = centers;
+  kpp_bind_workspace(a, ws);
+  launch_kpp(a, (hipStream_t)stream);
+  return check_hip("k-means++ seeding");
+}
+
 }  // extern "C"

@@ -82,4 +82,26 @@ int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s);
 // *value = NaN when the cooperative pass reported a timed-out wait (status != 0).
 void launch_coop_check(const unsigned* status, float* value, hipStream_t s);
 
+// Greedy k-means++ seeding (kmeans.hip).  Row sample [B][S][D] fp32; the first
+// centre's row index per batch and T uniform draws per later centre are inputs.
+constexpr int kKppMaxTrials = 16;
+constexpr int kKppMaxRows = 65536;
+struct KppArgs {
+  const float* sample;         // [B][S][D]
+  int B, S, D, K, T;
+  int vec;                     // rows 16-byte aligned and D % 4 == 0
+  const int64_t* first;        // [B]
+  const float* draws;          // [B][K-1][T] in [0, 1)
+  float* centers;              // [B][K][D]
+  // workspace (kpp_bind_workspace)
+  float* closest;              // [B][S]
+  float* dist;                 // [B][kKppMaxTrials][S]
+  float* pot_part;             // [B][nblk][kKppMaxTrials]
+  int* cand;                   // [B][kKppMaxTrials]
+  int nblk;
+};
+int64_t kpp_workspace_bytes(int B, int S, int K, int T);
+void kpp_bind_workspace(KppArgs& a, void* ws);
+void launch_kpp(const KppArgs& a, hipStream_t s);
+
 }  // namespace gx

@@ -81,14 +81,16 @@ def _init_weights(init_weights, bsz, k, device):
 
 def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init_means=None,
                init_covs=None, init_weights=None, reg_covar: float = 1e-6,
-               init_params: str = "kmeans", generator: Optional[torch.Generator] = None):
+               init_params: str = "kmeans", generator: Optional[torch.Generator] = None,
+               kmeans_init_iters: int = 10, kmeans_init_tol: float = 1e-4):
     """Initial (means, covariances, weights, source), fp32 on x's device.
 
     Explicit parameters get the reference's entry clamps
     (torch_fallback.py:1661-1682, :1731-1742, :1791-1802, :1851-1862).  Without
-    ``init_means`` the reference's ``kmeans``/``random`` initialisers reduce to
-    random data rows plus the global variance when flash-kmeans is absent
-    (:1580-1582, :1706-1714); rows are drawn on the device.
+    ``init_means``, ``init_params="kmeans"`` runs k-means++ seeding, Lloyd
+    refinement and the hard-label statistics on the device (``kmeans.py``; the
+    reference's branch at :1701-1716, :1747-1762, :1807-1822, :1867-1882), and
+    ``"random"`` takes random data rows plus the global variance (:1718-1727).
     """
     bsz, n, d = x.shape
     dev = x.device
@@ -102,6 +104,12 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
         if init_params not in {"kmeans", "random"}:
             raise ValueError("init_params must be 'kmeans' or 'random'")
         k = int(n_components)
+        if init_params == "kmeans":
+            from . import kmeans
+            means, covs, weights = kmeans.kmeans_initialize(
+                x, covariance_type, k, max_iters=kmeans_init_iters, tol=kmeans_init_tol, reg_covar=reg_covar,
+                generator=generator)
+            return means, covs, weights, "kmeans"
         idx = torch.randint(0, n, (bsz, k), device=dev, generator=generator)
         means = torch.gather(x, 1, idx[..., None].expand(-1, -1, d)).to(torch.float32).contiguous()
         source = "random"
@@ -185,13 +193,17 @@ class _TopkStep:
             total = g if total is None else total + g
         return total
 
-    def step(self, means, covs, weights, lb_out, gram, reg_covar, min_weight):
+    def stats(self, means, covs, weights, reg_covar, min_weight):
+        """(nk, sum_x, sum_q, ll_sum) of the top-k E-step, summed over the chunks."""
         tot = None
         for xc, ws in self.chunks():
             part = _hip.estep_stats_topk(self.cov, xc, means, covs, weights, self.top_k, reg_covar=reg_covar,
                                          min_weight=min_weight, ws=ws)
             tot = list(part) if tot is None else [a if a is None else a + b for a, b in zip(tot, part)]
-        nk, sum_x, sum_q, ll = tot
+        return tot
+
+    def step(self, means, covs, weights, lb_out, gram, reg_covar, min_weight):
+        nk, sum_x, sum_q, ll = self.stats(means, covs, weights, reg_covar, min_weight)
         _hip.finalize_stats(self.cov, nk, sum_x, sum_q, means, covs, weights, self.n, gram_xx=gram,
                             reg_covar=reg_covar, min_weight=min_weight, ws=self.fin_ws)
         torch.div(ll, float(self.x.shape[0] * self.n), out=lb_out)
@@ -202,7 +214,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         tol: float = 1e-4, init_means=None, init_covs=None, init_weights=None, verbose: bool = False,
         init_params: str = "kmeans", reg_covar: float = 1e-6, min_weight: float = 1e-8,
         compute_labels: bool = True, generator: Optional[torch.Generator] = None,
-        approx_top_k: Optional[int] = None,
+        approx_top_k: Optional[int] = None, kmeans_init_iters: int = 10, kmeans_init_tol: float = 1e-4,
         ) -> Tuple[Optional[torch.Tensor], torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, object]]:
     """Soft EM on the HIP engine; see the module docstring.  ``approx_top_k``
     (1 <= k < K) restricts each row's responsibilities to its k largest logits,
@@ -222,7 +234,8 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         raise ValueError("x must contain at least one sample")
     means, covs, weights, source = initialize(
         x, covariance_type, n_components, init_means=init_means, init_covs=init_covs,
-        init_weights=init_weights, reg_covar=reg_covar, init_params=init_params, generator=generator)
+        init_weights=init_weights, reg_covar=reg_covar, init_params=init_params, generator=generator,
+        kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol)
     k = means.shape[1]
     if not _hip.supported(covariance_type, x.dtype, bsz, n, d, k):
         raise _hip.HipRuntimeError(
@@ -290,16 +303,17 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
 def _api(covariance_type):
     def run(x, n_components, max_iters=100, tol=1e-4, init_means=None, init_variances=None,
             init_weights=None, verbose=False, *, init_params="kmeans", reg_covar=1e-6,
-            min_weight=1e-8, compute_labels=True, generator=None, approx_top_k=None, **unused):
+            min_weight=1e-8, compute_labels=True, generator=None, approx_top_k=None, kmeans_init_iters=10,
+            kmeans_init_tol=1e-4, **unused):
         for key in unused:
-            if key not in {"chunk_size_N", "chunk_size_K", "kmeans_init_iters", "kmeans_init_tol",
-                           "kmeans_use_triton", "gmm_use_triton", "gmm_use_triton_estep",
-                           "gmm_use_triton_streaming_update"}:
+            if key not in {"chunk_size_N", "chunk_size_K", "kmeans_use_triton", "gmm_use_triton",
+                           "gmm_use_triton_estep", "gmm_use_triton_streaming_update"}:
                 raise TypeError(f"unexpected keyword argument {key!r}")
         return fit(x, n_components, covariance_type, max_iters=max_iters, tol=tol, init_means=init_means,
                    init_covs=init_variances, init_weights=init_weights, verbose=verbose,
                    init_params=init_params, reg_covar=reg_covar, min_weight=min_weight,
-                   compute_labels=compute_labels, generator=generator, approx_top_k=approx_top_k)
+                   compute_labels=compute_labels, generator=generator, approx_top_k=approx_top_k,
+                   kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol)
     run.__name__ = f"batch_gmm_{covariance_type.capitalize()}_hip"
     run.__doc__ = (f"{covariance_type} soft EM on the HIP engine; signature and return value of "
                    f"the reference's batch_gmm_*_torch_native (chunk/Triton knobs are accepted and ignored).")

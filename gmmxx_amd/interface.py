@@ -288,14 +288,16 @@ class GMMXX:
                 x_host, self.k, self.covariance_type, device=self.device, max_iters=self.niter, tol=self.tol,
                 verbose=self.verbose, init_params=self.init_params, reg_covar=self.reg_covar,
                 chunk_size_N=self.chunk_size_data_cpu, compute_labels=self.compute_labels_on_fit,
-                seed=self.seed, approx_top_k=self.approx_top_k)
+                seed=self.seed, approx_top_k=self.approx_top_k, kmeans_init_iters=self.init_kmeans_iters,
+                kmeans_init_tol=self.init_kmeans_tol)
         else:
             x_b = self._engine_tensor(x_b)
             self.last_backend_used_ = self._resolve(x_b, self.k)
             labels_b, means_b, covs_b, weights_b, info = em.fit(
                 x_b, self.k, self.covariance_type, max_iters=self.niter, tol=self.tol, verbose=self.verbose,
                 init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit,
-                approx_top_k=self.approx_top_k)
+                approx_top_k=self.approx_top_k, kmeans_init_iters=self.init_kmeans_iters,
+                kmeans_init_tol=self.init_kmeans_tol)
         self.cluster_ids_b = labels_b
         self.means_b = means_b
         self.variances_b = covs_b

@@ -118,7 +118,7 @@ class ChunkStream:
 
 
 def _sample_init(x_cpu, n_components, covariance_type, device, dtype, *, init_params, reg_covar,
-                 max_init_samples, seed):
+                 max_init_samples, seed, kmeans_init_iters=10, kmeans_init_tol=1e-4):
     """Random-row sample of at most max_init_samples rows (gmmxx/large_n.py:630-646),
     then the in-memory initialiser on it (:649-735)."""
     n = int(x_cpu.shape[1])
@@ -133,7 +133,9 @@ def _sample_init(x_cpu, n_components, covariance_type, device, dtype, *, init_pa
     sample = sample_cpu.to(device=device, dtype=dtype).contiguous()
     dg = torch.Generator(device=device).manual_seed(int(seed))
     means, covs, weights, source = em.initialize(sample, covariance_type, n_components, reg_covar=reg_covar,
-                                                 init_params=init_params, generator=dg)
+                                                 init_params=init_params, generator=dg,
+                                                 kmeans_init_iters=kmeans_init_iters,
+                                                 kmeans_init_tol=kmeans_init_tol)
     if sample_n < n:
         source = f"{source}_sampled"
     return means, covs, weights, source, sample_n
@@ -165,7 +167,8 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
                 verbose: bool = False, init_params: str = "kmeans", reg_covar: float = 1e-6,
                 chunk_size_N: int = 1 << 20, min_weight: float = 1e-8, compute_labels: bool = True,
                 max_init_samples: int = 65536, init_means=None, init_covs=None, init_weights=None,
-                seed: int = 0, approx_top_k: Optional[int] = None):
+                seed: int = 0, approx_top_k: Optional[int] = None, kmeans_init_iters: int = 10,
+                kmeans_init_tol: float = 1e-4):
     """Soft EM with x (1, N, D) in host memory; returns (labels, means, covariances,
     weights, info) like gmmxx/large_n.py:866-1595 (labels on the host).
     ``approx_top_k`` selects the approximate top-k E-step per chunk, as the
@@ -194,7 +197,8 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
     else:
         means, covs, weights, source, sample_n = _sample_init(
             x_cpu, n_components, covariance_type, device, dtype, init_params=init_params,
-            reg_covar=reg_covar, max_init_samples=max_init_samples, seed=seed)
+            reg_covar=reg_covar, max_init_samples=max_init_samples, seed=seed,
+            kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol)
     k = int(means.shape[1])
     top_k = em.resolve_approx_top_k(approx_top_k, k)
     stream = ChunkStream(x_cpu, device, dtype, chunk_size_N)

@@ -169,6 +169,22 @@ int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* 
 int gmmxx_hip_gram(const gmmxx_problem* p, const void* x, float* out, void* workspace,
                    int64_t workspace_bytes, void* stream);
 
+/* Greedy k-means++ seeding of K centres (B, K, D) fp32 from a row sample
+ * (B, S, D) fp32: centre 0 is row first_idx[b] (int64, clamped to [0, S)); each
+ * later centre c is the best of `trials` candidates drawn by D² sampling with
+ * the uniform numbers draws[b][c-1][0..trials) in [0, 1) -- the row where the
+ * running sum of squared distances to the nearest centre first reaches
+ * u·total (the last row beyond the total, row 0 when the total is 0) -- best
+ * meaning the least potential Σ_i min(closest_i, ‖s_i - c‖²), first on ties.
+ * 1 <= K <= S <= 65536, D <= 1024, trials <= 16.  The workspace takes
+ * gmmxx_hip_kmeans_pp_workspace_bytes bytes (-1: arguments out of range).
+ * Replaces _kmeans_plus_plus_init_means (gmmxx/torch_fallback.py:1390-1451),
+ * which draws the same numbers with torch.randint / torch.rand. */
+int64_t gmmxx_hip_kmeans_pp_workspace_bytes(int64_t B, int64_t S, int64_t D, int64_t K, int trials);
+int gmmxx_hip_kmeans_pp(const float* sample, int64_t B, int64_t S, int64_t D, int64_t K, int trials,
+                        const int64_t* first_idx, const float* draws, float* centers, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,7 +26,13 @@ How each part is pinned (checked independently of this restatement):
   * approximate top-k statistics: top_k = 1 equals hard-assignment group-by
     sums over the float64 argmax, top_k = K - 1 with one unreachable component
     equals the exact statistics, and a float64 brute force (sorted logits, then
-    scatter) on tiny inputs (tests/test_oracle_pinned.py).
+    scatter) on tiny inputs (tests/test_oracle_pinned.py);
+  * k-means initialisation: k-means++ against an independent float64 numpy
+    implementation fed the same random numbers, K = S taking every row once,
+    one seed per well-separated blob; Lloyd against a float64 brute force and
+    the closed-form blob means; hard-label statistics against float64 loops
+    (tests/test_oracle_kmeans.py).  The Lloyd stopping rule restates
+    flash-kmeans (absent here) and is not pinned.
 
 Difference from the reference that is deliberate: the reference records the
 lower bound of non-final iterations as 0.0 for diag/tied/full when ``tol == 0``
@@ -660,3 +666,118 @@ def fit_one_iteration_stats(x, covariance_type, means, covs, weights, reg_covar=
                            init_means=means, init_covs=covs, init_weights=weights,
                            reg_covar=reg_covar, min_weight=min_weight, compute_labels=False)
     return m, c, w, info["lower_bound"]
+
+
+# ---------------------------------------------------------------------------
+# k-means initialisation (init_params="kmeans", torch_fallback.py:1390-1631)
+# ---------------------------------------------------------------------------
+
+def kmeans_pp(sample, k, first_idx, draws):
+    """Greedy k-means++ on a row sample (torch_fallback.py:1390-1451, its
+    vectorised branch) with the random numbers given instead of drawn:
+    ``first_idx`` (B,) replaces torch.randint and ``draws[:, c-1, :]`` (B, T)
+    the torch.rand of step c.  Returns the centres (B, K, D) fp32."""
+    bsz, s, d = sample.shape
+    sf = sample.to(torch.float32)
+    bidx = torch.arange(bsz)
+    centers = torch.empty((bsz, k, d), dtype=torch.float32)
+    centers[:, 0, :] = sf[bidx, first_idx]
+    closest = (sf - centers[:, 0:1, :]).square().sum(dim=-1)
+    for c in range(1, k):
+        dist_sum = closest.sum(dim=1)
+        cumulative = closest.cumsum(dim=1)
+        targets = draws[:, c - 1, :].to(torch.float32) * dist_sum.unsqueeze(1)
+        cand = torch.searchsorted(cumulative, targets).clamp_max(s - 1)
+        cand = torch.where(dist_sum.unsqueeze(1) > 0, cand, torch.zeros_like(cand))
+        cands = sf[bidx[:, None], cand]                                   # (B, T, D)
+        new_dist = (sf.unsqueeze(2) - cands.unsqueeze(1)).square().sum(dim=-1)
+        trial = torch.minimum(closest.unsqueeze(-1), new_dist)            # (B, S, T)
+        best = trial.sum(dim=1).argmin(dim=1)
+        centers[:, c, :] = sf[bidx, cand[bidx, best]]
+        closest = trial[bidx, :, best]
+    return centers
+
+
+def lloyd(x, centers, max_iters, tol, chunk_n=DEFAULT_CHUNK_N):
+    """Lloyd k-means from ``centers``: assign every row to its nearest centre
+    (first on ties), move each centre to the mean of its rows (an empty cluster
+    keeps its centre), stop after max_iters or when tol > 0 and no centre moved
+    by tol or more.  This restates flash-kmeans' batch_kmeans_Euclid
+    (flash-kmeans>=0.2, not in the reference tree; called at
+    torch_fallback.py:1588-1622) from the textbook algorithm: the stopping rule
+    is an assumption.  Returns (labels of the last assignment, centres, iterations)."""
+    bsz, n, d = x.shape
+    k = centers.shape[1]
+    xf = x.to(torch.float32)
+    means = centers.to(torch.float32).clone()
+    labels = None
+    it = 0
+    for it in range(1, max(1, int(max_iters)) + 1):
+        labels = torch.empty((bsz, n), dtype=torch.long)
+        for n0 in range(0, n, chunk_n):
+            xc = xf[:, n0:n0 + chunk_n]
+            dist = (xc.unsqueeze(2) - means.unsqueeze(1)).square().sum(dim=-1)
+            labels[:, n0:n0 + chunk_n] = dist.argmin(dim=-1)
+        counts = torch.zeros((bsz, k), dtype=torch.float32)
+        sums = torch.zeros((bsz, k, d), dtype=torch.float32)
+        for b in range(bsz):
+            counts[b].index_add_(0, labels[b], torch.ones(n))
+            sums[b].index_add_(0, labels[b], xf[b])
+        new = torch.where((counts > 0).unsqueeze(-1), sums / counts.clamp_min(1.0).unsqueeze(-1), means)
+        shift = float((new - means).norm(dim=-1).max())
+        means = new
+        if tol > 0.0 and shift < tol:
+            break
+    return labels, means, it
+
+
+def hard_label_init_stats(x, covariance_type, means, labels, reg_covar):
+    """Initial (weights, covariances) from hard labels and centres, by
+    _hard_label_init_stats (torch_fallback.py:1453-1477), _diag (:1480-1504),
+    _tied (:1544-1566) and _full (:1507-1541): direct differences to the
+    assigned centre, weights ∝ max(count, 1), the global (co)variance for empty
+    clusters."""
+    bsz, n, d = x.shape
+    k = means.shape[1]
+    xf = x.to(torch.float32)
+    mf = means.to(torch.float32)
+    counts = torch.zeros((bsz, k), dtype=torch.float32)
+    for b in range(bsz):
+        counts[b].index_add_(0, labels[b], torch.ones(n))
+    weights = counts.clamp_min(1.0)
+    weights = weights / weights.sum(dim=-1, keepdim=True)
+    diffs = xf - torch.gather(mf, 1, labels.unsqueeze(-1).expand(-1, -1, d))
+    eye = torch.eye(d, dtype=torch.float32)
+    if covariance_type == "spherical":
+        sq = torch.zeros((bsz, k), dtype=torch.float32)
+        for b in range(bsz):
+            sq[b].index_add_(0, labels[b], diffs[b].square().sum(dim=-1))
+        var = sq / counts.clamp_min(1.0) / float(d)
+        var = torch.where(counts > 0, var, global_spherical_variance(xf, k, reg_covar))
+        return weights, var.clamp_min(reg_covar)
+    if covariance_type == "diag":
+        sq = torch.zeros((bsz, k, d), dtype=torch.float32)
+        for b in range(bsz):
+            sq[b].index_add_(0, labels[b], diffs[b].square())
+        var = sq / counts.clamp_min(1.0).unsqueeze(-1)
+        var = torch.where((counts > 0).unsqueeze(-1), var, global_diag_variance(xf, k, reg_covar))
+        return weights, var.clamp_min(reg_covar)
+    if covariance_type == "tied":
+        cov = torch.bmm(diffs.transpose(1, 2), diffs) / float(n) + reg_covar * eye
+        return weights, symmetrize(cov)
+    cov = torch.zeros((bsz, k, d, d), dtype=torch.float32)
+    for b in range(bsz):
+        cov[b].index_add_(0, labels[b], diffs[b].unsqueeze(-1) * diffs[b].unsqueeze(-2))
+    cov = cov / counts.clamp_min(1.0)[..., None, None] + reg_covar * eye
+    glob = global_tied_covariance(xf, reg_covar).unsqueeze(1).expand(-1, k, -1, -1)
+    cov = torch.where((counts > 0)[..., None, None], cov, glob)
+    return weights, symmetrize(cov)
+
+
+def kmeans_initialize_from(x, covariance_type, centers, *, max_iters=10, tol=1e-4, reg_covar=1e-6):
+    """(means, covariances, weights) of init_params="kmeans" from given seed
+    centres: Lloyd refinement, then the hard-label statistics
+    (torch_fallback.py:1701-1716 and the diag/tied/full counterparts)."""
+    labels, means, _ = lloyd(x, centers, max_iters, tol)
+    weights, covs = hard_label_init_stats(x, covariance_type, means, labels, reg_covar)
+    return means, covs, weights

@@ -1,0 +1,113 @@
+"""k-means initialisation on the GPU against the CPU oracle.
+
+* ``gmmxx_hip_kmeans_pp`` vs oracle ``kmeans_pp`` with the same sample and
+  random numbers: the centres are copies of sample rows, so they must be the
+  same rows (equal bits).  A draw that lands within rounding of a cumulative-sum
+  boundary could pick a neighbouring row; the seeded cases have none.
+* Lloyd + hard-label statistics (``kmeans.lloyd`` / ``hard_label_init_stats``
+  on the top-1 E-step) vs the oracle from the same seed centres: parameters
+  rtol 1e-4 against each tensor's scale.
+* The estimator's default ``init_params="kmeans"`` path end to end.
+"""
+
+import math
+
+import pytest
+import torch
+
+from gmmxx_amd import GMMXX, em, kmeans
+from oracle import torch_ref
+from tests.test_hip_parity import make_problem, to_dev
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _close(got, exp, tol):
+    torch.testing.assert_close(got.cpu(), exp, rtol=tol, atol=tol * float(exp.abs().max()))
+
+
+KPP_CASES = [
+    # B, S, D, K
+    (2, 5000, 32, 64),
+    (1, 777, 5, 40),        # D not a multiple of 4: scalar row loads
+    (1, 16384, 128, 256),   # the reference's largest sample and K
+    (3, 100, 3, 100),       # K = S: every row once
+    (2, 50, 8, 1),          # one centre: the first row only
+]
+
+
+@pytest.mark.parametrize("case", KPP_CASES, ids=lambda c: "B{}-S{}-D{}-K{}".format(*c))
+def test_kmeans_pp_matches_oracle(hip, case):
+    b, s, d, k = case
+    print(f"[kmeans++] B={b} S={s} D={d} K={k}", flush=True)
+    g = torch.Generator().manual_seed(s + k)
+    sample = torch.randn((b, s, d), generator=g) * 3
+    first = torch.randint(0, s, (b,), generator=g)
+    draws = torch.rand((b, k - 1, kmeans.kmeans_pp_trials(k)), generator=g)
+    got = hip.kmeans_pp(sample.to(DEV), k, first.to(DEV), draws.to(DEV))
+    torch.cuda.synchronize()
+    exp = torch_ref.kmeans_pp(sample, k, first, draws)
+    assert torch.equal(got.cpu(), exp)
+
+
+@pytest.mark.parametrize("cov,b,n,d,k", [("spherical", 2, 6000, 16, 12), ("spherical", 1, 8000, 128, 64),
+                                         ("diag", 1, 5000, 24, 10), ("tied", 2, 3000, 8, 6),
+                                         ("full", 1, 4000, 6, 5)])
+def test_lloyd_and_hard_label_stats_match_oracle(hip, cov, b, n, d, k):
+    print(f"[lloyd] {cov} B={b} N={n} D={d} K={k}", flush=True)
+    x, _, _, _ = make_problem(cov, b, n, d, k, seed=51)
+    g = torch.Generator().manual_seed(52)
+    seeds = torch.gather(x, 1, torch.randint(0, n, (b, k, 1), generator=g).expand(-1, -1, d))
+    xd = to_dev(x)
+    stats = kmeans._HardStats(xd, cov, k)
+    means, nk, sx, sq, it = kmeans.lloyd(xd, cov, seeds.to(DEV), 10, 1e-4, stats)
+    gram = stats.gram() if cov == "tied" else None
+    w, c = kmeans.hard_label_init_stats(xd, cov, means, nk, sx, sq, 1e-6, gram)
+    torch.cuda.synchronize()
+    e_lab, e_means, e_it = torch_ref.lloyd(x, seeds, 10, 1e-4)
+    e_w, e_c = torch_ref.hard_label_init_stats(x, cov, e_means, e_lab, 1e-6)
+    assert it == e_it
+    counts = torch.stack([torch.bincount(e_lab[i], minlength=k) for i in range(b)]).float()
+    torch.testing.assert_close(nk.cpu(), counts, rtol=0, atol=0)
+    _close(means, e_means, 1e-4)
+    _close(w, e_w, 1e-5)
+    _close(c, e_c, 1e-4)
+
+
+@pytest.mark.parametrize("cov", ["spherical", "diag", "tied", "full"])
+def test_estimator_kmeans_init_finds_the_blobs(hip, cov):
+    """Well-separated blobs: the k-means initialisation lands on the blob means,
+    so the fitted means match them (sorted) and init_source says kmeans."""
+    d, k = (8, 6) if cov == "full" else (16, 10)
+    g = torch.Generator().manual_seed(53)
+    centers = torch.randn((k, d), generator=g) * 30
+    lab = torch.randint(0, k, (20000,), generator=g)
+    x = centers[lab] + torch.randn((20000, d), generator=g)
+    gm = GMMXX(n_components=k, covariance_type=cov, backend="hip", device=DEV, max_iter=5, tol=0.0, seed=4)
+    gm.fit(x.to(DEV))
+    assert gm.init_source_ == "kmeans"
+    got = gm.means_.cpu()
+    exp = torch.stack([x[lab == j].mean(0) for j in range(k)])
+    order = lambda m: m[torch.argsort(m[:, 0])]
+    torch.testing.assert_close(order(got), order(exp), rtol=1e-3, atol=1e-2)
+
+
+def test_kmeans_initialize_many_components_uses_random_seeds(hip):
+    """K > 256: no k-means++ (as the reference), Lloyd from random rows."""
+    x, _, _, _ = make_problem("spherical", 1, 30000, 8, 300, seed=54)
+    means, covs, weights = kmeans.kmeans_initialize(to_dev(x), "spherical", 300, max_iters=3,
+                                                    generator=torch.Generator(device=DEV).manual_seed(1))
+    assert means.shape == (1, 300, 8) and covs.shape == (1, 300) and bool(torch.isfinite(means).all())
+    torch.testing.assert_close(weights.sum(-1).cpu(), torch.ones(1))
+    assert kmeans.kmeans_plus_plus(to_dev(x), 300) is None
+
+
+def test_em_fit_default_init_is_kmeans(hip):
+    x, _, _, _ = make_problem("diag", 2, 5000, 12, 7, seed=55)
+    _, m, c, w, info = em.fit(to_dev(x), 7, "diag", max_iters=3, tol=0.0,
+                              generator=torch.Generator(device=DEV).manual_seed(2))
+    assert info["init_source"] == "kmeans"
+    _, m2, _, _, info2 = em.fit(to_dev(x), 7, "diag", max_iters=3, tol=0.0, init_params="random")
+    assert info2["init_source"] == "random"
+    assert math.isfinite(info["lower_bound"]) and info["lower_bound"] >= info2["lower_bound"] - 1.0

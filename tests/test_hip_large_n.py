@@ -119,7 +119,7 @@ def test_estimator_streams_long_host_input(hip):
                max_iter=8, tol=0.0, seed=3)
     gm.fit(x[0])
     assert gm.large_n_streaming_enabled_ is True and gm.copy_stream_prefetch_enabled_ is True
-    assert gm.fit_info_["init_source"] == "random_sampled"
+    assert gm.fit_info_["init_source"] == "kmeans_sampled"
     labels = gm.predict(x[0])
     scores = gm.score_samples(x[0])
     proba = gm.predict_proba(x[0])
