@@ -39,8 +39,22 @@ struct Dims {
   static constexpr int NK_COL = (COV == SPH) ? DP : (COV == DIAG ? 2 * DP : (COV == TIED ? DP : DP + S));
 };
 
-// Index of (d, e), d <= e, in the packed upper triangle of a DP x DP matrix.
-__host__ __device__ constexpr int sym_index(int d, int e, int dp) { return d * dp - d * (d - 1) / 2 + (e - d); }
+// Position of the product x_d·x_e (d <= e < 16) among the 136 second-order
+// features of the full covariance (DP = 16), in the order the tile kernel's
+// loader writes them: x is read as four 4-column chunks, one per lane of a row
+// quad, and lane c owns (a) the products inside its chunk (10 per chunk, upper
+// triangle row by row), (b) its chunk times chunk c+1 mod 4 (16 each, own
+// column major: 4·(own) + partner), (c) for c < 2, its chunk times chunk c+2.
+//   [0, 40)    diagonal chunk blocks, chunk c at 10c
+//   [40, 104)  pairs {c, c+1 mod 4}, owner c at 40 + 16c ({0, 3} is owned by 3)
+//   [104, 136) pairs {0, 2} and {1, 3}, owner c at 104 + 16c
+__host__ __device__ constexpr int full_feature(int d, int e) {
+  const int cd = d / 4, ce = e / 4, i = d % 4, j = e % 4;
+  if (cd == ce) return 10 * cd + i * 4 - i * (i - 1) / 2 + (j - i);
+  if (ce == cd + 1) return 40 + 16 * cd + 4 * i + j;
+  if (cd == 0 && ce == 3) return 40 + 48 + 4 * j + i;
+  return 104 + 16 * cd + 4 * i + j;   // ce == cd + 2
+}
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

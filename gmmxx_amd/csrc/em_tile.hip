@@ -137,14 +137,6 @@ __device__ __forceinline__ int lanes_min_i(int v) {
 }
 
 // Packed upper-triangle index -> (d, e) for the full covariance (DP = 16).
-struct SymTable {
-  unsigned char d[136], e[136];
-  constexpr SymTable() : d(), e() {
-    int s = 0;
-    for (int i = 0; i < 16; ++i)
-      for (int j = i; j < 16; ++j) { d[s] = (unsigned char)i; e[s] = (unsigned char)j; ++s; }
-  }
-};
 
 template <int COV, typename XT, int DP, int CW, int MODE>
 __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
@@ -169,9 +161,12 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   // this machine, and the second accumulator set only costs registers.
   constexpr bool PIPE = BF && COV != FULL;
   constexpr int PD = PIPE ? 2 : 1;                       // loader runs PD blocks ahead
-  constexpr int NB = PD + 1;                             // staged-row buffers
+  // Staged-row buffers: the loader fills one while the waves read the other, one
+  // barrier per block.  Full covariance stages three 176-column parts per row and
+  // keeps a single buffer (a second barrier per block) so that two workgroups of
+  // two waves fit a CU's LDS twice over.
+  constexpr int NB = (COV == FULL) ? 1 : PD + 1;
   constexpr int XS = DP + (BF ? 8 : 4);                  // staged-row stride, elements
-  constexpr int PS = EP + 4;                             // φ row stride (full)
   constexpr int QS = kBN + 8;                            // ψᵀ row stride, bf16 elements
   using FT = typename std::conditional<BF, __bf16, float>::type;
   using WF = typename std::conditional<BF, bf16x8, f32x4>::type;
@@ -183,18 +178,17 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   // the fp32 MFMA.  φ parts are staged once per block for all waves.
   // Every pass of a shape uses the same E-GEMM, so all of them see identical logits
   // (off for diag at D = 128: its three staged φ parts would not fit the LDS).
-  constexpr bool X3 = !BF && COV != FULL && !(COV == DIAG && DP >= 128);
+  constexpr bool X3 = !BF && !(COV == DIAG && DP >= 128);
   constexpr int X3K = EP / 32;                           // k-steps of the split E-GEMM
   constexpr int EPS = EP + 16;                           // split-φ row stride (s ≡ 8 or 24 mod 32 dwords)
   constexpr int X3P = NB * kBN * EPS;                    // one part, all buffers
   // Wide statistics passes keep W's third part in LDS (per wave, in the exact
   // per-lane fragment order) to stay within the register file.
-  constexpr bool W3L = X3 && STATS && EP >= 128;
+  constexpr bool W3L = X3 && STATS && EP >= 128 && COV != FULL;
 
   __shared__ __align__(16) XT xs[(COV == FULL || X3) ? 8 : NB * kBN * XS];
   __shared__ __align__(16) __bf16 phx[X3 ? 3 * X3P : 8];
   __shared__ __align__(16) bf16x8 w3s[W3L ? 8 * (CW / 16) * X3K * 64 : 1];   // [wave][ct][ec][lane]
-  __shared__ __align__(16) float phi[COV == FULL ? NB * kBN * PS : 4];
   __shared__ __align__(16) FT psiT[PSI_LDS ? 2 * JP * QS : 8];
   __shared__ float rowq_s[NB * kBN];
   __shared__ float lse_s[NB * kBN];
@@ -328,12 +322,6 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       phx[row * EPS + EP + c] = (__bf16)((c == 0 && row < NB * kBN) ? 1.f : 0.f);
     }
   }
-  if constexpr (COV == FULL) {
-    for (int i = tid; i < NB * kBN * (EP - S - DP); i += nthr) {
-      const int row = i / (EP - S - DP), c = i % (EP - S - DP);
-      phi[row * PS + S + DP + c] = 0.f;
-    }
-  }
 
   const XT* xb = reinterpret_cast<const XT*>(a.x) + (size_t)b * N * D;
 
@@ -379,12 +367,65 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
           *reinterpret_cast<uint2*>(base + X3P) = make_uint2(q2[0], q2[1]);
           *reinterpret_cast<uint2*>(base + 2 * X3P) = make_uint2(q3[0], q3[1]);
         };
+        // NN (even) consecutive features from column col: 16-byte stores when the
+        // run is a multiple of 8 (col is then a multiple of 8), else 4-byte stores.
+        auto put3n = [&](int col, const auto& f) {
+          constexpr int NN = sizeof(f) / sizeof(float);
+          uint32_t q[3][NN / 2];
+#pragma unroll
+          for (int j = 0; j < NN; j += 2) split3x2(f[j], f[j + 1], q[0][j / 2], q[1][j / 2], q[2][j / 2]);
+          __bf16* base = phx + (buf * kBN + r) * EPS + col;
+#pragma unroll
+          for (int p = 0; p < 3; ++p) {
+            if constexpr (NN % 8 == 0) {
+#pragma unroll
+              for (int u = 0; u < NN / 8; ++u)
+                *reinterpret_cast<uint4*>(base + p * X3P + 8 * u) =
+                    make_uint4(q[p][4 * u], q[p][4 * u + 1], q[p][4 * u + 2], q[p][4 * u + 3]);
+            } else {
+#pragma unroll
+              for (int u = 0; u < NN / 2; ++u) *reinterpret_cast<uint32_t*>(base + p * X3P + 2 * u) = q[p][u];
+            }
+          }
+        };
         if constexpr (COV == DIAG) {
           float sq[VEC];
 #pragma unroll
           for (int j = 0; j < VEC; ++j) sq[j] = v[j] * v[j];
           put3(cc, sq);
           put3(DP + cc, v);
+        } else if constexpr (COV == FULL) {
+          // φ = [xxᵀ products in full_feature order | x]: the row's four chunks sit
+          // in a quad of lanes; this lane (chunk c = cc / 4) writes its diagonal
+          // block, its chunk times chunks c+1 and (c < 2) c+2, and its x values.
+          static_assert(DP == 16 && VEC == 4 && CPR == 4, "full covariance runs at DP = 16");
+          const int c = cc / VEC, q0 = lane & ~3;
+          float w1[VEC], w2[VEC];
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            w1[j] = __shfl(v[j], q0 + ((c + 1) & 3));
+            w2[j] = __shfl(v[j], q0 + ((c + 2) & 3));
+          }
+          float dg[10];
+#pragma unroll
+          for (int i = 0, t = 0; i < VEC; ++i)
+#pragma unroll
+            for (int j = i; j < VEC; ++j, ++t) dg[t] = v[i] * v[j];
+          put3n(10 * c, dg);
+          float o[16];
+#pragma unroll
+          for (int i = 0; i < VEC; ++i)
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) o[4 * i + j] = v[i] * w1[j];
+          put3n(40 + 16 * c, o);
+          if (c < 2) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i)
+#pragma unroll
+              for (int j = 0; j < VEC; ++j) o[4 * i + j] = v[i] * w2[j];
+            put3n(104 + 16 * c, o);
+          }
+          put3(S + cc, v);
         } else {
           put3(cc, v);
         }
@@ -413,24 +454,6 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         if (cc == 0) rowq_s[buf * kBN + r] = (n < rend && a.rowq) ? a.rowq[(size_t)b * N + n] : 0.f;
       } else {
         if (cc == 0) rowq_s[buf * kBN + r] = 0.f;
-      }
-      if constexpr (COV == FULL) {
-        // Gather the row (CPR = 4 consecutive lanes) and write this lane's share of
-        // the packed xxᵀ products plus its own x values into φ.
-        float* pr = phi + (buf * kBN + r) * PS;
-        const int q0 = lane & ~(CPR - 1), mine = lane - q0;
-        float xr[DP];
-#pragma unroll
-        for (int qq = 0; qq < CPR; ++qq)
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) xr[qq * VEC + j] = __shfl(v[j], q0 + qq);
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) pr[S + cc + j] = v[j];
-        // Lane `mine` of the row's 4 lanes writes the products s with s % 4 == mine.
-        constexpr SymTable tab{};
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-          if ((s & (CPR - 1)) == mine) pr[s] = xr[tab.d[s]] * xr[tab.e[s]];
       }
       if constexpr (!LSE) {
         if (cc == 0) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
@@ -469,9 +492,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
 
   // φ fragment (4 consecutive E-step features of staged row r), fp32 path.
   auto phi4 = [&](int buf, int r, int e0) -> f32x4 {
-    if constexpr (COV == FULL) {
-      return ld16<f32x4>(&phi[(buf * kBN + r) * PS + e0]);
-    } else if constexpr (COV == DIAG) {
+    if constexpr (COV == DIAG) {
       const int c = e0 < DP ? e0 : e0 - DP;
       f32x4 v = ld16<f32x4>(&xs[buf * kBN * XS + r * XS + c]);
       if (e0 < DP) v = v * v;
@@ -482,21 +503,14 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   };
   // ψ element (M-step feature j of staged row r), fp32 path.
   auto psi1 = [&](int buf, int r, int j) -> float {
-    if constexpr (COV == FULL) {
-      const float* pr = phi + (buf * kBN + r) * PS;
-      if (j < DP) return pr[S + j];
-      if (j < DP + S) return pr[j - DP];
-      return j == DP + S ? 1.f : 0.f;
-    } else {
-      const float* xr = reinterpret_cast<const float*>(xs) + buf * kBN * XS + r * XS;
-      if (j < DP) return xr[j];
-      if constexpr (COV == SPH) return j == DP ? 1.f : (j == DP + 1 ? rowq_s[buf * kBN + r] : 0.f);
-      if constexpr (COV == DIAG) {
-        if (j < 2 * DP) { const float t = xr[j - DP]; return t * t; }
-        return j == 2 * DP ? 1.f : 0.f;
-      }
-      return j == DP ? 1.f : 0.f;  // tied
+    const float* xr = reinterpret_cast<const float*>(xs) + buf * kBN * XS + r * XS;
+    if (j < DP) return xr[j];
+    if constexpr (COV == SPH) return j == DP ? 1.f : (j == DP + 1 ? rowq_s[buf * kBN + r] : 0.f);
+    if constexpr (COV == DIAG) {
+      if (j < 2 * DP) { const float t = xr[j - DP]; return t * t; }
+      return j == 2 * DP ? 1.f : 0.f;
     }
+    return j == DP ? 1.f : 0.f;  // tied
   };
 
   // Cross-wave merge of one block's per-row partials, written to global memory:
@@ -693,9 +707,13 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         }
         // ψ tile jt = 16 consecutive φ columns (diag: x then x², spherical/tied: x) or the
         // augmented columns at EP.
-        auto psi_col = [](int jt) {
+        // Full: ψ = [x | products | 1] from φ = [products | x]; the last tile holds
+        // products 128..135 (column groups 0, 1) and the constant chunk at EP
+        // (groups 2, 3, whose lane offsets are 8 and 12).
+        auto psi_col = [&](int jt) {
           constexpr int XT16 = DP / 16;
           if constexpr (COV == DIAG) return jt < XT16 ? DP + 16 * jt : (jt < 2 * XT16 ? 16 * (jt - XT16) : EP);
+          else if constexpr (COV == FULL) return jt == 0 ? S : (jt < JT - 1 ? 16 * (jt - 1) : ((li & 3) < 2 ? S - 8 : EP - 8));
           else return jt < XT16 ? 16 * jt : EP;
         };
         const __bf16* tb = phx + (bx * kBN + 4 * g + (li >> 2)) * EPS + 4 * (li & 3);
@@ -804,6 +822,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     if constexpr (PSI_LDS) {
       if (ib + 1 < nblk) build_psi((int)((ib + 1) % NB), pb ^ 1);
     }
+    if constexpr (NB == 1) __syncthreads();   // every wave is done with the only buffer
     if (ahead) stash((int)((ib + PD) % NB), n0 + PD * kBN);
     __syncthreads();
   }

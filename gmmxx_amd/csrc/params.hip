@@ -155,7 +155,7 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
       mpm = fmaf(mus[d], pm, mpm);
       put_f32(S + d, -2.f * pm);
       for (int e = d; e < D; ++e)
-        put_f32(sym_index(d, e, DP), d == e ? P[d * D + d] : P[d * D + e] + P[e * D + d]);
+        put_f32(full_feature(d, e), d == e ? P[d * D + d] : P[d * D + e] + P[e * D + d]);
     }
     colq = wave_sum(mpm);
     ca = -0.5f * kLog2e;
@@ -573,7 +573,7 @@ __global__ void finalize_full_kernel(FinalizeArgs a) {
   const bool active = nk > a.min_weight;
   const float nk_safe = fmaxf(nk, a.min_weight);
   const float* mu = a.means + bk * D;
-  const float sxx = sk[DP + sym_index(d < e ? d : e, d < e ? e : d, DP)];
+  const float sxx = sk[DP + full_feature(d < e ? d : e, d < e ? e : d)];
   const float ade = (sxx - nk * (mu[d] * mu[e])) / nk_safe;
   const float aed = (sxx - nk * (mu[e] * mu[d])) / nk_safe;
   float* C = a.covs + bk * D * D;
@@ -601,7 +601,7 @@ __global__ void unpack_stats_kernel(UnpackArgs a) {
   } else if (a.cov == FULL) {
     for (int d = 0; d < D; ++d)
       for (int e = 0; e < D; ++e)
-        a.sum_q[(bk * D + d) * D + e] = sk[DP + sym_index(d < e ? d : e, d < e ? e : d, DP)];
+        a.sum_q[(bk * D + d) * D + e] = sk[DP + full_feature(d < e ? d : e, d < e ? e : d)];
   }
 }
 
@@ -627,7 +627,7 @@ __global__ void pack_stats_kernel(PackArgs a) {
     }
   } else if (a.cov == FULL) {
     for (int d = 0; d < D; ++d)
-      for (int e = d; e < D; ++e) sk[DP + sym_index(d, e, DP)] = a.sum_q[(bk * D + d) * D + e];
+      for (int e = d; e < D; ++e) sk[DP + full_feature(d, e)] = a.sum_q[(bk * D + d) * D + e];
   }
 }
 
