@@ -34,6 +34,7 @@ struct Plan {
   int lnw = 0, lktiles = 0;  // waves / component tiles of the plain log-normaliser pass (MODE_LSE)
   bool fused = false;        // EM iteration as one fused pass (small K; em_fused.hip)
   bool coop = false;         // EM iteration as one cooperative pass (spherical bf16, D = 128; em_coop.hip)
+  bool single = false;       // EM iteration as one tile pass (fp32 x, all K in one workgroup; MODE_STATS_LSE)
   int cG = 0, cNG = 0, cspb = 0;   // coop: workgroups per group, groups, row items per batch
   int64_t crows = 0;         // coop: rows per item
   int fslices = 0;           // fused: one wave per row slice
@@ -45,7 +46,8 @@ struct Plan {
   int chol_m = 0;
   size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
   size_t o_xch = 0, o_flags = 0;
-  size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_prec = 0, o_logdet = 0, o_gram = 0, total = 0;
+  size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_lbuf = 0, o_prec = 0, o_logdet = 0,
+         o_gram = 0, total = 0;
 };
 
 constexpr int kTargetWaves = 4096;      // 16 waves per CU on 256 CUs
@@ -152,6 +154,12 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
     q.crows = ((q.N + spb - 1) / spb + kBN - 1) / kBN * kBN;
     q.cspb = (int)((q.N + q.crows - 1) / q.crows);
   }
+  // One-tile single pass: the workgroup holds every component, so the tile kernel
+  // forms the row log-normalisers itself (diag at D = 128 keeps two passes: its
+  // statistics kernel is at the register limit).  GMMXX_HIP_NO_SINGLE=1 selects
+  // the two passes.
+  const char* no_single = getenv("GMMXX_HIP_NO_SINGLE");
+  q.single = !sph_bf && q.ktiles == 1 && !(q.cov == DIAG && q.DP >= 128) && !(no_single && no_single[0] == '1');
   int64_t gs = std::min<int64_t>(64, row_blocks);
   q.gram_rows = ((q.N + gs - 1) / gs + kBN - 1) / kBN * kBN;
   q.gram_slices = (int)((q.N + q.gram_rows - 1) / q.gram_rows);
@@ -177,10 +185,11 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_pstats = take((size_t)std::max({q.slices, q.fslices, q.cspb}) * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
   // (+B: the tied EM iteration's per-batch log-likelihood shift, after the row partials)
-  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb}) + 1) * 8);
+  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices}) + 1) * 8);
   q.o_xch = take(q.coop ? (size_t)q.cNG * kRing * q.cG * kBN * 8 : 0);
   q.o_flags = take(q.coop ? 4 : 0);   // status word of the cooperative pass
-  q.o_first = take((size_t)q.chol_m * 4);
+  q.o_first = take((size_t)q.chol_m * 4 + 4);   // per-matrix first levels, then the global level
+  q.o_lbuf = take(q.chol_m ? (size_t)q.chol_m * chol_dp(q.D) * chol_dp(q.D) * 4 : 0);
   q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
   q.o_logdet = take((size_t)q.chol_m * 4);
   q.o_gram = take(q.cov == TIED ? (size_t)q.gram_slices * q.B * q.D * q.D * 4 : 0);
@@ -285,7 +294,9 @@ int stat_slices(const Plan& pl) { return pl.fused ? pl.fparts : (pl.coop ? pl.cs
 // the scratch of the grouped slice reduction.
 float* red_tmp(const Plan& pl, void* ws) { return at<float>(ws, pl.o_pms); }
 int64_t red_tmp_floats(const Plan& pl) { return (int64_t)std::max(pl.ktiles, pl.lktiles) * pl.B * pl.N * 2; }
-int ll_parts(const Plan& pl) { return pl.B * (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : pl.cblocks)); }
+int ll_parts(const Plan& pl) {
+  return pl.B * (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.single ? pl.slices : pl.cblocks)));
+}
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
 int prepare(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights,
@@ -295,7 +306,8 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   if (pl.cov == TIED || pl.cov == FULL) {
     prec = at<float>(ws, pl.o_prec);
     logdet = at<float>(ws, pl.o_logdet);
-    launch_chol(covs, pl.D, pl.chol_m, at<int>(ws, pl.o_first), prec, logdet, s);
+    launch_chol(covs, pl.D, pl.chol_m, at<int>(ws, pl.o_first), at<int>(ws, pl.o_first) + pl.chol_m,
+                at<float>(ws, pl.o_lbuf), prec, logdet, s);
   }
   PrepArgs a{};
   a.cov = pl.cov;
@@ -454,14 +466,22 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     case GMMXX_PHASE_LSE_TILE: {
       if (pl.coop) return run_coop(pl, x, ws, s);
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
+      if (pl.single) {
+        if (run_tile(pl, MODE_STATS_LSE, t, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+        return check_hip("single-pass tile kernel");
+      }
       if ((pl.fused ? run_fused(pl, t, s) : run_tile(pl, MODE_LSE, t, s)) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip(pl.fused ? "fused tile kernel" : "log-normaliser tile kernel");
     }
     case GMMXX_PHASE_COMBINE: {
-      if (pl.fused || pl.coop) {  // the single pass already produced per-slice log-likelihoods
-        launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0 / ((double)pl.B * (double)pl.N),
-                         lower_bound, s);
+      if (pl.fused || pl.coop || pl.single) {  // the single pass already produced per-slice log-likelihoods
+        int parts = ll_parts(pl);
+        if (pl.single && pl.cov == TIED) {   // -½ tr(P XᵀX) per batch after the slice partials
+          launch_tied_ll_shift(at<float>(ws, pl.o_prec), gram, pl.B, pl.D, at<double>(ws, pl.o_ll) + parts, s);
+          parts += pl.B;
+        }
+        launch_ll_reduce(at<double>(ws, pl.o_ll), parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
         if (pl.coop) launch_coop_check(coop_status(pl, ws), lower_bound, s);
         return check_hip("log-likelihood reduction");
       }
@@ -483,7 +503,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip("combine");
     }
     case GMMXX_PHASE_STATS_TILE: {
-      if (pl.fused || pl.coop) return GMMXX_OK;  // statistics came out of the single pass
+      if (pl.fused || pl.coop || pl.single) return GMMXX_OK;  // statistics came out of the single pass
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if (run_tile(pl, MODE_STATS, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
@@ -524,9 +544,12 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
-  if (pl.fused || pl.coop) {
+  if (pl.fused || pl.coop || pl.single) {
     if (pl.coop) {
       if ((rc = run_coop(pl, x, ws, s))) return rc;
+    } else if (pl.single) {
+      if (run_tile(pl, MODE_STATS_LSE, tile_args(pl, x, ws), s) != 0)
+        return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
     } else if (run_fused(pl, tile_args(pl, x, ws), s) != 0) {
       return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
     }

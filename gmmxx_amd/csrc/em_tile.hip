@@ -30,6 +30,13 @@
 //               threshold (value, then lower index), else contributes 0.  The
 //               E-GEMM and logit arithmetic are those of MODE_PROBA, so the
 //               recomputed logits equal the ones the threshold was chosen from.
+//   MODE_STATS_LSE
+//               MODE_STATS when the workgroup holds all K components (one
+//               component tile): each wave reduces its rows' (max, sum) over
+//               its components with DPP, the waves' partials meet in LDS after
+//               one barrier, and every wave merges them for its own use, so the
+//               EM iteration needs no separate log-normaliser pass.  The
+//               workgroup also writes its rows' log-likelihood sum.
 //
 // Logits are kept in log2 units (l2 = l·log2 e) so exp2 maps to v_exp_f32:
 //   l2 = A_k·S + (a_k·rowq_n + C_k)
@@ -110,6 +117,7 @@ __device__ __forceinline__ float group_max(float v) {
   if constexpr (G >= 2) v = fmaxf(v, dpp<0xB1>(v));
   if constexpr (G >= 4) v = fmaxf(v, dpp<0x4E>(v));
   if constexpr (G >= 8) v = fmaxf(v, dpp<0x141>(v));
+  if constexpr (G >= 16) v = fmaxf(v, dpp<0x140>(v));
   return v;
 }
 template <int G>
@@ -143,7 +151,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr bool BF = sizeof(XT) == 2;
   constexpr bool LSE = (MODE == MODE_LSE || MODE == MODE_LSE_IDX);
   constexpr bool WANT_IDX = MODE == MODE_LSE_IDX;
-  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK;
+  constexpr bool SLSE = MODE == MODE_STATS_LSE;
+  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK || SLSE;
   constexpr bool TOPK = MODE == MODE_STATS_TOPK;
   using Dm = Dims<COV, DP, BF>;
   constexpr int EP = Dm::EP, JP = Dm::JP, J = Dm::J, S = Dm::S;
@@ -194,8 +203,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   __shared__ float lse_s[NB * kBN];
   __shared__ float thr_s[TOPK ? NB * kBN : 1];     // top-k threshold logit and index per row
   __shared__ int thri_s[TOPK ? NB * kBN : 1];
-  __shared__ float red_m[LSE ? 2 * kBN * 8 : 1];   // [parity][row][wave]
-  __shared__ float red_s[LSE ? 2 * kBN * 8 : 1];
+  __shared__ float red_m[(LSE || SLSE) ? 2 * kBN * 8 : 1];   // [parity][row][wave]
+  __shared__ float red_s[(LSE || SLSE) ? 2 * kBN * 8 : 1];
+  __shared__ __align__(16) float lsw[SLSE ? 8 * kBN : 4];     // [wave][row] merged log-normalisers
   __shared__ int red_i[WANT_IDX ? 2 * kBN * 8 : 1];
 
   const int tid = threadIdx.x;
@@ -295,6 +305,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   };
 
   f32x4 acc[STATS ? CT : 1][STATS ? JT : 1];
+  double ll_acc = 0.0;     // MODE_STATS_LSE, wave 0: Σ log2-normalisers of this workgroup's rows
   if constexpr (STATS) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
@@ -456,7 +467,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         if (cc == 0) rowq_s[buf * kBN + r] = 0.f;
       }
       if constexpr (!LSE) {
-        if (cc == 0) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
+        if (cc == 0 && !SLSE) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
       }
       if constexpr (TOPK) {
         if (cc == 0) {
@@ -669,6 +680,57 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     } else {
       // Responsibilities for every component tile of this wave.
       float rr[CT][2][4];
+      if constexpr (SLSE) {
+        // Row r = 16rt + 4g + v: this wave's (max, Σ 2^(l2 - max)) over its
+        // components (16 lanes x CT tiles), then the merge over the waves.
+        float l2v[CT][2][4];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              l2v[ct][rt][v] = logit(cS[ct], A.t[ct][rt][v], rowq_s[bx * kBN + 16 * rt + 4 * g + v]);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float m = kLogFloor;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) m = fmaxf(m, l2v[ct][rt][v]);
+            m = group_max<16>(m);
+            float sm = 0.f;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) sm += fast_exp2(l2v[ct][rt][v] - m);
+            sm = group_sum<16>(sm);
+            if (li == 0) {
+              red_m[(16 * rt + 4 * g + v) * 8 + wave] = m;
+              red_s[(16 * rt + 4 * g + v) * 8 + wave] = sm;
+            }
+          }
+        __syncthreads();
+        if (lane < kBN) {
+          float M = kLogFloor;
+          for (int w = 0; w < nw; ++w) M = fmaxf(M, red_m[lane * 8 + w]);
+          float S = 0.f;
+          for (int w = 0; w < nw; ++w) S += red_s[lane * 8 + w] * fast_exp2(red_m[lane * 8 + w] - M);
+          const bool valid = n0 + lane < rend;
+          const float l = M + __log2f(S);
+          lsw[wave * kBN + lane] = valid ? l : INFINITY;
+          if (wave == 0 && valid) ll_acc += (double)l;
+        }
+        // The wave's own LDS writes above are read back by its other lanes below.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const f32x4 lv = ld16<f32x4>(&lsw[wave * kBN + 16 * rt + 4 * g]);
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) rr[ct][rt][v] = fast_exp2(l2v[ct][rt][v] - lv[v]);
+        }
+      } else {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
@@ -688,6 +750,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               rr[ct][rt][v] = fast_exp2(l2 - lse_s[bx * kBN + r]);
             }
           }
+      }
       if constexpr (STATS && X3) {
         // M-GEMM on split bf16 operands: r in three parts (A element j = 4rt + v is
         // data row 16rt + 4g + v), ψ tiles read from the staged split φ rows with the
@@ -843,6 +906,15 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         }
       }
   }
+  if constexpr (SLSE) {
+    // This workgroup's rows: Σ lse (natural log), one partial per (batch, slice).
+    if (wave == 0) {
+      double t = ll_acc;
+#pragma unroll
+      for (int off = 32; off >= 1; off /= 2) t += __shfl_xor(t, off);
+      if (lane == 0) a.ll_part[(size_t)b * (gridDim.x / a.ktiles) + slice] = t * (double)kLn2;
+    }
+  }
 }
 
 template <int COV, typename XT, int DP>
@@ -855,6 +927,7 @@ static int launch_tile_t(int mode, const TileArgs& a, dim3 grid, int nw, hipStre
     case MODE_STATS: em_tile_kernel<COV, XT, DP, CW, MODE_STATS><<<grid, block, 0, s>>>(a); break;
     case MODE_PROBA: em_tile_kernel<COV, XT, DP, CW, MODE_PROBA><<<grid, block, 0, s>>>(a); break;
     case MODE_STATS_TOPK: em_tile_kernel<COV, XT, DP, CW, MODE_STATS_TOPK><<<grid, block, 0, s>>>(a); break;
+    case MODE_STATS_LSE: em_tile_kernel<COV, XT, DP, CW, MODE_STATS_LSE><<<grid, block, 0, s>>>(a); break;
     default: return -1;
   }
   return 0;

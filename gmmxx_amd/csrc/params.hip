@@ -170,17 +170,20 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
 // Batched Cholesky, precision and log-determinant (torch_fallback.py:316-334)
 //
 // chol_try:    per matrix, the first jitter level that factorises
-//              (level 0 = no jitter, level i = 1e-6 * 10^(i-1), i = 1..6; 7 = none)
-// chol_finish: the batch-global level is the largest first level (all
-//              matrices factorise there); refactorise at it and form
-//              P = L^-T L^-1 and log det = 2 Σ log L_jj.
-// One workgroup of 256 threads per matrix (D <= 64): the factorisation and the
-// triangular inverse run four threads per row / column (quad reductions), the
-// staging of C and the product P = XᵀX use every thread.
+//              (level 0 = no jitter, level i = 1e-6 * 10^(i-1), i = 1..6; 7 = none),
+//              and that factor
+// chol_level:  the batch-global level: the largest first level (every matrix
+//              factorises there)
+// chol_finish: the factor at the global level (the stored one when it is the
+//              matrix's own first level, else refactorised), X = L^-1,
+//              P = XᵀX = L^-T L^-1 and log det = 2 Σ log L_jj.
+// One wave per matrix, lane i = row i, the matrix padded to DP x DP with the
+// identity and held in a per-wave LDS tile: the dependency chains of the
+// factorisation and the inverse run within the wave (its LDS writes are read
+// back after a wavefront-scope fence), with no workgroup barrier.
 // ---------------------------------------------------------------------------
 
 constexpr int kMaxCholD = 64;
-constexpr int kCS = kMaxCholD + 1;
 
 // The ladder is built in double and cast once, like the reference's Python float.
 __device__ float jitter_of(int level) {
@@ -189,123 +192,147 @@ __device__ float jitter_of(int level) {
   return (float)j;
 }
 
-// Dot product of length n of two LDS vectors with strides sa / sb, four
-// independent partial sums (the loads of consecutive terms overlap).
-__device__ __forceinline__ float lds_dot(const float* a, int sa, const float* b, int sb, int n) {
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Row stride of the per-wave LDS tiles: 16-byte aligned rows, and lanes i and
+// i + 1 four banks apart, so per-lane 16-byte row reads are conflict-free.
+template <int DP>
+constexpr int chol_rs() { return DP + 4; }
+
+// Lane i writes row i of sym(C) + jitter·I (identity outside D x D) to A.
+template <int DP>
+__device__ __forceinline__ void chol_load(const float* C, int D, float jitter, float* A) {
+  const int i = threadIdx.x & 63;
+  if (i >= DP) return;
+  for (int c = 0; c < DP; ++c) {
+    float v = (i == c) ? 1.f : 0.f;
+    if (i < D && c < D) v = (i == c) ? C[i * D + i] + jitter : 0.5f * (C[i * D + c] + C[c * D + i]);
+    A[i * chol_rs<DP>() + c] = v;
+  }
+}
+
+// Σ_{c<n} a[c]·b[c] over LDS rows (16-byte aligned), four partial sums.
+__device__ __forceinline__ float lds_dot4(const float* a, const float* b, int n) {
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   int c = 0;
   for (; c + 4 <= n; c += 4) {
-    s0 = fmaf(a[c * sa], b[c * sb], s0);
-    s1 = fmaf(a[(c + 1) * sa], b[(c + 1) * sb], s1);
-    s2 = fmaf(a[(c + 2) * sa], b[(c + 2) * sb], s2);
-    s3 = fmaf(a[(c + 3) * sa], b[(c + 3) * sb], s3);
+    const f32x4 u = *reinterpret_cast<const f32x4*>(a + c), v = *reinterpret_cast<const f32x4*>(b + c);
+    acc[0] = fmaf(u[0], v[0], acc[0]);
+    acc[1] = fmaf(u[1], v[1], acc[1]);
+    acc[2] = fmaf(u[2], v[2], acc[2]);
+    acc[3] = fmaf(u[3], v[3], acc[3]);
   }
-  for (; c < n; ++c) s0 = fmaf(a[c * sa], b[c * sb], s0);
-  return (s0 + s1) + (s2 + s3);
+  for (; c < n; ++c) acc[0] = fmaf(a[c], b[c], acc[0]);
+  return (acc[0] + acc[1]) + (acc[2] + acc[3]);
 }
 
-// Sum over the 4 lanes of a quad (lanes 4i .. 4i+3), result in every lane.
-__device__ __forceinline__ float quad_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // lane ^ 1
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // lane ^ 2
-  return v;
-}
-
-// Factorises sym(C) + jitter·I into Ls (lower triangle), left-looking: column j
-// is L_ij = (A_ij - Σ_{c<j} L_ic L_jc) / L_jj.  Four threads per row i (t = 4i + p)
-// each take the terms c ≡ p (mod 4) and a quad reduction joins them; tmp (LDS,
-// D floats) carries the column's numerators.  Returns success.  C is staged with
-// coalesced loads by the whole block; the lower triangle is then symmetrised in
-// place (it reads only the untouched upper triangle).
-__device__ bool chol_factor(const float* C, int D, float jitter, float* Ls, float* tmp) {
-  const int t = threadIdx.x, i = t >> 2, p = t & 3;
-  for (int o = t; o < D * D; o += blockDim.x) Ls[(o / D) * kCS + o % D] = C[o];
-  __syncthreads();
-  for (int o = t; o < D * D; o += blockDim.x) {
-    const int r = o / D, c = o % D;
-    if (c < r) Ls[r * kCS + c] = 0.5f * (Ls[r * kCS + c] + Ls[c * kCS + r]);
-    else if (c == r) Ls[r * kCS + r] += jitter;
-  }
-  __syncthreads();
+// Left-looking factorisation in place in the LDS tile A (lane i owns row i):
+// step j: t_i = A_ij - Σ_{c<j} L_ic L_jc, the pivot t_j comes from lane j,
+// L_jj = sqrt(t_j), L_ij = t_i / L_jj (rows i > j), 0 above the diagonal.
+// Only entries c < j of the rows are read, which step c has written.  (Rows
+// in registers would need 64-wide masked updates at every step: that variant
+// measured 2.3x slower at D = 64.)  Returns success (uniform across the wave).
+template <int DP>
+__device__ bool chol_wave(float* A) {
+  constexpr int RS = chol_rs<DP>();
+  const int i = threadIdx.x & 63;
+  const int ir = (i < DP) ? i : 0;           // lanes past DP shadow row 0 and store nothing
   bool ok = true;
-  const bool row = i < D;
-  for (int j = 0; j < D; ++j) {
-    float part = 0.f;
-    if (row && i >= j)
-      for (int c = p; c < j; c += 4) part = fmaf(Ls[i * kCS + c], Ls[j * kCS + c], part);
-    const float sum = quad_sum(part);
-    if (row && i >= j && p == 0) tmp[i] = Ls[i * kCS + j] - sum;
-    __syncthreads();
-    const float djj = tmp[j];
-    if (!(djj > 0.f)) { ok = false; break; }     // uniform across the block
-    const float ljj = sqrtf(djj);
-    if (row && p == 0) {
-      if (i == j) Ls[j * kCS + j] = ljj;
-      else if (i > j) Ls[i * kCS + j] = tmp[i] / ljj;
-    }
-    __syncthreads();
+  for (int j = 0; j < DP; ++j) {
+    wave_lds_sync();
+    const float t = A[ir * RS + j] - lds_dot4(A + ir * RS, A + j * RS, j);
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), j));
+    ok = ok && (d > 0.f);
+    const float ljj = sqrtf(d);
+    if (i < DP) A[i * RS + j] = (i < j) ? 0.f : ((i == j) ? ljj : t / ljj);
   }
+  wave_lds_sync();
   return ok;
 }
 
-__global__ void chol_try_kernel(const float* cov, int D, int* first_ok) {
-  __shared__ float Ls[kMaxCholD * kCS];
-  __shared__ float tmp[kMaxCholD];
-  const int m = blockIdx.x;
+constexpr int kCholWaves = 4;   // matrices (waves) per workgroup
+
+template <int DP>
+__global__ __launch_bounds__(64 * kCholWaves) void chol_try_kernel(const float* cov, int D, int M, int* first_ok,
+                                                                   float* lbuf) {
+  constexpr int RS = chol_rs<DP>();
+  __shared__ __align__(16) float Lsh[kCholWaves][DP * RS];
+  const int w = threadIdx.x / 64, i = threadIdx.x & 63;
+  const int m = blockIdx.x * kCholWaves + w;
+  if (m >= M) return;   // whole wave
+  float* A = Lsh[w];
   const float* C = cov + (size_t)m * D * D;
   int level = 7;
-  for (int l = 0; l < 7; ++l) {
-    if (chol_factor(C, D, jitter_of(l), Ls, tmp)) { level = l; break; }
+  for (int lv = 0; lv < 7; ++lv) {
+    chol_load<DP>(C, D, jitter_of(lv), A);
+    if (chol_wave<DP>(A)) { level = lv; break; }
   }
-  if (threadIdx.x == 0) first_ok[m] = level;
+  if (i == 0) first_ok[m] = level;
+  if (i < DP) {
+    float* Lg = lbuf + ((size_t)m * DP + i) * DP;
+    for (int c = 0; c < DP; ++c) Lg[c] = A[i * RS + c];
+  }
 }
 
-__global__ void chol_finish_kernel(const float* cov, int D, int M, const int* first_ok,
-                                   float* prec, float* logdet) {
-  __shared__ float Ls[kMaxCholD * kCS];
-  __shared__ float Xs[kMaxCholD * kCS];
-  __shared__ float tmp[kMaxCholD];
-  __shared__ int lvl_s;
-  const int m = blockIdx.x;
-  const int i = threadIdx.x;
-  if (i == 0) {
-    int lv = 0;
-    for (int t = 0; t < M; ++t) lv = first_ok[t] > lv ? first_ok[t] : lv;
-    lvl_s = lv > 6 ? 6 : lv;
-  }
+// Largest first level over the batch (one workgroup).
+__global__ void chol_level_kernel(const int* first_ok, int M, int* level) {
+  __shared__ int red[256];
+  int v = 0;
+  for (int m = threadIdx.x; m < M; m += blockDim.x) v = max(v, first_ok[m]);
+  red[threadIdx.x] = v;
   __syncthreads();
-  chol_factor(cov + (size_t)m * D * D, D, jitter_of(lvl_s), Ls, tmp);
-  // X = L^-1 (lower triangular) by forward substitution, X_ri = -(Σ_{i<=c<r} L_rc X_ci) / L_rr:
-  // column ci = i / 4 by a quad of threads, each taking the terms c ≡ ci + p (mod 4).
-  // The four lanes of a quad run the same trip counts and all store the same X_ri
-  // (one wave: the stores land before the next step's loads).
-  {
-    const int ci = i >> 2, p = i & 3;
-    if (ci < D) {
-      for (int r = p; r < ci; r += 4) Xs[r * kCS + ci] = 0.f;
-      Xs[ci * kCS + ci] = 1.f / Ls[ci * kCS + ci];
-      for (int r = ci + 1; r < D; ++r) {
-        float part = 0.f;
-        for (int c = ci + p; c < r; c += 4) part = fmaf(Ls[r * kCS + c], Xs[c * kCS + ci], part);
-        Xs[r * kCS + ci] = -quad_sum(part) / Ls[r * kCS + r];
-      }
-    }
+  for (int o = blockDim.x / 2; o > 0; o /= 2) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] = max(red[threadIdx.x], red[threadIdx.x + o]);
+    __syncthreads();
   }
-  __syncthreads();
-  // P = Xᵀ X: P_ij = Σ_{r >= max(i,j)} X_ri X_rj, symmetric; every thread of the
-  // block forms entries, consecutive threads consecutive entries of one row.
-  {
-    float* Pm = prec + (size_t)m * D * D;
-    for (int o = i; o < D * D; o += blockDim.x) {
-      const int pi = o % D, pj = o / D;
-      const int r0 = pi > pj ? pi : pj;
-      Pm[pj * D + pi] = lds_dot(Xs + r0 * kCS + pi, kCS, Xs + r0 * kCS + pj, kCS, D - r0);
+  if (threadIdx.x == 0) *level = min(red[0], 6);
+}
+
+template <int DP>
+__global__ __launch_bounds__(64 * kCholWaves) void chol_finish_kernel(const float* cov, int D, int M,
+                                                                      const int* first_ok, const int* level,
+                                                                      const float* lbuf, float* prec, float* logdet) {
+  constexpr int RS = chol_rs<DP>();
+  __shared__ __align__(16) float Lsh[kCholWaves][DP * RS];
+  __shared__ __align__(16) float Xsh[kCholWaves][DP * RS];
+  const int w = threadIdx.x / 64, i = threadIdx.x & 63;
+  const int m = blockIdx.x * kCholWaves + w;
+  if (m >= M) return;   // whole wave
+  float* L = Lsh[w];
+  float* X = Xsh[w];
+  const int lv = *level;
+  if (first_ok[m] == lv) {
+    if (i < DP) {
+      const float* Lg = lbuf + ((size_t)m * DP + i) * DP;
+      for (int c = 0; c < DP; ++c) L[i * RS + c] = Lg[c];
     }
+    wave_lds_sync();
+  } else {
+    chol_load<DP>(cov + (size_t)m * D * D, D, jitter_of(lv), L);
+    chol_wave<DP>(L);
   }
-  if (i == 0) {
-    float s = 0.f;
-    for (int j = 0; j < D; ++j) s += logf(Ls[j * kCS + j]);
-    logdet[m] = 2.f * s;
+  // log det = 2 Σ_{i<D} log L_ii
+  float ld = (i < D) ? logf(L[i * RS + i]) : 0.f;
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) ld += __shfl_xor(ld, off);
+  if (i == 0) logdet[m] = 2.f * ld;
+  // X = L^-1 by columns, lane c owning column c (stored as row c of X):
+  // x_r = -(Σ_{k<r} L_rk x_k) / L_rr for r > c, x_c = 1 / L_cc, 0 above.
+  const int ir = (i < DP) ? i : 0;
+  for (int r = 0; r < DP; ++r) {
+    const float sacc = lds_dot4(L + r * RS, X + ir * RS, r);
+    const float lrr = L[r * RS + r];
+    if (i < DP) X[i * RS + r] = (r < i) ? 0.f : ((r == i) ? 1.f / lrr : -sacc / lrr);
+    wave_lds_sync();
+  }
+  // P_ij = Σ_r X_ri X_rj: lane i forms row i (the same products in the same order
+  // as lane j forms P_ji: P is exactly symmetric).
+  if (i < D) {
+    float* Pm = prec + (size_t)m * D * D + (size_t)i * D;
+    for (int j = 0; j < D; ++j) Pm[j] = lds_dot4(X + i * RS, X + j * RS, DP);
   }
 }
 
@@ -688,9 +715,24 @@ void launch_tied_ll_shift(const float* prec, const float* gram, int B, int D, do
   tied_ll_shift_kernel<<<B, 256, 0, s>>>(prec, gram, D, out);
 }
 
-void launch_chol(const float* cov, int D, int M, int* first_ok, float* prec, float* logdet, hipStream_t s) {
-  chol_try_kernel<<<M, 256, 0, s>>>(cov, D, first_ok);
-  chol_finish_kernel<<<M, 256, 0, s>>>(cov, D, M, first_ok, prec, logdet);
+int chol_dp(int D) { return D <= 16 ? 16 : (D <= 32 ? 32 : 64); }
+
+template <int DP>
+static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
+                           float* logdet, hipStream_t s) {
+  const int blocks = (M + kCholWaves - 1) / kCholWaves;
+  chol_try_kernel<DP><<<blocks, 64 * kCholWaves, 0, s>>>(cov, D, M, first_ok, lbuf);
+  chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
+  chol_finish_kernel<DP><<<blocks, 64 * kCholWaves, 0, s>>>(cov, D, M, first_ok, level, lbuf, prec, logdet);
+}
+
+void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
+                 float* logdet, hipStream_t s) {
+  switch (chol_dp(D)) {
+    case 16: launch_chol_dp<16>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
+    case 32: launch_chol_dp<32>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
+    default: launch_chol_dp<64>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
+  }
 }
 
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s) {

@@ -268,3 +268,37 @@ def test_canary(hip):
     inp = torch.arange(1000, dtype=torch.int32, device=DEV)
     out = hip.canary_add_offset(inp, 7)
     assert torch.equal(out.cpu(), torch.arange(1000, dtype=torch.int32) + 7)
+
+
+@pytest.mark.parametrize("cov,b,n,d,k", [("spherical", 2, 9000, 32, 64), ("diag", 1, 8000, 64, 200),
+                                         ("tied", 1, 8000, 64, 256), ("full", 3, 6000, 16, 32),
+                                         ("full", 1, 5000, 9, 100)])
+def test_one_tile_single_pass_matches_two_pass(hip, monkeypatch, cov, b, n, d, k):
+    """fp32 x with every component in one workgroup: the single tile pass
+    (in-workgroup log-normalisers) and the two passes (GMMXX_HIP_NO_SINGLE=1)
+    compute the same iteration up to the order of the log-normaliser merge."""
+    print(f"[one-tile] {cov} B={b} N={n} D={d} K={k}", flush=True)
+    x, means, covs, w = make_problem(cov, b, n, d, k, seed=22)
+    xd = to_dev(x)
+    out = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("GMMXX_HIP_NO_SINGLE", mode)
+        m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
+        ws = hip.Workspace(hip.problem(cov, torch.float32, b, n, d, k), xd.device)
+        gram = hip.gram(xd, ws) if cov == "tied" else None
+        lbs = []
+        for _ in range(3):
+            lb = torch.zeros(1, device=DEV)
+            hip.em_step(cov, xd, m_d, c_d, w_d, lb, gram_xx=gram, ws=ws)
+            lbs.append(float(lb))
+        stats = hip.estep_stats(cov, xd, m_d, c_d, w_d)
+        torch.cuda.synchronize()
+        out[mode] = (m_d.cpu(), c_d.cpu(), w_d.cpu(), lbs, [t.cpu() if t is not None else None for t in stats])
+    (m1, c1, w1, l1, s1), (m2, c2, w2, l2, s2) = out["0"], out["1"]
+    for a, e in zip(l1, l2):
+        assert a == pytest.approx(e, rel=1e-6)
+    for a, e in ((m1, m2), (c1, c2), (w1, w2)):
+        torch.testing.assert_close(a, e, rtol=1e-5, atol=1e-5 * float(e.abs().max()))
+    for a, e in zip(s1, s2):
+        if e is not None:
+            torch.testing.assert_close(a, e, rtol=1e-5, atol=1e-5 * float(e.abs().max()))
