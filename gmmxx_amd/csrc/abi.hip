@@ -160,8 +160,10 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   // the two passes.
   const char* no_single = getenv("GMMXX_HIP_NO_SINGLE");
   q.single = !sph_bf && q.ktiles == 1 && !(q.cov == DIAG && q.DP >= 128) && !(no_single && no_single[0] == '1');
-  int64_t gs = std::min<int64_t>(64, row_blocks);
-  q.gram_rows = ((q.N + gs - 1) / gs + kBN - 1) / kBN * kBN;
+  // XᵀX: about 512 workgroups in all, slices of whole 16-row groups (the kernel's
+  // four waves take four rows at a time).
+  int64_t gs = std::max<int64_t>(1, std::min<int64_t>((512 + q.B - 1) / q.B, (q.N + 255) / 256));
+  q.gram_rows = ((q.N + gs - 1) / gs + 15) / 16 * 16;
   q.gram_slices = (int)((q.N + q.gram_rows - 1) / q.gram_rows);
   q.chol_m = (q.cov == TIED) ? q.B : (q.cov == FULL ? q.B * q.K : 0);
 

@@ -662,35 +662,59 @@ __global__ void pack_stats_kernel(PackArgs a) {
 // XᵀX per batch (tied, once per fit; torch_fallback.py:2856-2862)
 // ---------------------------------------------------------------------------
 
-__global__ void gram_partial_kernel(const float* x, int64_t N, int D, int64_t rows_per_slice, float* part) {
-  __shared__ float xs[32 * (kMaxCholD + 1)];
+// One workgroup per (row slice, batch), kGramWaves waves over consecutive row
+// quarters of the slice.  Four rows at a time feed T x T fp32 MFMAs
+// (v_mfma_f32_16x16x4f32): lane (i, g) loads x[n + g][16t + i] for each 16-column
+// tile t, which is both the A fragment (Xᵀ) and the B fragment (X) of the tile
+// pairs; the accumulator of tiles (ti, tj) holds G[16ti + 4g + v][16tj + i].
+// The waves' sums meet in LDS and the workgroup writes one partial.
+constexpr int kGramWaves = 4;
+
+template <int T>
+__global__ __launch_bounds__(64 * kGramWaves) void gram_mfma_kernel(const float* x, int64_t N, int D,
+                                                                    int64_t rows_per_slice, float* part) {
+  constexpr int DPG = 16 * T;
+  __shared__ float red[kGramWaves][DPG * DPG];
   const int b = blockIdx.y, slice = blockIdx.x;
+  const int w = threadIdx.x / 64, lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
   const int64_t r0 = (int64_t)slice * rows_per_slice;
   const int64_t r1 = (r0 + rows_per_slice < N) ? r0 + rows_per_slice : N;
+  const int64_t q = rows_per_slice / kGramWaves;             // multiple of 4
+  const int64_t w0 = r0 + w * q;
+  const int64_t w1 = (w0 + q < r1) ? w0 + q : r1;
   const float* xb = x + (size_t)b * N * D;
-  constexpr int kPer = (kMaxCholD * kMaxCholD + 255) / 256;
-  float acc[kPer];
-  for (int i = 0; i < kPer; ++i) acc[i] = 0.f;
-  for (int64_t n0 = r0; n0 < r1; n0 += 32) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < 32 * D; i += blockDim.x) {
-      const int r = i / D, c = i % D;
-      xs[r * (kMaxCholD + 1) + c] = (n0 + r < r1) ? xb[(size_t)(n0 + r) * D + c] : 0.f;
+  f32x4 acc[T][T];
+#pragma unroll
+  for (int ti = 0; ti < T; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < T; ++tj) acc[ti][tj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t n = w0; n < w1; n += 4) {
+    const int64_t row = n + g;
+    float f[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int c = 16 * t + li;
+      f[t] = (row < w1 && c < D) ? xb[(size_t)row * D + c] : 0.f;
     }
-    __syncthreads();
-    for (int i = 0; i < kPer; ++i) {
-      const int t = threadIdx.x + i * blockDim.x;
-      if (t < D * D) {
-        const int d = t / D, e = t % D;
-        float s = acc[i];
-        for (int r = 0; r < 32; ++r) s = fmaf(xs[r * (kMaxCholD + 1) + d], xs[r * (kMaxCholD + 1) + e], s);
-        acc[i] = s;
-      }
-    }
+#pragma unroll
+    for (int ti = 0; ti < T; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < T; ++tj) acc[ti][tj] = mfma_f32(f[ti], f[tj], acc[ti][tj]);
   }
-  for (int i = 0; i < kPer; ++i) {
-    const int t = threadIdx.x + i * blockDim.x;
-    if (t < D * D) part[((size_t)slice * gridDim.y + b) * D * D + t] = acc[i];
+#pragma unroll
+  for (int ti = 0; ti < T; ++ti)
+#pragma unroll
+    for (int tj = 0; tj < T; ++tj)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[w][(16 * ti + 4 * g + v) * DPG + 16 * tj + li] = acc[ti][tj][v];
+  __syncthreads();
+  float* out = part + ((size_t)slice * gridDim.y + b) * D * D;
+  for (int o = threadIdx.x; o < D * D; o += blockDim.x) {
+    const int d = o / D, e = o % D;
+    float sum = 0.f;
+#pragma unroll
+    for (int u = 0; u < kGramWaves; ++u) sum += red[u][d * DPG + e];
+    out[o] = sum;
   }
 }
 
@@ -792,7 +816,10 @@ void launch_pack(const PackArgs& a, int B, hipStream_t s) {
 
 void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
                  hipStream_t s) {
-  gram_partial_kernel<<<dim3(slices, B), 256, 0, s>>>(x, N, D, rows_per_slice, part);
+  const dim3 grid(slices, B), block(64 * kGramWaves);
+  if (D <= 16) gram_mfma_kernel<1><<<grid, block, 0, s>>>(x, N, D, rows_per_slice, part);
+  else if (D <= 32) gram_mfma_kernel<2><<<grid, block, 0, s>>>(x, N, D, rows_per_slice, part);
+  else gram_mfma_kernel<4><<<grid, block, 0, s>>>(x, N, D, rows_per_slice, part);
 }
 
 void launch_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, hipStream_t s) {
