@@ -705,10 +705,10 @@ int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* 
   if (!means || !covs || !weights || !proba) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
-  if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, false, s))) return rc;
+  if (!pl.single && (rc = lse_pass(pl, x, ws, nullptr, nullptr, false, s))) return rc;
   TileArgs t = tile_args(pl, x, ws);
   t.proba = proba;
-  if (run_tile(pl, MODE_PROBA, t, s) != 0)
+  if (run_tile(pl, pl.single ? MODE_PROBA_LSE : MODE_PROBA, t, s) != 0)
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
   return check_hip("predict_proba");
 }

@@ -13,9 +13,12 @@ enum Cov { SPH = 0, DIAG = 1, TIED = 2, FULL = 3 };
 // MODE_STATS_TOPK: the statistics pass of approximate top-k EM -- responsibilities
 // only for each row's top-k components (ranked by logit, then lower index), the
 // rest zero, against the top-k log-normaliser.
-// MODE_STATS_LSE: the statistics pass with the row log-normalisers formed inside
-// the workgroup (every component is in it): one pass per EM iteration.
-enum Mode { MODE_LSE = 0, MODE_STATS = 1, MODE_PROBA = 2, MODE_LSE_IDX = 3, MODE_STATS_TOPK = 4, MODE_STATS_LSE = 5 };
+// MODE_STATS_LSE / MODE_PROBA_LSE: the statistics / responsibility pass with the
+// row log-normalisers formed inside the workgroup (every component is in it).
+enum Mode {
+  MODE_LSE = 0, MODE_STATS = 1, MODE_PROBA = 2, MODE_LSE_IDX = 3, MODE_STATS_TOPK = 4, MODE_STATS_LSE = 5,
+  MODE_PROBA_LSE = 6
+};
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;

@@ -37,6 +37,8 @@
 //               one barrier, and every wave merges them for its own use, so the
 //               EM iteration needs no separate log-normaliser pass.  The
 //               workgroup also writes its rows' log-likelihood sum.
+//   MODE_PROBA_LSE
+//               MODE_PROBA with the same in-workgroup log-normalisers.
 //
 // Logits are kept in log2 units (l2 = l·log2 e) so exp2 maps to v_exp_f32:
 //   l2 = A_k·S + (a_k·rowq_n + C_k)
@@ -151,8 +153,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr bool BF = sizeof(XT) == 2;
   constexpr bool LSE = (MODE == MODE_LSE || MODE == MODE_LSE_IDX);
   constexpr bool WANT_IDX = MODE == MODE_LSE_IDX;
-  constexpr bool SLSE = MODE == MODE_STATS_LSE;
-  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK || SLSE;
+  constexpr bool SLSE = MODE == MODE_STATS_LSE || MODE == MODE_PROBA_LSE;
+  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK || MODE == MODE_STATS_LSE;
   constexpr bool TOPK = MODE == MODE_STATS_TOPK;
   using Dm = Dims<COV, DP, BF>;
   constexpr int EP = Dm::EP, JP = Dm::JP, J = Dm::J, S = Dm::S;
@@ -906,7 +908,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         }
       }
   }
-  if constexpr (SLSE) {
+  if constexpr (MODE == MODE_STATS_LSE) {
     // This workgroup's rows: Σ lse (natural log), one partial per (batch, slice).
     if (wave == 0) {
       double t = ll_acc;
@@ -928,6 +930,7 @@ static int launch_tile_t(int mode, const TileArgs& a, dim3 grid, int nw, hipStre
     case MODE_PROBA: em_tile_kernel<COV, XT, DP, CW, MODE_PROBA><<<grid, block, 0, s>>>(a); break;
     case MODE_STATS_TOPK: em_tile_kernel<COV, XT, DP, CW, MODE_STATS_TOPK><<<grid, block, 0, s>>>(a); break;
     case MODE_STATS_LSE: em_tile_kernel<COV, XT, DP, CW, MODE_STATS_LSE><<<grid, block, 0, s>>>(a); break;
+    case MODE_PROBA_LSE: em_tile_kernel<COV, XT, DP, CW, MODE_PROBA_LSE><<<grid, block, 0, s>>>(a); break;
     default: return -1;
   }
   return 0;
