@@ -9,7 +9,7 @@
 // E-GEMM runs once per (row, component) and its exponentials are reused:
 //
 //   block i:    E-GEMM (logits l2, log2 units, as in em_sph_bf16.hip)
-//               m_w = wave row max, e = 2^(l2 - m_w) (kept in LDS), s_w = Σ e
+//               m_w = wave row max, e = 2^(l2 - m_w) (kept in LDS as bf16), s_w = Σ e
 //               workgroup partials (M, S) per row -> published to the group
 //   block i-2:  lse2 = merge of the group's partials (same order in every
 //               member, so all members use bit-identical log-normalisers)
@@ -155,9 +155,12 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
   __shared__ float red_s[2 * kNW * RR];
   __shared__ float lse_s[2 * kBN];
   // e = 2^(l2 - m_w) of the two blocks in flight, per wave and block parity, in
-  // the accumulator layout (one 16-byte vector per lane and (ct, row tile)); kept
-  // in LDS, which leaves the registers to the W operands and the statistics.
-  __shared__ f32x4 es[kNW * 2 * kCT * 2 * 64];
+  // the accumulator layout (four bf16 per lane and (ct, row tile)); kept in LDS,
+  // which leaves the registers to the W operands and the statistics.  e is
+  // rounded to bf16 here and r = e·2^(m_w - lse2) again before the M-GEMM (r is a
+  // bf16 MFMA operand in any case): half the LDS bytes of fp32 e, measured 3 %
+  // faster at K = 1024, with the sums and the log-normalisers still from fp32 e.
+  __shared__ uint2 es[kNW * 2 * kCT * 2 * 64];
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     };
 
     // Responsibilities of block i-2 (parity pb, first row rf): r = e · 2^(m_w - lse2)
-    // with e read back from this wave's LDS slot, rounded to bf16 and staged
+    // with e read back (bf16) from this wave's LDS slot, rounded to bf16 and staged
     // row-major for the transposing reads of the M-GEMM.
     auto prep_r = [&](auto PB_, int rf, int nr) {
       constexpr int pb = decltype(PB_)::value;
@@ -288,12 +291,15 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
         f[h] = (rf + r < nr) ? fast_exp2(mw[pb][h] - l2) : 0.f;
       }
       __bf16* rw = rs + wave * kBN * kRS;
-      const f32x4* ew = es + ((wave * 2 + pb) * kCT * 2) * 64 + lane;
+      const uint2* ew = es + ((wave * 2 + pb) * kCT * 2) * 64 + lane;
 #pragma unroll
       for (int ct = 0; ct < kCT; ++ct)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const f32x4 e = ew[(ct * 2 + h) * 64];
+          const uint2 q = ew[(ct * 2 + h) * 64];
+          const f32x2 e01 = __builtin_convertvector(__builtin_bit_cast(bf16x2, q.x), f32x2);
+          const f32x2 e23 = __builtin_convertvector(__builtin_bit_cast(bf16x2, q.y), f32x2);
+          const f32x4 e = f32x4{e01[0], e01[1], e23[0], e23[1]};
           const int r = 16 * h + li;
           const uint2 pk = make_uint2(cvt2(e[0] * f[h], e[1] * f[h]), cvt2(e[2] * f[h], e[3] * f[h]));
           *reinterpret_cast<uint2*>(rw + r * kRS + rswz(r, 16 * ct + 4 * g)) = pk;
@@ -346,7 +352,7 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     // block parity) and the wave's row sums for the workgroup combine.
     auto lse_epilogue = [&](const f32x4 (&T)[kCT][2], auto PB_) {
       constexpr int pb = decltype(PB_)::value;
-      f32x4* ew = es + ((wave * 2 + pb) * kCT * 2) * 64 + lane;
+      uint2* ew = es + ((wave * 2 + pb) * kCT * 2) * 64 + lane;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         float m = T[0][h][0];
@@ -362,7 +368,7 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) e[v] = fast_exp2(T[ct][h][v] - m);
           sum += (e[0] + e[1]) + (e[2] + e[3]);
-          ew[(ct * 2 + h) * 64] = e;
+          ew[(ct * 2 + h) * 64] = make_uint2(cvt2(e[0], e[1]), cvt2(e[2], e[3]));
         }
         sum = lanes_op<32, false>(lanes_op<16, false>(sum));
         mw[pb][h] = m;
