@@ -66,7 +66,7 @@ def _declare(lib):
         "gmmxx_hip_finalize_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_kmeans_pp_workspace_bytes": (i64, [i64, i64, i64, i64, ctypes.c_int]),
         "gmmxx_hip_kmeans_pp": (ctypes.c_int, [vp, i64, i64, i64, i64, ctypes.c_int, vp, vp, vp, vp, i64, vp]),
-        "gmmxx_hip_topk_workspace_bytes": (i64, [P]),
+        "gmmxx_hip_topk_workspace_bytes": (i64, [P, ctypes.c_int]),
         "gmmxx_hip_estep_stats_topk": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, ctypes.c_int, vp, vp, vp,
                                                       vp, vp, i64, vp]),
     }
@@ -177,10 +177,13 @@ def _device_tensor(t: torch.Tensor, name: str, dtype: Optional[torch.dtype] = No
 class Workspace:
     """Device scratch for one problem shape, sized by the library (256-byte aligned)."""
 
-    def __init__(self, prob: _Problem, device: torch.device, *, topk: bool = False):
+    def __init__(self, prob: _Problem, device: torch.device, *, top_k: Optional[int] = None):
+        """``top_k``: size for gmmxx_hip_estep_stats_topk with that k instead."""
         lib = load_library()
-        query = lib.gmmxx_hip_topk_workspace_bytes if topk else lib.gmmxx_hip_workspace_bytes
-        nbytes = int(query(ctypes.byref(prob)))
+        if top_k is None:
+            nbytes = int(lib.gmmxx_hip_workspace_bytes(ctypes.byref(prob)))
+        else:
+            nbytes = int(lib.gmmxx_hip_topk_workspace_bytes(ctypes.byref(prob), int(top_k)))
         if nbytes < 0:
             raise HipRuntimeError("problem not supported by the HIP engine: "
                                   + lib.gmmxx_hip_last_error().decode(errors="replace"))
@@ -307,8 +310,9 @@ def estep_stats_topk(covariance_type: str, x: torch.Tensor, means: torch.Tensor,
     """Approximate top-k E-step statistics (nk, sum_x, sum_q, ll_sum): each row's
     responsibility mass is spread over its ``top_k`` largest logits only (ties by
     lower component index), normalised over them; ``ll_sum`` sums the top-k
-    log-normalisers.  ``1 <= top_k < K``.  The workspace holds the (B, N, K)
-    logits, so callers pass row chunks (gmmxx/torch_fallback.py:667-777)."""
+    log-normalisers.  ``1 <= top_k < K``.  For top_k > 1 the workspace holds the
+    (B, N, K) logits, so callers pass row chunks (gmmxx/torch_fallback.py:667-777);
+    top_k = 1 (hard assignment) stores none."""
     require_hip()
     x = _device_tensor(x, "x")
     means = _device_tensor(means, "means", torch.float32)
@@ -319,7 +323,7 @@ def estep_stats_topk(covariance_type: str, x: torch.Tensor, means: torch.Tensor,
     if not 1 <= int(top_k) < K:
         raise ValueError(f"top_k must satisfy 1 <= top_k < K={K}, got {top_k}")
     prob = problem(covariance_type, x.dtype, B, N, D, K)
-    ws = ws or Workspace(prob, x.device, topk=True)
+    ws = ws or Workspace(prob, x.device, top_k=int(top_k))
     dev = x.device
     nk = torch.empty((B, K), dtype=torch.float32, device=dev)
     sum_x = torch.empty((B, K, D), dtype=torch.float32, device=dev)

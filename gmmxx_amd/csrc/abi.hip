@@ -393,10 +393,11 @@ void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, dou
   launch_finalize(f, s);
 }
 
-// Approximate top-k EM: the (B, N, K) log2 logits, each row's threshold logit
-// and index, and per-block log-likelihood sums, after the plan's workspace.
+// Approximate top-k EM: each row's threshold logit and index, per-block
+// log-likelihood sums, and (top_k > 1) the (B, N, K) log2 logits, after the
+// plan's workspace.  top_k = 1 stops before the logits (`hard`).
 struct TopkLayout {
-  size_t o_logits = 0, o_thr = 0, o_thri = 0, o_ll = 0, total = 0;
+  size_t o_logits = 0, o_thr = 0, o_thri = 0, o_ll = 0, hard = 0, total = 0;
 };
 TopkLayout topk_layout(const Plan& pl) {
   TopkLayout t;
@@ -407,10 +408,11 @@ TopkLayout topk_layout(const Plan& pl) {
     return o;
   };
   const size_t BN = (size_t)pl.B * pl.N;
-  t.o_logits = take(BN * pl.K * 4);
   t.o_thr = take(BN * 4);
   t.o_thri = take(BN * 4);
   t.o_ll = take((size_t)pl.B * topk_select_blocks(pl.N) * 8);
+  t.hard = off;
+  t.o_logits = take(BN * pl.K * 4);
   t.total = off;
   return t;
 }
@@ -582,10 +584,11 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   return check_hip("statistics unpack");
 }
 
-int64_t gmmxx_hip_topk_workspace_bytes(const gmmxx_problem* p) {
+int64_t gmmxx_hip_topk_workspace_bytes(const gmmxx_problem* p, int top_k) {
   Plan pl;
   if (plan_problem(p, &pl) != GMMXX_OK) return -1;
-  return (int64_t)topk_layout(pl).total;
+  const TopkLayout tl = topk_layout(pl);
+  return (int64_t)(top_k == 1 ? tl.hard : tl.total);
 }
 
 int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
@@ -597,9 +600,10 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   if (rc) return rc;
   if (!x) return fail(GMMXX_ERR_INVALID_ARGUMENT, "x is NULL");
   const TopkLayout tl = topk_layout(pl);
+  const size_t need = top_k == 1 ? tl.hard : tl.total;
   if (!ws) return fail(GMMXX_ERR_WORKSPACE, "workspace is NULL");
-  if (ws_bytes < 0 || (uint64_t)ws_bytes < tl.total)
-    return fail(GMMXX_ERR_WORKSPACE, "workspace too small: need " + std::to_string(tl.total) + " bytes");
+  if (ws_bytes < 0 || (uint64_t)ws_bytes < need)
+    return fail(GMMXX_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
   if ((uintptr_t)ws % 256 != 0) return fail(GMMXX_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (!means || !covs || !weights || !nk || !sum_x || !ll_sum) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
   if (pl.cov != TIED && !sum_q) return fail(GMMXX_ERR_INVALID_ARGUMENT, "sum_q is required for this covariance type");
@@ -612,12 +616,39 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
   // spherical bf16 at D = 128: the later passes read the augmented row chunk
   // that the log-normaliser pass stores.
+  float* thr = at<float>(ws, tl.o_thr);
+  int* thri = at<int>(ws, tl.o_thri);
+  if (top_k == 1) {
+    // Hard assignment: the first-argmax pass gives each row's maximum (the
+    // log-normaliser of a single component) and its index; the statistics pass
+    // then gives that component r = 1 by index, no logits stored.
+    TileArgs t = tile_args(pl, x, ws);
+    if (run_tile(pl, MODE_LSE_IDX, t, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+    CombineArgs c{};
+    c.B = pl.B;
+    c.ktiles = pl.ktiles;
+    c.N = pl.N;
+    c.part_ms = t.part_ms;
+    c.part_idx = t.part_idx;
+    c.lse2 = thr;
+    c.idx32 = thri;
+    c.max_only = 1;
+    c.ll_part = at<double>(ws, pl.o_ll);
+    launch_combine(c, s);
+    TileArgs u = tile_args(pl, x, ws);
+    u.lse2 = thr;
+    u.thr2 = thr;
+    u.thr_idx = thri;
+    u.hard = 1;
+    if (run_tile(pl, MODE_STATS_TOPK, u, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
+    launch_reduce_slices(u.part_stats, pl.slices, (int64_t)pl.B * pl.K * pl.JP, at<float>(ws, pl.o_stats), s,
+                         red_tmp(pl, ws), red_tmp_floats(pl));
+    launch_ll_reduce(at<double>(ws, pl.o_ll), pl.B * pl.cblocks, 1.0, ll_sum, s);
+  } else {
   if (pl.bf && pl.cov == SPH && pl.DP >= 128) {
     if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, false, s))) return rc;
   }
   float* logits = at<float>(ws, tl.o_logits);
-  float* thr = at<float>(ws, tl.o_thr);
-  int* thri = at<int>(ws, tl.o_thri);
   double* tll = at<double>(ws, tl.o_ll);
   TileArgs t = tile_args(pl, x, ws);
   t.proba = logits;
@@ -632,6 +663,7 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   launch_reduce_slices(u.part_stats, pl.slices, (int64_t)pl.B * pl.K * pl.JP, at<float>(ws, pl.o_stats), s,
                        red_tmp(pl, ws), red_tmp_floats(pl));
   launch_ll_reduce(tll, pl.B * sel_blocks, 1.0, ll_sum, s);
+  }
   if ((rc = check_hip("approximate top-k statistics"))) return rc;
   UnpackArgs k{};
   k.cov = pl.cov;

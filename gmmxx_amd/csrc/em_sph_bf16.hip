@@ -446,10 +446,11 @@ __global__ __launch_bounds__(64 * NW) void sph_bf16_kernel(TileArgs a) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const float l0 = A.t[ct][0][v], l1 = A.t[ct][1][v];
-            const bool k0 = l0 > t0[v] || (l0 == t0[v] && kk <= i0[v]);
-            const bool k1 = l1 > t1[v] || (l1 == t1[v] && kk <= i1[v]);
-            ar[ct][v] = (__bf16)(k0 ? fast_exp2(l0 - ls0[v]) : 0.f);
-            ar[ct][4 + v] = (__bf16)(k1 ? fast_exp2(l1 - ls1[v]) : 0.f);
+            // (hard: the one component thr_idx, by index, with r = 1 exactly)
+            const bool k0 = a.hard ? kk == i0[v] : (l0 > t0[v] || (l0 == t0[v] && kk <= i0[v]));
+            const bool k1 = a.hard ? kk == i1[v] : (l1 > t1[v] || (l1 == t1[v] && kk <= i1[v]));
+            ar[ct][v] = (__bf16)(k0 ? (a.hard ? 1.f : fast_exp2(l0 - ls0[v])) : 0.f);
+            ar[ct][4 + v] = (__bf16)(k1 ? (a.hard ? 1.f : fast_exp2(l1 - ls1[v])) : 0.f);
           }
         }
       } else {

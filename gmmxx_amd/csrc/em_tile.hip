@@ -745,9 +745,11 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               rr[ct][rt][v] = a.raw_logits ? l2 : fast_exp2(l2 - lse_s[bx * kBN + r]);
             } else if constexpr (TOPK) {
               // Only the row's top k (logit descending, then lower index) get mass.
+              // (hard: the one component thr_idx, by index, with r = 1 exactly)
               const float t = thr_s[bx * kBN + r];
-              const bool keep = l2 > t || (l2 == t && kbase + 16 * ct + li <= thri_s[bx * kBN + r]);
-              rr[ct][rt][v] = keep ? fast_exp2(l2 - lse_s[bx * kBN + r]) : 0.f;
+              const int kk = kbase + 16 * ct + li, ti = thri_s[bx * kBN + r];
+              const bool keep = a.hard ? kk == ti : (l2 > t || (l2 == t && kk <= ti));
+              rr[ct][rt][v] = keep ? (a.hard ? 1.f : fast_exp2(l2 - lse_s[bx * kBN + r])) : 0.f;
             } else {
               rr[ct][rt][v] = fast_exp2(l2 - lse_s[bx * kBN + r]);
             }

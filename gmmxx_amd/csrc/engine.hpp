@@ -29,6 +29,7 @@ struct TileArgs {
   int raw_logits;              // PROBA: write the log2-domain logits instead of responsibilities
   const float* thr2;           // [B][N] STATS_TOPK: each row's k-th largest logit (log2)
   const int* thr_idx;          // [B][N] STATS_TOPK: its component index (ties: lower index first)
+  int hard;                    // STATS_TOPK with k = 1: r = 1 for component thr_idx, else 0
 };
 
 // Approximate top-k EM (params.hip): per row of the (B, N, K) log2 logits, the

@@ -386,14 +386,15 @@ __global__ void combine_kernel(CombineArgs a) {
     for (int t = 0; t < a.ktiles; ++t) {
       const size_t o = ((size_t)t * a.B + b) * a.N + n;
       // Argmax partials exist only when the tile pass tracked them (labels requested).
-      lse_merge(m, s, idx, a.part_ms[2 * o], a.part_ms[2 * o + 1], a.labels ? a.part_idx[o] : 0);
+      lse_merge(m, s, idx, a.part_ms[2 * o], a.part_ms[2 * o + 1], (a.labels || a.idx32) ? a.part_idx[o] : 0);
     }
-    const float lse2 = m + __log2f(s);
+    const float lse2 = a.max_only ? m : m + __log2f(s);
     const size_t o = (size_t)b * a.N + n;
     if (a.lse2) a.lse2[o] = lse2;
     const float lse = lse2 * kLn2;
     if (a.scores) a.scores[o] = lse;
     if (a.labels) a.labels[o] = (int64_t)idx;
+    if (a.idx32) a.idx32[o] = idx;
     contrib = (double)lse;
   }
   const double t = block_sum(contrib, scratch);

@@ -31,6 +31,8 @@ struct CombineArgs {
   float* scores;           // [B][N] natural-log scores or null
   int64_t* labels;         // [B][N] or null
   double* ll_part;         // [B][gridDim.x] or null
+  int* idx32;              // [B][N] first argmax as int, or null (needs the argmax partials)
+  int max_only;            // lse2 (and the log-likelihood) from the row maximum alone
 };
 
 struct FinalizeArgs {

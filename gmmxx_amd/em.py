@@ -171,7 +171,8 @@ class _TopkStep:
         self.x, self.cov, self.k, self.top_k = x, covariance_type, k, top_k
         bsz, n, d = x.shape
         self.n = n
-        self.rows = topk_chunk_rows(bsz, n, k)
+        # top-1 (hard assignment) keeps no logits: one chunk
+        self.rows = n if top_k == 1 else topk_chunk_rows(bsz, n, k)
         self.ws: Dict[int, _hip.Workspace] = {}
         self.fin_ws = _hip.Workspace(_hip.problem(covariance_type, torch.float32, bsz, 1, d, k), x.device)
 
@@ -182,7 +183,7 @@ class _TopkStep:
             ws = self.ws.get(rows)
             if ws is None:
                 ws = _hip.Workspace(_hip.problem(self.cov, xc.dtype, xc.shape[0], rows, xc.shape[2], self.k),
-                                    xc.device, topk=True)
+                                    xc.device, top_k=self.top_k)
                 self.ws[rows] = ws
             yield xc, ws
 

@@ -144,9 +144,9 @@ def _sample_init(x_cpu, n_components, covariance_type, device, dtype, *, init_pa
 class _Workspaces:
     """One workspace per chunk shape (the full chunk and the last, shorter one)."""
 
-    def __init__(self, covariance_type, dtype, d, k, device, topk=False):
+    def __init__(self, covariance_type, dtype, d, k, device, top_k=None):
         self.cov, self.dtype, self.d, self.k, self.device = covariance_type, dtype, d, k, device
-        self.topk = topk
+        self.top_k = top_k
         self.cache: Dict[int, _hip.Workspace] = {}
 
     def get(self, rows: int) -> _hip.Workspace:
@@ -156,7 +156,7 @@ class _Workspaces:
                 raise _hip.HipRuntimeError(
                     f"shape not supported by the hip backend: {self.cov} N={rows} D={self.d} K={self.k}")
             ws = _hip.Workspace(_hip.problem(self.cov, self.dtype, 1, rows, self.d, self.k), self.device,
-                                topk=self.topk)
+                                top_k=self.top_k)
             self.cache[rows] = ws
         return ws
 
@@ -204,8 +204,9 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
     stream = ChunkStream(x_cpu, device, dtype, chunk_size_N)
     wss = _Workspaces(covariance_type, dtype, d, k, device)
     # the top-k E-step holds a chunk's logits: sub-chunks bound that buffer
-    sub_rows = em.topk_chunk_rows(1, min(n, chunk_size_N), k) if top_k is not None else 0
-    topk_wss = _Workspaces(covariance_type, dtype, d, k, device, topk=True) if top_k is not None else None
+    sub_rows = (min(n, chunk_size_N) if top_k == 1 else em.topk_chunk_rows(1, min(n, chunk_size_N), k)) \
+        if top_k is not None else 0
+    topk_wss = _Workspaces(covariance_type, dtype, d, k, device, top_k=top_k) if top_k is not None else None
     fin_ws = _hip.Workspace(_hip.problem(covariance_type, torch.float32, 1, 1, d, k), device)
 
     gram = None

@@ -117,14 +117,16 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
  * row's responsibilities cover only its top_k components (largest logits,
  * ties to the lower component index), normalised over those, and ll_sum sums
  * the top-k log-normalisers.  1 <= top_k <= K-1 (top_k >= K is exact EM: use
- * gmmxx_hip_estep_stats).  The (B, N, K) logits are materialised in the
- * workspace, whose size is gmmxx_hip_topk_workspace_bytes; callers bound it
- * by passing row chunks, as the reference does with chunk_size_N.
+ * gmmxx_hip_estep_stats).  For top_k > 1 the (B, N, K) logits are materialised
+ * in the workspace, whose size is gmmxx_hip_topk_workspace_bytes(p, top_k);
+ * callers bound it by passing row chunks, as the reference does with
+ * chunk_size_N.  top_k = 1 (hard assignment to the first maximum) stores no
+ * logits and needs only O(B·N) beyond the plan's workspace.
  * Replaces _topk_logits_for_chunk + _accumulate_topk_stats
  * (gmmxx/torch_fallback.py:667-777, used by the EM loops at :2101-2145,
  * :2504-2526, :2915-2936) and the CUDA/Triton approximate updates
  * (gmmxx/_cuda.py:783-889, gmmxx/approx_update_triton.py:25-281). */
-int64_t gmmxx_hip_topk_workspace_bytes(const gmmxx_problem* p);
+int64_t gmmxx_hip_topk_workspace_bytes(const gmmxx_problem* p, int top_k);
 int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const float* means,
                                const float* covariances, const float* weights, double reg_covar,
                                double min_weight, int top_k, float* nk, float* sum_x, float* sum_q,

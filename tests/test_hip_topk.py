@@ -162,7 +162,7 @@ def test_topk_abi_rejects_bad_top_k(hip):
     x, means, covs, w = make_problem("spherical", 1, 256, 8, 4, seed=46)
     xd, md, cd, wd = to_dev(x), to_dev(means), to_dev(covs), to_dev(w)
     prob = hip.problem("spherical", torch.float32, 1, 256, 8, 4)
-    ws = hip.Workspace(prob, xd.device, topk=True)
+    ws = hip.Workspace(prob, xd.device, top_k=2)
     out = [torch.empty(s, device=DEV) for s in ((1, 4), (1, 4, 8), (1, 4), (1,))]
     lib = hip.load_library()
     for bad in (0, 4, -1):
