@@ -463,10 +463,72 @@ __global__ __launch_bounds__(64 * kSelWaves) void topk_select_kernel(const float
   }
 }
 
+// The same selection with the row held in registers (NV values per lane,
+// K <= 64·NV): the row is read once instead of once per round.
+template <int NV>
+__global__ __launch_bounds__(64 * kSelWaves) void topk_select_reg_kernel(const float* __restrict__ logits,
+                                                                         int64_t N, int K, int top_k, float* lse2,
+                                                                         float* thr2, int* thr_idx, double* ll_part) {
+  __shared__ double llw[kSelWaves];
+  const int b = blockIdx.y, wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int64_t n = (int64_t)blockIdx.x * kSelWaves + wave;
+  double contrib = 0.0;
+  if (n < N) {
+    const float* row = logits + ((size_t)b * N + n) * K;
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = (lane + 64 * j < K) ? row[lane + 64 * j] : -INFINITY;
+    float pv = INFINITY;   // previous pick (value, index)
+    int pi = -1;
+    float m = 0.f, sum = 0.f;
+    for (int r = 0; r < top_k; ++r) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int k = lane + 64 * j;
+        const bool after = v[j] < pv || (v[j] == pv && k > pi);
+        if (k < K && after && (v[j] > bv || (v[j] == bv && k < bi))) { bv = v[j]; bi = k; }
+      }
+      for (int off = 32; off >= 1; off /= 2) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if (r == 0) m = bv;
+      sum += fast_exp2(bv - m);
+      pv = bv;
+      pi = bi;
+    }
+    const float l2 = m + __log2f(sum);
+    if (lane == 0) {
+      const size_t o = (size_t)b * N + n;
+      lse2[o] = l2;
+      thr2[o] = pv;
+      thr_idx[o] = pi;
+    }
+    contrib = (double)l2 * (double)kLn2;
+  }
+  if (lane == 0) llw[wave] = contrib;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < kSelWaves; ++w) t += llw[w];
+    ll_part[(size_t)b * gridDim.x + blockIdx.x] = t;
+  }
+}
+
 void launch_topk_select(const float* logits, int B, int64_t N, int K, int top_k, float* lse2, float* thr2,
                         int* thr_idx, double* ll_part, int ll_blocks, hipStream_t s) {
-  topk_select_kernel<<<dim3(ll_blocks, B), 64 * kSelWaves, 0, s>>>(logits, N, K, top_k, lse2, thr2, thr_idx,
-                                                                     ll_part);
+  const dim3 grid(ll_blocks, B), block(64 * kSelWaves);
+  if (K <= 64 * 4)
+    topk_select_reg_kernel<4><<<grid, block, 0, s>>>(logits, N, K, top_k, lse2, thr2, thr_idx, ll_part);
+  else if (K <= 64 * 16)
+    topk_select_reg_kernel<16><<<grid, block, 0, s>>>(logits, N, K, top_k, lse2, thr2, thr_idx, ll_part);
+  else if (K <= 64 * 64)
+    topk_select_reg_kernel<64><<<grid, block, 0, s>>>(logits, N, K, top_k, lse2, thr2, thr_idx, ll_part);
+  else
+    topk_select_kernel<<<grid, block, 0, s>>>(logits, N, K, top_k, lse2, thr2, thr_idx, ll_part);
 }
 
 // Tied EM iteration: the logits leave out the per-row xᵀPx, so the row
