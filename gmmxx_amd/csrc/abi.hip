@@ -51,7 +51,7 @@ struct Plan {
 };
 
 constexpr int kTargetWaves = 4096;      // 16 waves per CU on 256 CUs
-constexpr int kMinBlocksPerSlice = 8;  // row blocks of one slice (bounds the partial-statistics count)
+constexpr int kMinBlocksPerSlice = 3;  // row blocks of one slice (bounds the partial-statistics count)
 
 int dp_for(int64_t d) {
   const int dps[] = {16, 32, 64, 128};
