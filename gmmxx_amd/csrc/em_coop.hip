@@ -377,28 +377,6 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
         red_s[(pb * kNW + wave) * RR + 16 * h + li] = sum;
       }
     };
-    // Issue order hints for the steady state (one MFMA, then VALU/LDS work).
-    auto interleave_e = [&]() {
-      constexpr int kMask_VALU = 0x002, kMask_MFMA = 0x008, kMask_DSR = 0x100, kMask_DSW = 0x200;
-#pragma unroll
-      for (int k = 0; k < kCT * 2 * (2 * ECH + 1); ++k) {
-        __builtin_amdgcn_sched_group_barrier(kMask_DSR, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kMask_MFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kMask_VALU, 1, 0);
-        if (k >= 12 && k < 16) __builtin_amdgcn_sched_group_barrier(kMask_DSW, 1, 0);
-      }
-    };
-    auto interleave_m = [&]() {
-      constexpr int kMask_VALU = 0x002, kMask_MFMA = 0x008, kMask_DSR = 0x100, kMask_DSW = 0x200;
-#pragma unroll
-      for (int k = 0; k < kCT * JT; ++k) {
-        __builtin_amdgcn_sched_group_barrier(kMask_DSR, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kMask_MFMA, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kMask_VALU, 4, 0);
-        if (k >= 10 && k < 14) __builtin_amdgcn_sched_group_barrier(kMask_DSW, 2, 0);
-      }
-    };
-
     if (nblk > 0) { fetch(0); stash(0); }
     if (nblk > 1) { fetch(kBN); stash(1); }
     __syncthreads();
@@ -443,7 +421,6 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       f32x4 T[kCT][2];
       if constexpr (FIN) prep_r(PB_, r0 - 2 * kBN, nrows);
       if constexpr (EGM) egemm(i % kNB, T);
-      if constexpr (FIN && EGM) interleave_e();
 
       // ---- wave 0: the partners' words of block i-1 (published at the top of
       // this iteration), loaded now and checked after the second half ----
@@ -469,7 +446,6 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
         mgemm((i - 2) % kNB);
       }
       if constexpr (EGM) lse_epilogue(T, PB_);
-      if constexpr (FIN && EGM) interleave_m();
       if constexpr (FIN) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
