@@ -12,11 +12,13 @@ large-N bf16 case (C1L) are measured the same way and reported under
 the BASELINE recipes, generated on the device with seeded generators.
 
 Reported per config:
-  * iter_per_s / ms_per_iter: wall time of the timed EM iterations;
+  * iter_per_s / ms_per_iter: wall time of the timed EM iterations, each one
+    ``gmmxx_hip_em_step`` call as in the estimator's fit loop;
   * roofline: the dominant kernel's algorithmic rate (FLOP/s, or bytes/s for
     the HBM-bound case) from its launch times, measured with HIP events
-    recorded on the stream the kernels are launched on, against the MI355X
-    peak of its bound;
+    recorded on the stream the kernels are launched on (a second pass over
+    the same iterations, one ``gmmxx_hip_em_phase`` call per phase), against
+    the MI355X peak of its bound;
   * em_iteration: the whole iteration's algorithmic rate;
   * cpu_baseline: the CPU oracle (a restatement of the reference torch
     fallback) timed on a bounded row sample, scaled linearly to full N.
@@ -280,15 +282,25 @@ def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
     means.copy_(means0)
     covs.copy_(covs0)
     w.copy_(w0)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(steps)]
+    # Timed: the product's EM loop, one gmmxx_hip_em_step call per iteration.
     print(f"[bench] {name}: timing {steps} EM iterations", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        step(warmup + i, evs[i])
+        _hip.em_step(cov, x, means, covs, w, lb[warmup + i:warmup + i + 1], gram_xx=gram, ws=ws)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = 1e3 * wall / steps
+    lb_last = float(lb[warmup + steps - 1].item())
+    # Per-phase kernel times (HIP events on the launch stream) from a second pass
+    # over the same iterations, one gmmxx_hip_em_phase call per phase.
+    means.copy_(means0)
+    covs.copy_(covs0)
+    w.copy_(w0)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(steps)]
+    for i in range(steps):
+        step(warmup + i, evs[i])
+    torch.cuda.synchronize()
     phase_ms = {ph: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, ph in enumerate(phases)}
     fl = flops(cfg)
     dominant = max(("lse_tile", "stats_tile"), key=lambda p: phase_ms[p])
@@ -317,7 +329,7 @@ def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
         "em_iteration": {"algorithmic_tflop": fl["iteration"] / 1e12, "achieved": it_rate, "unit": it_unit,
                          "frac": it_rate / peak, "phase_ms": phase_ms},
         "setup_ms": setup_ms,
-        "lower_bound_last": float(lb[warmup + steps - 1].item()),
+        "lower_bound_last": lb_last,
     }
     if name == "c5":
         # Tail of the config: predict_proba + score_samples on all points.
