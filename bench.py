@@ -46,20 +46,27 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK = {"bf16": 2516.6, "fp32": 157.3, "hbm": 8000.0}   # TFLOP/s, TFLOP/s, GB/s (MI355X)
+# MI355X peaks: dense bf16 and fp32 MFMA (TFLOP/s), HBM (GB/s).  "fp32x3" is the
+# bound of what the fp32 configs execute: each fp32-accurate product is six
+# bf16 MFMAs on three-way bf16 splits of both operands, so their algorithmic
+# fp32 FLOPs top out at the bf16 peak / 6.
+PEAK = {"bf16": 2516.6, "fp32": 157.3, "fp32x3": 2516.6 / 6.0, "hbm": 8000.0}
+PEAK_BASIS = {"bf16": "dense bf16 MFMA peak 2516.6 TFLOP/s",
+              "fp32x3": "dense bf16 MFMA peak / 6 = 419.4 TFLOP/s (six bf16 MFMAs per fp32-accurate product)",
+              "hbm": "HBM3E 8 TB/s"}
 METRIC = "EM iter/s + % bf16 MFMA peak, spherical bf16 N=4M D=128 K=1024"
 HEADLINE = "c2"
 
 CONFIGS = {
-    "c1": dict(cov="spherical", B=1, N=100_000, D=32, K=64, dtype="fp32", iters=20, seed=0, bound="fp32",
+    "c1": dict(cov="spherical", B=1, N=100_000, D=32, K=64, dtype="fp32", iters=20, seed=0, bound="fp32x3",
                desc="spherical fp32 N=100000 D=32 K=64, 20 iterations"),
     "c2": dict(cov="spherical", B=1, N=4_194_304, D=128, K=1024, dtype="bf16", iters=10, seed=1, bound="bf16",
                desc="spherical bf16 N=4194304 D=128 K=1024, 10 iterations"),
-    "c3": dict(cov="diag", B=1, N=2_097_152, D=64, K=512, dtype="fp32", iters=10, seed=2, bound="fp32",
+    "c3": dict(cov="diag", B=1, N=2_097_152, D=64, K=512, dtype="fp32", iters=10, seed=2, bound="fp32x3",
                desc="diag fp32 N=2097152 D=64 K=512, 10 iterations"),
-    "c4": dict(cov="tied", B=1, N=1_048_576, D=64, K=256, dtype="fp32", iters=10, seed=3, bound="fp32",
+    "c4": dict(cov="tied", B=1, N=1_048_576, D=64, K=256, dtype="fp32", iters=10, seed=3, bound="fp32x3",
                desc="tied fp32 N=1048576 D=64 K=256, 10 iterations"),
-    "c5": dict(cov="full", B=16, N=262_144, D=16, K=32, dtype="fp32", iters=10, seed=4, bound="fp32",
+    "c5": dict(cov="full", B=16, N=262_144, D=16, K=32, dtype="fp32", iters=10, seed=4, bound="fp32x3",
                desc="full fp32 B=16 N=262144 D=16 K=32, 10 iterations + predict_proba + score_samples"),
     "c1l": dict(cov="spherical", B=1, N=1 << 24, D=32, K=64, dtype="bf16", iters=20, seed=0, bound="hbm",
                 desc="spherical bf16 N=16777216 D=32 K=64 (C1 recipe, large N), 20 iterations"),
@@ -71,14 +78,18 @@ CPU_SAMPLE = {"c1": (100_000, 20), "c2": (131_072, 2), "c3": (131_072, 2), "c4":
 
 def flops(cfg):
     """Algorithmic FLOPs of the minimal contractions (E-step logits and M-step
-    rᵀ·[x-features | 1]) per EM iteration, split by the kernel computing them."""
+    rᵀ·[x-features | 1]) per EM iteration, split by the kernel computing them.
+    Tied: the per-row xᵀPx (2·N·D² per iteration in the reference) is not
+    computed by the EM iteration here -- it cancels in the responsibilities
+    and the lower bound takes it back as -½·tr(P·XᵀX) -- so it is left out of
+    the count rather than credited as work done."""
     b, n, d, k = cfg["B"], cfg["N"], cfg["D"], cfg["K"]
     bn = b * n
     s = d * (d + 1) // 2
     e, m = {
         "spherical": (2 * bn * k * d, 2 * bn * k * (d + 2)),
         "diag": (2 * bn * k * 2 * d, 2 * bn * k * (2 * d + 1)),
-        "tied": (2 * bn * d * d + 2 * bn * k * d, 2 * bn * k * (d + 1)),
+        "tied": (2 * bn * k * d, 2 * bn * k * (d + 1)),
         "full": (2 * bn * k * (s + d), 2 * bn * k * (s + d + 1)),
     }[cfg["cov"]]
     return {"lse_tile": float(e), "stats_tile": float(m), "iteration": float(e + m)}
@@ -125,9 +136,13 @@ def _global_cov(x, reg=1e-6):
     return cov.to(torch.float32)
 
 
-def make_data(name, device):
+def make_data(name, device, n=None):
+    """(x, initial means, covariances, weights) of a config's recipe; ``n``
+    overrides the row count per problem (the parity tests run the recipes at
+    sizes the CPU oracle finishes in seconds)."""
     cfg = CONFIGS[name]
-    b, n, d, k = cfg["B"], cfg["N"], cfg["D"], cfg["K"]
+    b, d, k = cfg["B"], cfg["D"], cfg["K"]
+    n = cfg["N"] if n is None else int(n)
     g = torch.Generator(device=device).manual_seed(cfg["seed"])
     xdt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
     x = torch.empty((b, n, d), dtype=xdt, device=device)
@@ -324,6 +339,7 @@ def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
         "steps": steps, "warmup": warmup, "ms_per_iter": ms_per_step, "iter_per_s": 1e3 / ms_per_step,
         "gflop_per_s": fl["iteration"] / (ms_per_step * 1e-3) / 1e9,
         "roofline": {"bound": "hbm" if bound == "hbm" else "mfma", "peak_kind": bound,
+                     "peak_basis": PEAK_BASIS[bound],
                      "kernel": kernel_label(cfg, dominant), "achieved": achieved, "peak": peak, "unit": unit,
                      "frac": achieved / peak, "traffic": _traffic_from_profile(name, dominant)},
         "em_iteration": {"algorithmic_tflop": fl["iteration"] / 1e12, "achieved": it_rate, "unit": it_unit,
@@ -331,21 +347,24 @@ def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
         "setup_ms": setup_ms,
         "lower_bound_last": lb_last,
     }
+    if bound == "fp32x3":
+        # the same rate against the fp32 MFMA peak, for comparison with fp32-only engines
+        out["roofline"]["fp32_peak_frac"] = achieved / PEAK["fp32"]
     if name == "c5":
-        # Tail of the config: predict_proba + score_samples on all points.
+        # Tail of the config: predict_proba + score_samples on all points, from
+        # one E-step (gmmxx_hip_predict_proba_score).
         for _ in range(2):
-            _hip.predict_proba(cov, x, means, covs, w, ws=ws)
-            _hip.score(cov, x, means, covs, w, want_labels=False, ws=ws)
+            _hip.predict_proba_score(cov, x, means, covs, w, ws=ws)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         reps = 5
         for _ in range(reps):
-            _hip.predict_proba(cov, x, means, covs, w, ws=ws)
-            _hip.score(cov, x, means, covs, w, want_labels=False, ws=ws)
+            _hip.predict_proba_score(cov, x, means, covs, w, ws=ws)
         torch.cuda.synchronize()
         tail_ms = 1e3 * (time.perf_counter() - t0) / reps
-        out["tail"] = {"ms": tail_ms, "what": "predict_proba (B,N,K fp32 written) + score_samples",
-                       "proba_write_gb_per_s": b * n * k * 4 / (tail_ms * 1e-3) / 1e9}
+        out["tail"] = {"ms": tail_ms, "what": "predict_proba (B,N,K fp32 written) + score_samples, one E-step",
+                       "proba_write_gb_per_s": b * n * k * 4 / (tail_ms * 1e-3) / 1e9,
+                       "hbm_frac": (x_bytes(cfg) + b * n * (k + 1) * 4) / (tail_ms * 1e-3) / 1e9 / PEAK["hbm"]}
     if copy_calibration:
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -356,29 +375,98 @@ def run_config(name, dev, steps=None, warmup=2, copy_calibration=False):
     return out, (x, means0, covs0, w0)
 
 
+def _cpu_facts():
+    """(threads to use, description): the CPUs this process may run on, capped by
+    the cgroup CPU quota when one is set; the CPU model from /proc/cpuinfo."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    threads = min(usable, quota) if quota else usable
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return threads, {"model": model, "logical_cpus": os.cpu_count(), "affinity_cpus": usable,
+                     "cgroup_cpu_quota": quota}
+
+
 def cpu_baseline(name, data):
     """Oracle EM iterations on the first rows of each problem (fp32 on the
-    same values), scaled linearly in N to the full workload."""
+    same values), scaled linearly in N to the full workload.  Also returns the
+    oracle's result on that sample, which the parity leg compares against."""
     from oracle import torch_ref
     cfg = CONFIGS[name]
     rows, iters = CPU_SAMPLE[name]
     x, m0, c0, w0 = data
     rows = min(rows, cfg["N"])
-    torch.set_num_threads(max(1, min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16")))))
+    threads, facts = _cpu_facts()
+    torch.set_num_threads(threads)
     xs = x[:, :rows].to(torch.float32).cpu()
     m, c, w = m0.cpu(), c0.cpu(), w0.cpu()
     torch_ref.fit(xs[:, :min(rows, 4096)], cfg["K"], cfg["cov"], max_iters=1, tol=0.0, init_means=m,
                   init_covs=c, init_weights=w, compute_labels=False)  # warm the thread pool
     t0 = time.perf_counter()
-    torch_ref.fit(xs, cfg["K"], cfg["cov"], max_iters=iters, tol=0.0, init_means=m, init_covs=c,
-                  init_weights=w, compute_labels=False)
+    ref = torch_ref.fit(xs, cfg["K"], cfg["cov"], max_iters=iters, tol=0.0, init_means=m, init_covs=c,
+                        init_weights=w, compute_labels=False)
     dt = (time.perf_counter() - t0) / iters
     full_iter_s = dt * (cfg["N"] / rows)
     sample = ("the full workload" if rows == cfg["N"] else
               f"the first {rows} of {cfg['N']} rows per problem, scaled linearly in N")
-    return {"value": 1.0 / full_iter_s, "unit": "EM iter/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{iters} oracle EM iterations on {sample} ({dt:.3f} s per sampled iteration)"}
+    out = {"value": 1.0 / full_iter_s, "unit": "EM iter/s", "cores": torch.get_num_threads(),
+           "kind": "port", "cpu": facts,
+           "sample": f"{iters} oracle EM iterations on {sample} ({dt:.3f} s per sampled iteration)"}
+    return out, (rows, iters, ref)
+
+
+def parity(name, data, sample):
+    """Part of the CPU-baseline leg, as the checker: one GPU fit (em_step per
+    iteration) on that leg's row sample from the same initial parameters,
+    judged against the oracle's fit of the sample by oracle/judge.py --
+    per-iteration mean log-likelihood rtol 1e-5 (fp32) / 2e-3 (bf16); fp32
+    parameters element-wise rtol 1e-4 with floors 1e-5·rms(x) (means),
+    1e-5·mean(x²) (covariances), 1e-7 (weights); values outside the bar count
+    as explained when at least as close to a float64 fit from the same start
+    as the oracle's are (factor 4).  For bf16 x the bar is the log-likelihood."""
+    from gmmxx_amd import em
+    from oracle import f64_em, judge
+    cfg = CONFIGS[name]
+    rows, iters, (_, e_m, e_c, e_w, e_info) = sample
+    x, m0, c0, w0 = data
+    xs = x[:, :rows].contiguous()
+    _, m, c, w, info = em.fit(xs, cfg["K"], cfg["cov"], max_iters=iters, tol=0.0, init_means=m0, init_covs=c0,
+                              init_weights=w0, compute_labels=False, record_all_lower_bounds=True)
+    bf = cfg["dtype"] == "bf16"
+    xc = xs.float().cpu()
+    truth = []
+
+    def t64():
+        if not truth:
+            truth.extend(f64_em.trajectory(xc, cfg["cov"], m0.cpu(), c0.cpu(), w0.cpu(), iters))
+        return truth
+
+    ll = judge.judge_ll(info["lower_bound_history"], e_info["lower_bound_history"], 2e-3 if bf else 1e-5,
+                        lambda: t64()[0])
+    res = {"rows": rows, "iters": iters, "lower_bound_hip": info["lower_bound_history"],
+           "lower_bound_oracle": e_info["lower_bound_history"], "lower_bound": ll}
+    ok = ll["unexplained"] == 0
+    for got, exp, kind, j in ((m, e_m, "means", 1), (c, e_c, "covs", 2), (w, e_w, "weights", 3)):
+        r = judge.judge_params(got, exp, kind, xc, bf, None if bf else (lambda j=j: t64()[j]))
+        res[kind] = r
+        ok = ok and (bf or r["unexplained"] == 0)
+    res["pass"] = bool(ok)
+    return res
 
 
 def main():
@@ -410,7 +498,9 @@ def main():
                                copy_calibration=args.copy_calibration and nm == names[-1])
         if not args.no_cpu_baseline:
             print(f"[bench] {nm}: cpu baseline", file=sys.stderr, flush=True)
-            res["cpu_baseline"] = cpu_baseline(nm, data)
+            res["cpu_baseline"], sample = cpu_baseline(nm, data)
+            print(f"[bench] {nm}: parity on the cpu-baseline sample", file=sys.stderr, flush=True)
+            res["parity"] = parity(nm, data, sample)
         del data
         torch.cuda.empty_cache()
         results[nm] = res
@@ -435,6 +525,8 @@ def main():
     }
     if "cpu_baseline" in head:
         result["cpu_baseline"] = head["cpu_baseline"]
+    if "parity" in head:
+        result["parity"] = head["parity"]
     result["configs"] = results
     print(json.dumps(result), flush=True)
 

@@ -34,8 +34,29 @@ class HipBackendUnavailable(RuntimeError):
 
 class HipRuntimeError(RuntimeError):
     """A library call returned a nonzero status (the message comes from
-    gmmxx_hip_last_error).  Role of CudaRuntimeFallback (gmmxx/_cuda.py:39-41),
-    except that nothing falls back: the error propagates to the caller."""
+    gmmxx_hip_last_error), or a cooperative pass reported a timed-out wait."""
+
+
+class HipRuntimeFallback(HipRuntimeError):
+    """The reference's runtime-error contract (CudaRuntimeFallback,
+    gmmxx/_cuda.py:39-54, gmmxx/_dispatch.py:189-204): a failing library call
+    raises this, unless ``GMMXX_HIP_NO_FALLBACK=1``, in which case the plain
+    HipRuntimeError propagates.  Nothing in this package catches it -- there is
+    no CPU or PyTorch path to fall to; a dispatcher that has one (the
+    reference's) catches it and re-resolves."""
+
+
+def no_fallback() -> bool:
+    """``GMMXX_HIP_NO_FALLBACK=1``: errors surface as plain HipRuntimeError
+    (role of _no_fallback, gmmxx/_cuda.py:51-54)."""
+    return os.environ.get("GMMXX_HIP_NO_FALLBACK", "").lower() in {"1", "true", "yes"}
+
+
+class DevInfo(ctypes.Structure):
+    _fields_ = [("device", ctypes.c_int32), ("supported", ctypes.c_int32), ("arch", ctypes.c_char * 64),
+                ("compute_units", ctypes.c_int32), ("wave_size", ctypes.c_int32), ("clock_khz", ctypes.c_int32),
+                ("coop_capacity", ctypes.c_int32), ("hbm_bytes", ctypes.c_int64),
+                ("lds_per_workgroup", ctypes.c_int64)]
 
 
 class _Problem(ctypes.Structure):
@@ -56,12 +77,15 @@ def _declare(lib):
         "gmmxx_hip_last_error": (ctypes.c_char_p, []),
         "gmmxx_hip_canary": (ctypes.c_int, [vp, vp, i64, i32, vp]),
         "gmmxx_hip_supported": (ctypes.c_int, [P]),
+        "gmmxx_hip_device_info": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(DevInfo)]),
+        "gmmxx_hip_take_status": (ctypes.c_int, [P, vp, i64, vp, vp]),
         "gmmxx_hip_workspace_bytes": (i64, [P]),
         "gmmxx_hip_em_step": (ctypes.c_int, [P, vp, vp, vp, vp, vp, f64, f64, vp, vp, i64, vp]),
         "gmmxx_hip_em_phase": (ctypes.c_int, [P, ctypes.c_int, vp, vp, vp, vp, vp, f64, f64, vp, vp, i64, vp]),
         "gmmxx_hip_estep_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_score": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_predict_proba": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, i64, vp]),
+        "gmmxx_hip_predict_proba_score": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_gram": (ctypes.c_int, [P, vp, vp, vp, i64, vp]),
         "gmmxx_hip_finalize_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_kmeans_pp_workspace_bytes": (i64, [i64, i64, i64, i64, ctypes.c_int]),
@@ -79,8 +103,9 @@ def _declare(lib):
 
 def exported_symbols() -> Tuple[str, ...]:
     return ("gmmxx_hip_abi_version", "gmmxx_hip_last_error", "gmmxx_hip_canary",
-            "gmmxx_hip_supported", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_phase",
+            "gmmxx_hip_supported", "gmmxx_hip_device_info", "gmmxx_hip_take_status", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_phase",
             "gmmxx_hip_estep_stats", "gmmxx_hip_score", "gmmxx_hip_predict_proba",
+            "gmmxx_hip_predict_proba_score",
             "gmmxx_hip_gram", "gmmxx_hip_finalize_stats", "gmmxx_hip_topk_workspace_bytes",
             "gmmxx_hip_estep_stats_topk", "gmmxx_hip_kmeans_pp_workspace_bytes", "gmmxx_hip_kmeans_pp")
 
@@ -142,7 +167,8 @@ def last_error() -> str:
 
 def _check(rc: int, what: str) -> None:
     if rc != 0:
-        raise HipRuntimeError(f"{what} failed (status {rc}): {last_error()}")
+        cls = HipRuntimeError if no_fallback() else HipRuntimeFallback
+        raise cls(f"{what} failed (status {rc}): {last_error()}")
 
 
 def problem(covariance_type: str, x_dtype: torch.dtype, B: int, N: int, D: int, K: int) -> _Problem:
@@ -187,10 +213,43 @@ class Workspace:
         if nbytes < 0:
             raise HipRuntimeError("problem not supported by the HIP engine: "
                                   + lib.gmmxx_hip_last_error().decode(errors="replace"))
-        self._buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+        # Zeroed once: the asynchronous status word (gmmxx_hip_take_status) starts clear.
+        self._buf = torch.zeros(nbytes + 256, dtype=torch.uint8, device=device)
         base = self._buf.data_ptr()
         self.ptr = ctypes.c_void_p(base + (-base) % 256)
         self.nbytes = nbytes
+        self.prob = prob
+        self.device = torch.device(device)
+
+
+def take_status(ws: Workspace) -> torch.Tensor:
+    """Device uint32 word: the asynchronous failures recorded on ``ws`` since the
+    last call (nonzero: a cooperative pass gave up waiting for a partner; its
+    iteration kept the parameters and wrote a NaN lower bound).  Clears it;
+    stream-ordered, no synchronisation."""
+    out = torch.zeros((1,), dtype=torch.int32, device=ws.device)
+    _check(_lib.gmmxx_hip_take_status(ctypes.byref(ws.prob), ws.ptr, ws.nbytes, _ptr(out), _stream(ws.device)),
+           "gmmxx_hip_take_status")
+    return out
+
+
+def raise_on_status(status: torch.Tensor, what: str) -> None:
+    """Raises HipRuntimeError when a take_status word is nonzero (synchronises)."""
+    if int(status.item()) != 0:
+        raise HipRuntimeError(
+            f"{what}: a cooperative single-pass launch timed out waiting for a partner workgroup "
+            "(are other kernels occupying the GPU?); the affected iterations left the parameters "
+            "unchanged and recorded a NaN lower bound")
+
+
+def device_info(device: int = 0) -> dict:
+    """The library's view of a device (gmmxx_hip_device_info)."""
+    info = DevInfo()
+    _check(load_library().gmmxx_hip_device_info(int(device), ctypes.byref(info)), "gmmxx_hip_device_info")
+    return {"device": info.device, "supported": bool(info.supported), "arch": info.arch.decode(errors="replace"),
+            "compute_units": info.compute_units, "wave_size": info.wave_size, "clock_khz": info.clock_khz,
+            "coop_capacity": info.coop_capacity, "hbm_bytes": info.hbm_bytes,
+            "lds_per_workgroup": info.lds_per_workgroup}
 
 
 def _shape(x: torch.Tensor, means: torch.Tensor) -> Tuple[int, int, int, int]:
@@ -271,7 +330,15 @@ def em_phase(phase: str, covariance_type: str, x: torch.Tensor, means: torch.Ten
              gram_xx: Optional[torch.Tensor] = None) -> None:
     """Runs one phase of em_step (see EM_PHASES) on the current stream; the
     workspace carries the state between phases."""
+    require_hip()
+    if phase not in EM_PHASES:
+        raise ValueError(f"phase must be one of {EM_PHASES}")
+    x = _device_tensor(x, "x")
     B, N, D, K = _shape(x, means)
+    for t, nm in ((means, "means"), (covs, "covariances"), (weights, "weights"), (lower_bound_out, "lower_bound")):
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise ValueError(f"{nm} must be a contiguous float32 GPU tensor")
+    _check_params(covariance_type, means, covs, weights, B, K, D)
     prob = problem(covariance_type, x.dtype, B, N, D, K)
     _check(_lib.gmmxx_hip_em_phase(ctypes.byref(prob), EM_PHASES.index(phase), _ptr(x), _ptr(means), _ptr(covs),
                                    _ptr(weights), _ptr(gram_xx), float(reg_covar), float(min_weight),
@@ -431,3 +498,24 @@ def predict_proba(covariance_type: str, x: torch.Tensor, means: torch.Tensor, co
                                         _ptr(out), ws.ptr, ws.nbytes, _stream(x.device)),
            "gmmxx_hip_predict_proba")
     return out
+
+
+def predict_proba_score(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+                        weights: torch.Tensor, *, ws: Optional[Workspace] = None):
+    """(responsibilities (B, N, K), per-sample log-likelihood (B, N)) from one
+    E-step (gmmxx_hip_predict_proba_score)."""
+    require_hip()
+    x = _device_tensor(x, "x")
+    means = _device_tensor(means, "means", torch.float32)
+    covs = _device_tensor(covs, "covariances", torch.float32)
+    weights = _device_tensor(weights, "weights", torch.float32)
+    B, N, D, K = _shape(x, means)
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    ws = ws or Workspace(prob, x.device)
+    proba = torch.empty((B, N, K), dtype=torch.float32, device=x.device)
+    scores = torch.empty((B, N), dtype=torch.float32, device=x.device)
+    _check(_lib.gmmxx_hip_predict_proba_score(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
+                                              _ptr(proba), _ptr(scores), ws.ptr, ws.nbytes, _stream(x.device)),
+           "gmmxx_hip_predict_proba_score")
+    return proba, scores

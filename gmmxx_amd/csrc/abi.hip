@@ -6,7 +6,9 @@
 
 #include <stdint.h>
 
+#include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <algorithm>
 #include <string>
@@ -189,7 +191,9 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   // (+B: the tied EM iteration's per-batch log-likelihood shift, after the row partials)
   q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices}) + 1) * 8);
   q.o_xch = take(q.coop ? (size_t)q.cNG * kRing * q.cG * kBN * 8 : 0);
-  q.o_flags = take(q.coop ? 4 : 0);   // status word of the cooperative pass
+  // [0] status of the last cooperative pass (zeroed by its launcher), [1] sticky
+  // status since the last gmmxx_hip_take_status
+  q.o_flags = take(8);
   q.o_first = take((size_t)q.chol_m * 4 + 4);   // per-matrix first levels, then the global level
   q.o_lbuf = take(q.chol_m ? (size_t)q.chol_m * chol_dp(q.D) * chol_dp(q.D) * 4 : 0);
   q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
@@ -284,13 +288,17 @@ int run_coop(const Plan& pl, const void* x, void* ws, hipStream_t s) {
   c.ll_part = at<double>(ws, pl.o_ll);
   c.xch = at<uint64_t>(ws, pl.o_xch);
   c.status = at<unsigned>(ws, pl.o_flags);
+  // Polls per wait before the pass gives up; GMMXX_HIP_COOP_SPIN_LIMIT overrides
+  // it (a negative value gives up at the first wait: the timeout path, on demand).
   c.spin_limit = 1 << 20;
+  if (const char* sl = getenv("GMMXX_HIP_COOP_SPIN_LIMIT")) c.spin_limit = atoi(sl);
   const int rc = launch_sph_bf16_coop(pl.DP, c, s);
   if (rc == -2) return fail(GMMXX_ERR_HIP, "cooperative launch of the single-pass kernel failed");
   if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no cooperative kernel for this shape");
   return check_hip("cooperative single-pass kernel");
 }
 const unsigned* coop_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags); }
+unsigned* sticky_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags) + 1; }
 int stat_slices(const Plan& pl) { return pl.fused ? pl.fparts : (pl.coop ? pl.cspb : pl.slices); }
 // The tile-partial buffer is free once the statistics are being reduced: it is
 // the scratch of the grouped slice reduction.
@@ -369,8 +377,10 @@ int stats_pass(const Plan& pl, const void* x, void* ws, hipStream_t s) {
 
 // M-step parameter update from the statistics rows in the workspace; n_rows is
 // the row count per batch that divides N_k into the weights.
+// skip: a nonzero word there leaves the parameters unchanged (a timed-out
+// cooperative pass), or null.
 void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, double min_weight, int64_t n_rows,
-              float* means, float* covs, float* weights, hipStream_t s) {
+              float* means, float* covs, float* weights, hipStream_t s, const unsigned* skip = nullptr) {
   FinalizeArgs f{};
   f.cov = pl.cov;
   f.B = pl.B;
@@ -390,6 +400,7 @@ void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, dou
   f.means = means;
   f.covs = covs;
   f.weights = weights;
+  f.skip = skip;
   launch_finalize(f, s);
 }
 
@@ -440,6 +451,32 @@ int gmmxx_hip_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset,
   return check_hip("canary");
 }
 
+int gmmxx_hip_device_info(int device, gmmxx_dev_info* out) {
+  if (!out) return fail(GMMXX_ERR_INVALID_ARGUMENT, "out is NULL");
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+    (void)hipGetLastError();
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "no such device");
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return check_hip("hipGetDeviceProperties");
+  *out = gmmxx_dev_info{};
+  out->device = device;
+  snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+  out->supported = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+  out->compute_units = prop.multiProcessorCount;
+  out->wave_size = prop.warpSize;
+  out->clock_khz = prop.clockRate;
+  out->hbm_bytes = (int64_t)prop.totalGlobalMem;
+  out->lds_per_workgroup = (int64_t)prop.sharedMemPerBlock;
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return check_hip("hipGetDevice");
+  if (cur != device && hipSetDevice(device) != hipSuccess) return check_hip("hipSetDevice");
+  out->coop_capacity = coop_capacity();
+  if (cur != device && hipSetDevice(cur) != hipSuccess) return check_hip("hipSetDevice");
+  return GMMXX_OK;
+}
+
 int gmmxx_hip_supported(const gmmxx_problem* p) {
   Plan pl;
   const std::string saved = g_last_error;
@@ -452,6 +489,17 @@ int64_t gmmxx_hip_workspace_bytes(const gmmxx_problem* p) {
   Plan pl;
   if (plan_problem(p, &pl) != GMMXX_OK) return -1;
   return (int64_t)pl.total;
+}
+
+int gmmxx_hip_take_status(const gmmxx_problem* p, void* ws, int64_t ws_bytes, uint32_t* status_out,
+                          void* stream) {
+  Plan pl;
+  int rc = plan_problem(p, &pl);
+  if (rc) return rc;
+  if ((rc = check_ws(pl, ws, ws_bytes))) return rc;
+  if (!status_out) return fail(GMMXX_ERR_INVALID_ARGUMENT, "status_out is NULL");
+  launch_take_status(sticky_status(pl, ws), status_out, (hipStream_t)stream);
+  return check_hip("take_status");
 }
 
 int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* means, float* covs,
@@ -486,7 +534,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
           parts += pl.B;
         }
         launch_ll_reduce(at<double>(ws, pl.o_ll), parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
-        if (pl.coop) launch_coop_check(coop_status(pl, ws), lower_bound, s);
+        if (pl.coop) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), lower_bound, s);
         return check_hip("log-likelihood reduction");
       }
       CombineArgs c{};
@@ -518,7 +566,9 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
                            at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
       return check_hip("statistics reduction");
     case GMMXX_PHASE_FINALIZE:
-      finalize(pl, ws, gram, reg_covar, min_weight, pl.N, means, covs, weights, s);
+      // A cooperative pass that timed out leaves the parameters as they were.
+      finalize(pl, ws, gram, reg_covar, min_weight, pl.N, means, covs, weights, s,
+               pl.coop ? coop_status(pl, ws) : nullptr);
       return check_hip("finalize");
     default:
       return fail(GMMXX_ERR_INVALID_ARGUMENT, "unknown phase");
@@ -558,7 +608,7 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
       return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
     }
     launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0, ll_sum, s);
-    if (pl.coop) launch_coop_check(coop_status(pl, ws), ll_sum, s);
+    if (pl.coop) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), ll_sum, s);
     launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                          at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
     if ((rc = check_hip("fused statistics pass"))) return rc;
@@ -729,20 +779,33 @@ int gmmxx_hip_score(const gmmxx_problem* p, const void* x, const float* means, c
   return lse_pass(pl, x, ws, scores, labels, false, s);
 }
 
-int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
-                            const float* weights, float* proba, void* ws, int64_t ws_bytes, void* stream) {
+int gmmxx_hip_predict_proba_score(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
+                                  const float* weights, float* proba, float* scores, void* ws, int64_t ws_bytes,
+                                  void* stream) {
   Plan pl;
   int rc = begin(p, &pl, x, ws, ws_bytes);
   if (rc) return rc;
-  if (!means || !covs || !weights || !proba) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  if (!means || !covs || !weights) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL parameter buffer");
+  if (!proba && !scores) return fail(GMMXX_ERR_INVALID_ARGUMENT, "proba and scores are both NULL");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
-  if (!pl.single && (rc = lse_pass(pl, x, ws, nullptr, nullptr, false, s))) return rc;
+  if (!proba) return lse_pass(pl, x, ws, scores, nullptr, false, s);
+  // One tile pass when the workgroup holds every component (the pass forms the
+  // row log-normalisers, which are the scores); otherwise the log-normaliser
+  // pass writes the scores and the responsibility pass reads its lse.
+  if (!pl.single && (rc = lse_pass(pl, x, ws, scores, nullptr, false, s))) return rc;
   TileArgs t = tile_args(pl, x, ws);
   t.proba = proba;
+  t.scores = pl.single ? scores : nullptr;
   if (run_tile(pl, pl.single ? MODE_PROBA_LSE : MODE_PROBA, t, s) != 0)
     return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
   return check_hip("predict_proba");
+}
+
+int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* means, const float* covs,
+                            const float* weights, float* proba, void* ws, int64_t ws_bytes, void* stream) {
+  if (!proba) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL buffer");
+  return gmmxx_hip_predict_proba_score(p, x, means, covs, weights, proba, nullptr, ws, ws_bytes, stream);
 }
 
 int gmmxx_hip_gram(const gmmxx_problem* p, const void* x, float* out, void* ws, int64_t ws_bytes, void* stream) {

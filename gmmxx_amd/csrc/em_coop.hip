@@ -127,8 +127,13 @@ __global__ void coop_zero_kernel(unsigned* p, int n, unsigned* status) {
   if (i == n) *status = 0u;
 }
 
-__global__ void coop_check_kernel(const unsigned* status, float* value) {
-  if (threadIdx.x == 0 && *status != 0u) *value = __builtin_nanf("");
+// After a pass: a timed-out wait turns *value into NaN and is added to the
+// sticky status word, which gmmxx_hip_take_status reads and clears.
+__global__ void coop_check_kernel(const unsigned* status, unsigned* sticky, float* value) {
+  if (threadIdx.x == 0 && *status != 0u) {
+    *value = __builtin_nanf("");
+    *sticky |= *status;
+  }
 }
 
 }  // namespace
@@ -184,12 +189,14 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
   const int kbase = mem * (kNW * kCW) + __builtin_amdgcn_readfirstlane(wave) * kCW;
   uint64_t* const gxch = a.xch + (size_t)grp * kRing * G * kBN;
 
-  // Constant augmented columns 8..31 of every staged row: [1 0 0 ...].
+  // Constant augmented columns 8..31 of every staged row: [1 0 0 ...]; the
+  // e slots start at zero, so no LDS word is read before it is written.
   for (int i = tid; i < kNB * kBN * 3; i += NTHR) {
     const int row = i / 3, ch = 1 + i % 3;
     const uint4 w = make_uint4(ch == 1 ? pack2((__bf16)1.f, (__bf16)0.f) : 0u, 0u, 0u, 0u);
     *reinterpret_cast<uint4*>(xs + row * XS + DP + 8 * ch) = w;
   }
+  for (int i = tid; i < kNW * 2 * kCT * 2 * 64; i += NTHR) es[i] = make_uint2(0u, 0u);
 
   bf16x8 whi[kCT][ECH], wlo[kCT][ECH], waug[kCT];
   f32x4 acc[kCT][JT];
@@ -465,8 +472,10 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
             }
             return ok;
           };
+          // A negative spin limit gives up at the first wait (the host's way to
+          // exercise the timeout path without a stalled partner).
           int spins = 0;
-          while (!dead && __ballot(!ready()) != 0) {
+          while (!dead && (a.spin_limit < 0 || __ballot(!ready()) != 0)) {
             if (++spins > a.spin_limit ||
                 ((spins & 63) == 0 && __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
               dead = true;
@@ -513,8 +522,10 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       step(T_{}, T_{}, P1{}, i + 1);
     }
     if (i < nblk) { step(T_{}, T_{}, P0{}, i); ++i; }
-    // drain: the last two blocks are finished (i = nblk, nblk + 1)
-    if (i & 1) { step(T_{}, F_{}, P1{}, i); step(T_{}, F_{}, P0{}, i + 1); }
+    // drain: the last two blocks are finished (i = nblk, nblk + 1); an item of
+    // one block has only block 0 left (i = 2), and block 1 was never staged.
+    if (nblk == 1) step(T_{}, F_{}, P0{}, 2);
+    else if (i & 1) { step(T_{}, F_{}, P1{}, i); step(T_{}, F_{}, P0{}, i + 1); }
     else { step(T_{}, F_{}, P0{}, i); step(T_{}, F_{}, P1{}, i + 1); }
     seq += (unsigned)nblk;
 
@@ -559,8 +570,8 @@ int coop_capacity() {
   return cache[dev];
 }
 
-void launch_coop_check(const unsigned* status, float* value, hipStream_t s) {
-  coop_check_kernel<<<1, 64, 0, s>>>(status, value);
+void launch_coop_check(const unsigned* status, unsigned* sticky, float* value, hipStream_t s) {
+  coop_check_kernel<<<1, 64, 0, s>>>(status, sticky, value);
 }
 
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s) {

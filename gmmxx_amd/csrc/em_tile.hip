@@ -720,6 +720,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
           const float l = M + __log2f(S);
           lsw[wave * kBN + lane] = valid ? l : INFINITY;
           if (wave == 0 && valid) ll_acc += (double)l;
+          // predict_proba with score_samples: the row's log-normaliser is the score
+          if constexpr (MODE == MODE_PROBA_LSE)
+            if (wave == 0 && valid && a.scores) a.scores[(size_t)b * N + n0 + lane] = l * kLn2;
         }
         // The wave's own LDS writes above are read back by its other lanes below.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

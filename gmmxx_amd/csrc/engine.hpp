@@ -24,6 +24,7 @@ struct TileArgs {
   int* part_idx;               // [ktiles][B][N] first argmax           (LSE)
   float* part_stats;           // [slices][B][K][JP]                    (STATS)
   float* proba;                // [B][N][K]                             (PROBA)
+  float* scores;               // [B][N] natural-log row log-normalisers (PROBA_LSE, or null)
   int nslices;                 // row slices of the fused kernel
   double* ll_part;             // [B][nslices] partial log-likelihood   (fused)
   int raw_logits;              // PROBA: write the log2-domain logits instead of responsibilities
@@ -80,8 +81,9 @@ struct CoopArgs {
 // Resident workgroups of the cooperative kernel on the current device.
 int coop_capacity();
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s);
-// *value = NaN when the cooperative pass reported a timed-out wait (status != 0).
-void launch_coop_check(const unsigned* status, float* value, hipStream_t s);
+// *value = NaN when the cooperative pass reported a timed-out wait (status != 0),
+// and *sticky |= status.
+void launch_coop_check(const unsigned* status, unsigned* sticky, float* value, hipStream_t s);
 
 // Greedy k-means++ seeding (kmeans.hip).  Row sample [B][S][D] fp32; the first
 // centre's row index per batch and T uniform draws per later centre are inputs.

@@ -586,6 +586,7 @@ __global__ __launch_bounds__(64 * kRedWaves) void reduce_slices_kernel(const flo
 
 __global__ void finalize_kernel(FinalizeArgs a) {
   __shared__ float scratch[32];
+  if (a.skip && *a.skip != 0u) return;   // uniform across the launch
   const int b = blockIdx.y;
   const int K = a.K, D = a.D, JP = a.JP;
   const float* st = a.stats + (size_t)b * K * JP;
@@ -631,7 +632,7 @@ __global__ void finalize_kernel(FinalizeArgs a) {
 __global__ void finalize_tied_kernel(FinalizeArgs a) {
   const int b = blockIdx.y, d = blockIdx.x, e = threadIdx.x;
   const int K = a.K, D = a.D, JP = a.JP;
-  if (e >= D) return;
+  if (e >= D || (a.skip && *a.skip != 0u)) return;
   const float* st = a.stats + (size_t)b * K * JP + a.nk_col;
   const float* mu = a.means + (size_t)b * K * D;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
@@ -655,7 +656,7 @@ __global__ void finalize_full_kernel(FinalizeArgs a) {
   const int b = blockIdx.y, k = blockIdx.x;
   const int K = a.K, D = a.D, JP = a.JP, DP = a.DP;
   const int t = threadIdx.x;
-  if (t >= D * D) return;
+  if (t >= D * D || (a.skip && *a.skip != 0u)) return;
   const int d = t / D, e = t % D;
   const size_t bk = (size_t)b * K + k;
   const float* sk = a.stats + bk * JP;
@@ -861,6 +862,17 @@ void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, 
   groups = (slices + per - 1) / per;  // every group non-empty
   reduce_slices_kernel<<<dim3((unsigned)blocks, groups), 64 * kRedWaves, 0, s>>>(part, slices, M, tmp, per);
   reduce_slices_kernel<<<(unsigned)blocks, 64 * kRedWaves, 0, s>>>(tmp, groups, M, out, groups);
+}
+
+__global__ void take_status_kernel(unsigned* sticky, uint32_t* out) {
+  if (threadIdx.x == 0) {
+    *out = *sticky;
+    *sticky = 0u;
+  }
+}
+
+void launch_take_status(unsigned* sticky, uint32_t* out, hipStream_t s) {
+  take_status_kernel<<<1, 64, 0, s>>>(sticky, out);
 }
 
 void launch_finalize(const FinalizeArgs& a, hipStream_t s) {

@@ -46,6 +46,7 @@ struct FinalizeArgs {
   float* means;
   float* covs;
   float* weights;
+  const unsigned* skip;    // nonzero *skip: leave the parameters unchanged (or null)
 };
 
 struct UnpackArgs {
@@ -92,6 +93,8 @@ void launch_unpack(const UnpackArgs& a, int B, hipStream_t s);
 void launch_pack(const PackArgs& a, int B, hipStream_t s);
 void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
                  hipStream_t s);
+// *out = *sticky; *sticky = 0.
+void launch_take_status(unsigned* sticky, uint32_t* out, hipStream_t s);
 void launch_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, hipStream_t s);
 
 }  // namespace gx

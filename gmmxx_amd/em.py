@@ -6,9 +6,16 @@ return tuple ``(labels, means, covariances, weights, info)``.  Every EM
 iteration is one call of ``gmmxx_hip_em_step`` on the current stream; with
 ``tol == 0`` and ``verbose=False`` nothing synchronises until the loop ends.
 
-Semantics follow the reference's soft EM on fp32 data: bf16 input (spherical
-only) is kept in bf16 in HBM and computed with fp32 accumulation, i.e. it
-equals the fp32 algorithm on the bf16-rounded values.  Parameters are fp32.
+Semantics follow the reference's soft EM.  fp32 input runs the fp32 algorithm
+(every product fp32-accurate).  bf16 input (spherical only) stays bf16 in HBM
+and is computed by the bf16 engine: exact bf16 x against a hi + lo bf16 split
+of each component's fp32 E-step operand (about 16 significand bits) with fp32
+accumulation, and the responsibilities rounded to bf16 before the M-step
+product -- more accurate than the reference's bf16 arithmetic on the same
+input, but not the fp32 algorithm (the bf16 bar is 2e-3 on the
+log-likelihood).  The estimator upcasts half-precision input to fp32 unless
+``dtype=torch.bfloat16`` is given, as the reference does.  Parameters are
+fp32.
 """
 
 from __future__ import annotations
@@ -216,10 +223,18 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         init_params: str = "kmeans", reg_covar: float = 1e-6, min_weight: float = 1e-8,
         compute_labels: bool = True, generator: Optional[torch.Generator] = None,
         approx_top_k: Optional[int] = None, kmeans_init_iters: int = 10, kmeans_init_tol: float = 1e-4,
+        record_all_lower_bounds: bool = False,
         ) -> Tuple[Optional[torch.Tensor], torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, object]]:
     """Soft EM on the HIP engine; see the module docstring.  ``approx_top_k``
     (1 <= k < K) restricts each row's responsibilities to its k largest logits,
-    renormalised over them, as the reference's approximate EM does."""
+    renormalised over them, as the reference's approximate EM does.
+
+    ``lower_bound_history`` follows the reference's bookkeeping: for diag, tied
+    and full with ``tol == 0`` and ``verbose=False`` only the last iteration's
+    lower bound is recorded and the others are 0.0
+    (gmmxx/torch_fallback.py:2484-2485, :2668-2679, :3169-3180); spherical
+    records every iteration.  ``record_all_lower_bounds=True`` records every
+    iteration for every type (the engine computes them all anyway)."""
     if covariance_type not in _COVS:
         raise ValueError("covariance_type must be 'spherical', 'diag', 'tied' or 'full'")
     if n_components <= 0:
@@ -280,7 +295,13 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
                 break
             if tol > 0.0:
                 prev = value
+    if ws is not None:
+        # A cooperative pass that gave up waiting left its iteration's parameters
+        # unchanged and a NaN lower bound; the fit reports it instead of returning.
+        _hip.raise_on_status(_hip.take_status(ws), "EM fit")
     history = [float(v) for v in lb[:n_iter].tolist()]
+    if not (spherical or tol > 0.0 or verbose or record_all_lower_bounds):
+        history = [0.0] * (n_iter - 1) + history[-1:]
     labels = None
     if compute_labels:
         _, labels = _hip.score(covariance_type, x, means, covs, weights, want_scores=False, ws=ws)
@@ -305,7 +326,7 @@ def _api(covariance_type):
     def run(x, n_components, max_iters=100, tol=1e-4, init_means=None, init_variances=None,
             init_weights=None, verbose=False, *, init_params="kmeans", reg_covar=1e-6,
             min_weight=1e-8, compute_labels=True, generator=None, approx_top_k=None, kmeans_init_iters=10,
-            kmeans_init_tol=1e-4, **unused):
+            kmeans_init_tol=1e-4, record_all_lower_bounds=False, **unused):
         for key in unused:
             if key not in {"chunk_size_N", "chunk_size_K", "kmeans_use_triton", "gmm_use_triton",
                            "gmm_use_triton_estep", "gmm_use_triton_streaming_update"}:
@@ -314,7 +335,8 @@ def _api(covariance_type):
                    init_covs=init_variances, init_weights=init_weights, verbose=verbose,
                    init_params=init_params, reg_covar=reg_covar, min_weight=min_weight,
                    compute_labels=compute_labels, generator=generator, approx_top_k=approx_top_k,
-                   kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol)
+                   kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol,
+                   record_all_lower_bounds=record_all_lower_bounds)
     run.__name__ = f"batch_gmm_{covariance_type.capitalize()}_hip"
     run.__doc__ = (f"{covariance_type} soft EM on the HIP engine; signature and return value of "
                    f"the reference's batch_gmm_*_torch_native (chunk/Triton knobs are accepted and ignored).")

@@ -14,9 +14,12 @@ call goes to ``libgmmxx_hip.so``; there is no CPU or PyTorch fallback (see
 Input handling follows the reference: ``(N, D)`` or ``(B, N, D)`` floating
 point tensors, fitted attributes squeezed when the input was unbatched
 (:322-325, :401-424), half-precision inputs computed in fp32 unless ``dtype=``
-says otherwise (:426-433).  bf16 spherical input stays bf16 in HBM: the engine
-multiplies the exact bf16 values with fp32 accumulation, which is the fp32
-algorithm on the same values.
+says otherwise (:426-433): bf16/fp16 input runs the fp32 algorithm.  With
+``dtype=torch.bfloat16`` spherical input stays bf16 in HBM and runs the bf16
+engine (exact bf16 x against a hi + lo bf16 split of the fp32 component
+operands, fp32 accumulation, responsibilities rounded to bf16 before the
+M-step product): more accurate than the reference's bf16 arithmetic, held to
+the bf16 bar (2e-3 on the log-likelihood), not to the fp32 one.
 """
 
 from __future__ import annotations
@@ -24,6 +27,7 @@ from __future__ import annotations
 import contextlib
 import math
 import warnings
+import weakref
 from typing import Any, Optional
 
 import torch
@@ -79,8 +83,9 @@ class GMMXX:
 
     ``covariance_type`` is ``spherical``, ``diag``/``diagonal``, ``tied`` or
     ``full``.  Supported shapes: D <= 128 (spherical, diag), D <= 64 (tied),
-    D <= 16 (full); any N, K <= 65536, B <= 65535.  bf16 input is kept in bf16
-    for spherical.  ``approx_top_k`` (1 <= k < K) opts into the reference's
+    D <= 16 (full); any N, K <= 65536, B <= 65535.  Half-precision input is
+    computed in fp32 unless ``dtype=torch.bfloat16`` (spherical: the bf16
+    engine).  ``approx_top_k`` (1 <= k < K) opts into the reference's
     approximate EM: each row's responsibilities cover only its k largest
     logits; prediction stays exact.
     """
@@ -187,6 +192,7 @@ class GMMXX:
         self.last_fallback_reason_: Optional[str] = None
         self.last_backend_used_: Optional[str] = None
         self._batch_size: Optional[int] = None
+        self._scores_cache = None
 
     def _squeeze_if_unbatched(self, value: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
         if value is None:
@@ -239,22 +245,22 @@ class GMMXX:
             return self.dtype
         return torch.float32 if x_b.dtype in (torch.float16, torch.bfloat16) else x_b.dtype
 
-    def _engine_tensor(self, x_b: torch.Tensor) -> torch.Tensor:
-        """x on the estimator's GPU in the dtype the engine reads: fp32, or
-        bf16 kept as is for spherical when no explicit dtype asks otherwise."""
-        if self.device.type != "cuda":
-            raise _hip.HipBackendUnavailable(
-                f"the hip backend runs on a ROCm GPU; estimator device is {self.device}")
+    def _engine_dtype(self, x_b: torch.Tensor) -> torch.dtype:
         compute = self._compute_dtype_for_input(x_b)
         if compute == torch.float64:
             raise TypeError("float64 data is not supported by the hip backend; pass dtype=torch.float32")
-        if x_b.dtype == torch.bfloat16 and self.dtype is None and self.covariance_type == "spherical":
-            target = torch.bfloat16
-        elif compute == torch.bfloat16 and self.covariance_type == "spherical":
-            target = torch.bfloat16
-        else:
-            target = torch.float32
-        return x_b.to(device=self.device, dtype=target).contiguous()
+        return torch.bfloat16 if (compute == torch.bfloat16 and self.covariance_type == "spherical") else torch.float32
+
+    def _engine_tensor(self, x_b: torch.Tensor) -> torch.Tensor:
+        """x on the estimator's GPU in the dtype the engine reads: fp32 (the
+        reference's compute dtype for float32 and half-precision input,
+        gmmxx/interface.py:426-433), or bf16 for spherical when
+        ``dtype=torch.bfloat16`` asks for it.  Other covariance types have no
+        bf16 engine and compute an explicit bf16 dtype in fp32."""
+        if self.device.type != "cuda":
+            raise _hip.HipBackendUnavailable(
+                f"the hip backend runs on a ROCm GPU; estimator device is {self.device}")
+        return x_b.to(device=self.device, dtype=self._engine_dtype(x_b)).contiguous()
 
     def _is_large_cpu_stream_input(self, x_b: torch.Tensor) -> bool:
         """Host data longer than chunk_size_data_cpu rows streams through HBM in
@@ -283,13 +289,13 @@ class GMMXX:
         if streaming:
             # gmmxx/interface.py:452-490: host data streams through HBM (B = 1).
             self.last_backend_used_ = self._resolve(x_b, self.k)
-            x_host = x_b if self.dtype is None else x_b.to(self.dtype)
+            x_host = x_b
             labels_b, means_b, covs_b, weights_b, info = large_n.fit_large_n(
                 x_host, self.k, self.covariance_type, device=self.device, max_iters=self.niter, tol=self.tol,
                 verbose=self.verbose, init_params=self.init_params, reg_covar=self.reg_covar,
                 chunk_size_N=self.chunk_size_data_cpu, compute_labels=self.compute_labels_on_fit,
                 seed=self.seed, approx_top_k=self.approx_top_k, kmeans_init_iters=self.init_kmeans_iters,
-                kmeans_init_tol=self.init_kmeans_tol)
+                kmeans_init_tol=self.init_kmeans_tol, compute_dtype=self._engine_dtype(x_b))
         else:
             x_b = self._engine_tensor(x_b)
             self.last_backend_used_ = self._resolve(x_b, self.k)
@@ -416,7 +422,8 @@ class GMMXX:
                              f"but received B={batch_size}.")
         self.last_backend_used_ = self._resolve(x_b, int(self.means_b.shape[1]))
         if self._is_large_cpu_stream_input(x_b):
-            return (x_b if self.dtype is None else x_b.to(self.dtype)), batch_size, True
+            self._engine_dtype(x_b)   # rejects float64 as the in-memory path does
+            return x_b, batch_size, True
         return self._engine_tensor(x_b), batch_size, False
 
     def _params(self):
@@ -429,31 +436,61 @@ class GMMXX:
             means, covs, weights = self._params()
             if streamed:
                 labels = large_n.predict_large_n(x_b, means, covs, weights, self.covariance_type,
+                    compute_dtype=self._engine_dtype(x_b),
                                                  device=self.device, chunk_size_N=self.chunk_size_data_cpu)
             else:
                 _, labels = _hip.score(self.covariance_type, x_b, means, covs, weights, want_scores=False)
             return labels.squeeze(0) if batch_size is None else labels
 
+    def _cache_scores(self, data: torch.Tensor, scores: torch.Tensor) -> None:
+        """Keeps the per-sample scores that predict_proba computed on ``data``
+        (the same E-step gives both), for a score_samples call on the same,
+        unmodified tensor under the same fitted parameters."""
+        try:
+            self._scores_cache = (weakref.ref(data), data._version, self._param_versions(), scores)
+        except TypeError:
+            self._scores_cache = None
+
+    def _param_versions(self):
+        return tuple((id(t), t._version) for t in (self.means_b, self.variances_b, self.weights_b))
+
+    def _cached_scores(self, data: torch.Tensor) -> Optional[torch.Tensor]:
+        c = self._scores_cache
+        if (c is None or not torch.is_tensor(data) or c[0]() is not data or c[1] != data._version
+                or c[2] != self._param_versions()):
+            return None
+        self._scores_cache = None
+        return c[3]
+
     def predict_proba(self, data: torch.Tensor) -> torch.Tensor:
-        """Responsibilities (B, N, K) fp32 (gmmxx/interface.py:1973-2268)."""
+        """Responsibilities (B, N, K) fp32 (gmmxx/interface.py:1973-2268).  The
+        per-sample scores come out of the same E-step
+        (gmmxx_hip_predict_proba_score) and serve a following score_samples
+        call on the same tensor."""
         with self._matmul_precision_scope():
             x_b, batch_size, streamed = self._prepare_predict_input(data)
             means, covs, weights = self._params()
             if streamed:
                 probs = large_n.predict_proba_large_n(x_b, means, covs, weights, self.covariance_type,
+                    compute_dtype=self._engine_dtype(x_b),
                                                       device=self.device, chunk_size_N=self.chunk_size_data_cpu)
             else:
-                probs = _hip.predict_proba(self.covariance_type, x_b, means, covs, weights)
+                probs, scores = _hip.predict_proba_score(self.covariance_type, x_b, means, covs, weights)
+                self._cache_scores(data, scores.squeeze(0) if batch_size is None else scores)
             return probs.squeeze(0) if batch_size is None else probs
 
     def score_samples(self, data: torch.Tensor) -> torch.Tensor:
         """Per-sample log-likelihood log Σ_k w_k N(x | μ_k, Σ_k), fp32
         (gmmxx/interface.py:2270-2521)."""
+        cached = self._cached_scores(data)
+        if cached is not None:
+            return cached
         with self._matmul_precision_scope():
             x_b, batch_size, streamed = self._prepare_predict_input(data)
             means, covs, weights = self._params()
             if streamed:
                 scores = large_n.score_samples_large_n(x_b, means, covs, weights, self.covariance_type,
+                    compute_dtype=self._engine_dtype(x_b),
                                                        device=self.device, chunk_size_N=self.chunk_size_data_cpu)
             else:
                 scores, _ = _hip.score(self.covariance_type, x_b, means, covs, weights, want_labels=False)

@@ -37,7 +37,12 @@ from . import _hip, em
 _COVS = ("spherical", "diag", "tied", "full")
 
 
-def _engine_dtype(x_cpu: torch.Tensor, covariance_type: str) -> torch.dtype:
+def _engine_dtype(x_cpu: torch.Tensor, covariance_type: str, requested: Optional[torch.dtype] = None) -> torch.dtype:
+    """bf16 (the bf16 engine) for spherical when requested, or by default for bf16
+    input at the function level; fp32 otherwise.  The estimator passes its compute
+    dtype, which is fp32 for half-precision input unless dtype= says otherwise."""
+    if requested is not None:
+        return torch.bfloat16 if (requested == torch.bfloat16 and covariance_type == "spherical") else torch.float32
     if x_cpu.dtype == torch.bfloat16 and covariance_type == "spherical":
         return torch.bfloat16
     return torch.float32
@@ -168,11 +173,13 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
                 chunk_size_N: int = 1 << 20, min_weight: float = 1e-8, compute_labels: bool = True,
                 max_init_samples: int = 65536, init_means=None, init_covs=None, init_weights=None,
                 seed: int = 0, approx_top_k: Optional[int] = None, kmeans_init_iters: int = 10,
-                kmeans_init_tol: float = 1e-4):
+                kmeans_init_tol: float = 1e-4, compute_dtype: Optional[torch.dtype] = None):
     """Soft EM with x (1, N, D) in host memory; returns (labels, means, covariances,
     weights, info) like gmmxx/large_n.py:866-1595 (labels on the host).
     ``approx_top_k`` selects the approximate top-k E-step per chunk, as the
-    reference's streamed loop does (gmmxx/large_n.py:1325-1370)."""
+    reference's streamed loop does (gmmxx/large_n.py:1325-1370).  ``compute_dtype``
+    (fp32, or bf16 for the spherical bf16 engine) defaults to bf16 for bf16
+    spherical input and fp32 otherwise."""
     device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     if covariance_type not in _COVS:
         raise ValueError("covariance_type must be 'spherical', 'diag', 'tied', or 'full'")
@@ -186,7 +193,7 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
         raise ValueError("min_weight must be positive")
     _validate(x_cpu, device)
     _hip.require_hip()
-    dtype = _engine_dtype(x_cpu, covariance_type)
+    dtype = _engine_dtype(x_cpu, covariance_type, compute_dtype)
     n, d = int(x_cpu.shape[1]), int(x_cpu.shape[2])
     if init_means is not None:
         sample = x_cpu[:, : min(n, max(4096, int(max_init_samples)))].to(device=device, dtype=dtype)
@@ -242,6 +249,9 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
                 if sq is not None:
                     sq += c_sq
                 ll += c_ll[0].double()
+        if top_k is None:   # a timed-out cooperative chunk pass: raise before its statistics are used
+            for ws in wss.cache.values():
+                _hip.raise_on_status(_hip.take_status(ws), "streamed EM fit")
         _hip.finalize_stats(covariance_type, nk, sx, sq, means, covs, weights, n, gram_xx=gram,
                             reg_covar=reg_covar, min_weight=min_weight, ws=fin_ws)
         value = float(ll.item()) / float(n)
@@ -281,11 +291,11 @@ def _params(means, covs, weights, device):
     return tuple(t.detach().to(device=device, dtype=torch.float32).contiguous() for t in (means, covs, weights))
 
 
-def _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, what):
+def _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, what, compute_dtype=None):
     device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     _validate(x_cpu, device)
     _hip.require_hip()
-    dtype = _engine_dtype(x_cpu, covariance_type)
+    dtype = _engine_dtype(x_cpu, covariance_type, compute_dtype)
     means, covs, weights = _params(means, covs, weights, device)
     n, d, k = int(x_cpu.shape[1]), int(x_cpu.shape[2]), int(means.shape[1])
     stream = ChunkStream(x_cpu, device, dtype, chunk_size_N)
@@ -304,16 +314,19 @@ def _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, w
     return out
 
 
-def predict_large_n(x_cpu, means, covs, weights, covariance_type, *, device=None, chunk_size_N=1 << 20):
+def predict_large_n(x_cpu, means, covs, weights, covariance_type, *, device=None, chunk_size_N=1 << 20,
+                    compute_dtype=None):
     """First-max labels (1, N) int64 on the host (gmmxx/large_n.py:1907-2076)."""
-    return _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, "labels")
+    return _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, "labels", compute_dtype)
 
 
-def score_samples_large_n(x_cpu, means, covs, weights, covariance_type, *, device=None, chunk_size_N=1 << 20):
+def score_samples_large_n(x_cpu, means, covs, weights, covariance_type, *, device=None, chunk_size_N=1 << 20,
+                          compute_dtype=None):
     """Per-sample log-likelihood (1, N) fp32 on the host (gmmxx/large_n.py:2078-2257)."""
-    return _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, "scores")
+    return _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, "scores", compute_dtype)
 
 
-def predict_proba_large_n(x_cpu, means, covs, weights, covariance_type, *, device=None, chunk_size_N=1 << 20):
+def predict_proba_large_n(x_cpu, means, covs, weights, covariance_type, *, device=None, chunk_size_N=1 << 20,
+                          compute_dtype=None):
     """Responsibilities (1, N, K) fp32 on the host (gmmxx/large_n.py:2259-2502)."""
-    return _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, "proba")
+    return _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, "proba", compute_dtype)

@@ -53,6 +53,25 @@ const char* gmmxx_hip_last_error(void);
  * Replaces `canary_add_offset` (gmmxx/csrc/canary/canary.cu:21-48, gmmxx/_cuda.py:67-95). */
 int gmmxx_hip_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, void* stream);
 
+/* Properties of device `device` as the engine sees them.  `supported` is 1 for
+ * gfx950 (the only target the library is built for); `coop_capacity` is the
+ * number of co-resident workgroups of the single-pass cooperative kernel.
+ * Replaces the device checks of the reference's runtime gates and
+ * require_cuda / has_cuda (gmmxx/_runtime.py:31-191, gmmxx/_cuda.py:44-64),
+ * which probe torch.cuda.get_device_capability. */
+typedef struct gmmxx_dev_info {
+  int32_t device;
+  int32_t supported;          /* 1: gfx950 */
+  char arch[64];              /* e.g. "gfx950:sramecc+:xnack-" */
+  int32_t compute_units;
+  int32_t wave_size;
+  int32_t clock_khz;
+  int32_t coop_capacity;
+  int64_t hbm_bytes;
+  int64_t lds_per_workgroup;
+} gmmxx_dev_info;
+int gmmxx_hip_device_info(int device, gmmxx_dev_info* out);
+
 /* 1 if the engine supports the problem shape/dtype, else 0.
  * Replaces the shape gates cuda_{spherical,diag,tied,full}_supported
  * (gmmxx/_runtime.py:31-191). */
@@ -76,6 +95,19 @@ int64_t gmmxx_hip_workspace_bytes(const gmmxx_problem* p);
 int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float* covariances,
                       float* weights, const float* gram, double reg_covar, double min_weight,
                       float* lower_bound, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Asynchronous failures of earlier calls on this workspace: the word is nonzero
+ * when a single-pass cooperative launch (spherical bf16 at D = 128,
+ * 256 < K <= 1024) gave up waiting for a partner workgroup.  Such an iteration
+ * writes NaN to its lower bound (or ll_sum) and leaves the parameters
+ * unchanged.  Copies the word into *status_out (device memory, 1 uint32) and
+ * clears it, stream-ordered.  A newly allocated workspace holds arbitrary
+ * bytes: zero it, or call this once and discard the result, before the calls
+ * whose status is wanted.  No reference counterpart: the reference's kernels
+ * report errors synchronously through TORCH_CHECK (gmmxx/_cuda.py:41-54); this
+ * is how the asynchronous C ABI reports its one asynchronous failure. */
+int gmmxx_hip_take_status(const gmmxx_problem* p, void* workspace, int64_t workspace_bytes,
+                          uint32_t* status_out, void* stream);
 
 /* The six phases of gmmxx_hip_em_step, for callers that time or interleave
  * them; gmmxx_hip_em_step(...) == phases PREPARE..FINALIZE in order with the
@@ -165,6 +197,19 @@ int gmmxx_hip_score(const gmmxx_problem* p, const void* x, const float* means,
 int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* means,
                             const float* covariances, const float* weights, float* proba,
                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/* predict_proba and score_samples from one E-step: responsibilities (B, N, K)
+ * and per-sample log-likelihood (B, N), either may be NULL (not both).  When
+ * every component fits one tile workgroup the single responsibility pass forms
+ * the row log-normalisers itself and writes them as the scores; otherwise the
+ * log-normaliser pass writes the scores and the responsibility pass reuses its
+ * log-normalisers.  Replaces the estimator's predict_proba + score_samples pair
+ * (gmmxx/interface.py:2138-2203, :2412-2467), each of which runs its own
+ * streamed log-normaliser (gmmxx/torch_fallback.py:1279-1345, :1094-1130), and
+ * the survey's fused full_proba_score. */
+int gmmxx_hip_predict_proba_score(const gmmxx_problem* p, const void* x, const float* means,
+                                  const float* covariances, const float* weights, float* proba,
+                                  float* scores, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* XᵀX per batch (B, D, D) fp32, the fit-constant of the tied M-step
  * (gmmxx/torch_fallback.py:2856-2862). */

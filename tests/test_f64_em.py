@@ -1,0 +1,55 @@
+"""The float64 EM helper (tests/f64_em.py) agrees with the fp32 oracle on
+well-conditioned problems, so it can serve as the truth for drifting fp32
+trajectories.  CPU only."""
+
+import pytest
+import torch
+
+from oracle import torch_ref
+from oracle import f64_em
+
+
+def _problem(cov, b, n, d, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    centers = (torch.rand((b, k, d), generator=g) * 2 - 1) * 4.0
+    lab = torch.randint(0, k, (b, n), generator=g)
+    x = torch.gather(centers, 1, lab[..., None].expand(-1, -1, d)) + torch.randn((b, n, d), generator=g)
+    means = centers + 0.3 * torch.randn((b, k, d), generator=g)
+    if cov == "spherical":
+        covs = torch.rand((b, k), generator=g) + 0.5
+    elif cov == "diag":
+        covs = torch.rand((b, k, d), generator=g) + 0.5
+    else:
+        shape = (b, d, d) if cov == "tied" else (b, k, d, d)
+        a = torch.randn(shape, generator=g) * 0.3
+        covs = a @ a.transpose(-1, -2) + 0.7 * torch.eye(d)
+    w = torch.rand((b, k), generator=g) + 0.2
+    return x, means, covs, w / w.sum(-1, keepdim=True)
+
+
+@pytest.mark.parametrize("cov", ["spherical", "diag", "tied", "full"])
+def test_f64_step_matches_oracle(cov):
+    x, means, covs, w = _problem(cov, 2, 3000, 6, 5, seed=71)
+    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, cov, means, covs, w)
+    m, c, wt, lb = f64_em.em_step(x, cov, means, covs, w)
+    assert lb == pytest.approx(e_lb, rel=1e-6)
+    torch.testing.assert_close(m.float(), e_m, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(c.float(), e_c, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(wt.float(), e_w, rtol=1e-5, atol=1e-7)
+
+
+def test_judge_flags_a_planted_error():
+    """The arbiter accepts a value outside the bar only when the float64 truth
+    sides with it: an error planted in a copy of the oracle's result is flagged."""
+    from oracle import judge
+    x, means, covs, w = _problem("diag", 1, 2000, 4, 3, seed=72)
+    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "diag", means, covs, w)
+    m64, c64, w64, lb64 = f64_em.em_step(x, "diag", means, covs, w)
+    planted = e_m.clone()
+    planted[0, 1, 2] += 1e-2
+    res = judge.judge_params(planted, e_m, "means", x, False, lambda: m64)
+    assert res["outside_bar"] == 1 and res["unexplained"] == 1
+    # the float64 value itself passes against the oracle's (it is the truth)
+    assert judge.judge_params(m64.float(), e_m, "means", x, False, lambda: m64)["unexplained"] == 0
+    res = judge.judge_ll([e_lb * (1 + 1e-3)], [e_lb], 1e-5, lambda: [lb64])
+    assert res["unexplained"] == 1

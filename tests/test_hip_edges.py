@@ -44,7 +44,8 @@ def test_few_rows(hip, cov, n):
 def test_single_component(hip, cov):
     """K = 1: every responsibility is 1 and the M-step gives the sample moments."""
     x, means, covs, w = make_problem(cov, 2, 3000, 5, 1, seed=62)
-    _, m, c, wt, info = em.fit(to_dev(x), 1, cov, max_iters=3, tol=0.0, init_means=means, init_covs=covs,
+    _, m, c, wt, info = em.fit(to_dev(x), 1, cov, max_iters=3, tol=0.0, record_all_lower_bounds=True,
+                               init_means=means, init_covs=covs,
                                init_weights=w, compute_labels=False)
     _, e_m, e_c, e_w, e_info = torch_ref.fit(x, 1, cov, max_iters=3, tol=0.0, init_means=means,
                                              init_covs=covs, init_weights=w, compute_labels=False)

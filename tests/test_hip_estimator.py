@@ -50,8 +50,11 @@ def test_fit_matches_oracle(cov, b, n, d, k):
     est.fit(data.to(DEV))
     assert est.last_backend_used_ == "hip"
     m0, c0, w0 = estimator_init(x.to(DEV), cov, k, 7)
+    # reference bookkeeping of lower_bound_history_ (0.0 before the last
+    # iteration for diag/tied/full with tol = 0)
     labels, means, covs, weights, info = torch_ref.fit(
-        x, k, cov, max_iters=4, tol=0.0, init_means=m0, init_covs=c0, init_weights=w0)
+        x, k, cov, max_iters=4, tol=0.0, init_means=m0, init_covs=c0, init_weights=w0,
+        record_all_lower_bounds=False)
     sq = (lambda t: t[0]) if b == 1 else (lambda t: t)
     assert est.means_.shape == sq(means).shape
     torch.testing.assert_close(est.means_.cpu(), sq(means), rtol=1e-4, atol=1e-4)
@@ -76,16 +79,47 @@ def test_fit_matches_oracle(cov, b, n, d, k):
     torch.testing.assert_close(est.score_samples(datat).cpu(), sq(ref_scores), rtol=1e-5, atol=1e-4)
     assert torch.equal(est.predict(datat).cpu(), sq(ref_labels))
     torch.testing.assert_close(est.predict_proba(datat).cpu(), sq(ref_proba), rtol=1e-4, atol=1e-5)
+    # score_samples right after predict_proba on the same tensor reuses that E-step's scores
+    torch.testing.assert_close(est.score_samples(datat).cpu(), sq(ref_scores), rtol=1e-5, atol=1e-4)
+    est.predict_proba(datat)
+    datat.mul_(1.5)                       # an in-place change invalidates the kept scores
+    torch.testing.assert_close(est.score_samples(datat).cpu(),
+                               sq(torch_ref.score_samples(xt * 1.5, fm, fc, fw, cov)), rtol=1e-5, atol=1e-4)
+    datat.div_(1.5)
     assert math.isclose(est.score(datat), float(ref_scores.mean()), rel_tol=1e-5)
     n_par = est._n_parameters(b)
     bic = -2.0 * float(ref_scores.double().sum()) + n_par * math.log(b * 3000)
     assert math.isclose(est.bic(datat), bic, rel_tol=1e-5)
 
 
-def test_bf16_spherical_keeps_bf16_and_matches_fp32_values():
+@pytest.mark.parametrize("cov", ["spherical", "diag"])
+def test_bf16_input_computes_in_fp32_by_default(cov):
+    """Half-precision input without dtype= is computed in fp32, as the
+    reference's estimator does (gmmxx/interface.py:426-433): the fit must match
+    the oracle's fp32 fit on the same (bf16-representable) values to the fp32
+    bars -- lower bounds rtol 1e-5, parameters rtol 1e-4."""
     x = blobs(1, 8192, 32, 8, seed=3)[0].to(torch.bfloat16)
-    est = GMMXX(k=8, max_iter=3, tol=0.0, random_state=1, backend="hip").fit(x.to(DEV))
-    ref = GMMXX(k=8, max_iter=3, tol=0.0, random_state=1, backend="hip").fit(x.to(DEV).float())
+    est = GMMXX(k=8, max_iter=4, tol=0.0, random_state=1, covariance_type=cov, backend="hip").fit(x.to(DEV))
+    assert est.means_.dtype == torch.float32
+    xf = x.float()[None]
+    m0, c0, w0 = estimator_init(xf.to(DEV), cov, 8, 1)
+    labels, means, covs, weights, info = torch_ref.fit(xf, 8, cov, max_iters=4, tol=0.0, init_means=m0,
+                                                       init_covs=c0, init_weights=w0, record_all_lower_bounds=False)
+    torch.testing.assert_close(torch.tensor(est.lower_bound_history_), torch.tensor(info["lower_bound_history"]),
+                               rtol=1e-5, atol=0.0)
+    torch.testing.assert_close(est.means_.cpu(), means[0], rtol=1e-4, atol=1e-4)
+    cancel = 3e-5 * float(xf.square().mean())
+    torch.testing.assert_close(est.covariances_.cpu(), covs[0], rtol=1e-4, atol=cancel)
+    torch.testing.assert_close(est.weights_.cpu(), weights[0], rtol=1e-4, atol=1e-7)
+    assert torch.equal(est.labels_.cpu(), labels[0])
+
+
+def test_bf16_engine_with_explicit_dtype():
+    """dtype=torch.bfloat16 selects the spherical bf16 engine (x kept in bf16):
+    held to the bf16 bar, 2e-3 on the per-iteration log-likelihood."""
+    x = blobs(1, 8192, 32, 8, seed=3)[0].to(torch.bfloat16)
+    est = GMMXX(k=8, max_iter=3, tol=0.0, random_state=1, dtype=torch.bfloat16, backend="hip").fit(x.to(DEV))
+    ref = GMMXX(k=8, max_iter=3, tol=0.0, random_state=1, backend="hip").fit(x.to(DEV))
     torch.testing.assert_close(torch.tensor(est.lower_bound_history_), torch.tensor(ref.lower_bound_history_),
                                rtol=2e-3, atol=0.0)
     assert est.means_.dtype == torch.float32

@@ -49,7 +49,7 @@ def test_hip_fit_matches_golden(hip, name):
     labels, m, c, w, info = em.fit(
         a["x"].to(DEV), a["init_means"].shape[1], cov, max_iters=meta["fit_kwargs"]["max_iters"],
         tol=0.0, init_means=a["init_means"], init_covs=a.get("init_variances"),
-        init_weights=a.get("init_weights"), reg_covar=meta["reg_covar"])
+        init_weights=a.get("init_weights"), reg_covar=meta["reg_covar"], record_all_lower_bounds=True)
     assert info["n_iter"] == meta["n_iter"]
     for got, exp in zip(info["lower_bound_history"], a["lower_bound_history"].tolist()):
         assert got == pytest.approx(exp, rel=1e-5, abs=1e-5)

@@ -5,7 +5,8 @@ iteration, so from the same initial parameters it must reproduce the
 in-memory EM fit (itself checked against the CPU oracle in test_hip_parity)
 and, at the end, the oracle's parameters.  Tolerances: lower bounds rtol 1e-5
 (fp32) / 2e-3 (bf16), parameters rtol 1e-4 (fp32) with an absolute floor of
-1e-4 of the largest entry, labels equal except float64 near-ties.  Only the
+1e-4 of the largest entry, labels equal except float64 near-ties
+(|Δlogit| < 1e-5·max(1, |logit|)).  Only the
 summation order over rows differs between the paths.
 """
 
@@ -14,6 +15,7 @@ import torch
 
 from gmmxx_amd import GMMXX, _hip, em, large_n
 from oracle import torch_ref
+from tests.test_hip_parity import assert_labels
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -66,7 +68,7 @@ def test_streamed_fit_matches_in_memory_fit(hip, case):
         x, k, cov, device=torch.device(DEV), max_iters=iters, tol=0.0, chunk_size_N=chunk,
         init_means=means, init_covs=covs, init_weights=w)
     lab_m, m_m, c_m, w_m, info_m = em.fit(x.to(DEV), k, cov, max_iters=iters, tol=0.0, init_means=means,
-                                          init_covs=covs, init_weights=w)
+                                          init_covs=covs, init_weights=w, record_all_lower_bounds=True)
     torch.cuda.synchronize()
     assert info_s["large_n_streaming_enabled"] and info_s["n_iter"] == iters
     ll_tol = 1e-5 if dt == torch.float32 else 2e-3
@@ -77,8 +79,9 @@ def test_streamed_fit_matches_in_memory_fit(hip, case):
     close(c_s, c_m, ptol)
     close(w_s, w_m, ptol)
     assert lab_s.device.type == "cpu" and lab_s.shape == (1, n)
-    mism = (lab_s != lab_m.cpu()).float().mean().item()
-    assert mism <= 1e-3, f"label mismatch fraction {mism}"
+    # the streamed labels are the first-max assignment under the streamed
+    # parameters (float64 near-ties aside)
+    assert_labels(lab_s, x.float(), m_s.cpu(), c_s.cpu(), w_s.cpu(), cov)
 
 
 def test_streamed_fit_matches_oracle(hip):

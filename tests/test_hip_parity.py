@@ -2,10 +2,16 @@
 
 Each case draws a seeded problem, runs one C-ABI entry point on the GPU and the
 oracle on the CPU from identical parameters.  Tolerances (stated per check):
-  * fp32 statistics / parameters: rtol 1e-4 (BASELINE north star: 1e-4 relative);
+  * fp32 parameters: element-wise rtol 1e-4, with the
+    absolute floors of ``assert_params``: means 1e-5·rms(x), covariances
+    1e-5·mean(x²) (the fp32 cancellation in E[x²] − μ² and Σr·xxᵀ − n·μμᵀ, whose
+    terms are summed in a different order on the two sides), weights 1e-7;
+  * bf16 x: parameters 2e-3 of the parameter's scale (the bf16 bar is the
+    log-likelihood);
+  * fp32 statistics: rtol 1e-4 of the statistic's scale;
   * per-iteration mean log-likelihood: rtol 1e-5 fp32, 2e-3 bf16;
   * labels: equal, except near-ties: rows whose float64 logit gap between the
-    two labels is below 1e-5·max(1, |logit|) (fp32) or 1e-3·max(1, |logit|) (bf16).
+    two labels is below 1e-5·max(1, |logit|), for fp32 and bf16 x alike.
 """
 
 import math
@@ -49,8 +55,9 @@ def to_dev(x, dtype=torch.float32):
     return x.to(DEV).to(dtype).contiguous()
 
 
-def assert_labels(got, x, means, covs, w, cov, gap_tol):
-    """Labels equal, except near-ties: |Δlogit| < gap_tol·max(1, |logit|) in float64."""
+def assert_labels(got, x, means, covs, w, cov, gap_tol=1e-5):
+    """Labels equal, except near-ties: |Δlogit| < gap_tol·max(1, |logit|) in float64.
+    Prints the mismatch count and the largest relative gap."""
     exp = torch_ref.assign(x, means, covs, w, cov)
     got = got.cpu()
     bad = (got != exp).nonzero(as_tuple=False)
@@ -59,21 +66,36 @@ def assert_labels(got, x, means, covs, w, cov, gap_tol):
     mdl = torch_ref._Model(cov, means.double(), covs.double(), w.double())
     xs = x.double().square().sum(-1) if cov == "spherical" else None
     logits = mdl.logits(x.double(), xs, 0, means.shape[1])
+    worst = 0.0
     for bi, ni in bad.tolist():
         l = logits[bi, ni]
         gap = abs(float(l[got[bi, ni]] - l[exp[bi, ni]]))
-        scale = max(1.0, abs(float(l[exp[bi, ni]])))
-        assert gap < gap_tol * scale, f"label mismatch at ({bi},{ni}) with logit gap {gap}"
+        worst = max(worst, gap / max(1.0, abs(float(l[exp[bi, ni]]))))
+    print(f"  labels: {bad.shape[0]} of {got.numel()} differ, largest relative logit gap {worst:.3e}", flush=True)
+    assert worst < gap_tol, f"{bad.shape[0]} label mismatches, largest relative logit gap {worst:.3e}"
+
+
+def assert_params(got, exp, kind, x, dt=torch.float32):
+    """fp32: element-wise rtol 1e-4 with the floors stated in the module
+    docstring; bf16 x: 2e-3 of the parameter's scale."""
+    got = got.cpu()
+    if dt != torch.float32:
+        torch.testing.assert_close(got, exp, rtol=2e-3, atol=2e-3 * float(exp.abs().max()))
+        return
+    xf = x.double()
+    floor = {"means": 1e-5 * float(xf.square().mean().sqrt()), "covs": 1e-5 * float(xf.square().mean()),
+             "weights": 1e-7}[kind]
+    torch.testing.assert_close(got, exp, rtol=1e-4, atol=floor)
 
 
 CASES = [
     # cov, B, N, D, K, dtype  -- at least ~50 rows per component (well conditioned)
     ("spherical", 2, 6000, 32, 64, torch.float32),
     ("spherical", 1, 24000, 128, 300, torch.float32),     # two k-tiles, partial second tile
-    ("spherical", 1, 30000, 128, 520, torch.bfloat16),    # single pass, groups of three workgroups
-    ("spherical", 1, 20000, 128, 256, torch.bfloat16),    # single pass, one workgroup per group (no exchange)
-    ("spherical", 2, 12345, 128, 1000, torch.bfloat16),   # single pass, groups of four, padded rows and components
-    ("spherical", 1, 40000, 128, 2048, torch.bfloat16),   # single pass, groups of eight (largest)
+    ("spherical", 1, 30000, 128, 520, torch.bfloat16),    # cooperative single pass, groups of three workgroups
+    ("spherical", 1, 20000, 128, 256, torch.bfloat16),    # two-pass bf16 kernels, one 8-wave component tile
+    ("spherical", 2, 12345, 128, 1000, torch.bfloat16),   # cooperative, groups of four, padded rows and components
+    ("spherical", 1, 40000, 128, 2048, torch.bfloat16),   # two-pass bf16 kernels, 16-wave log-normaliser tiles
     ("spherical", 2, 6000, 32, 64, torch.bfloat16),        # fused single pass, whole-chunk rows
     ("spherical", 1, 5000, 20, 10, torch.bfloat16),        # fused, padded rows, one component tile
     ("spherical", 3, 4000, 50, 30, torch.bfloat16),        # fused, D 64 padded, two component tiles
@@ -131,10 +153,14 @@ def test_score_labels_proba_match_oracle(hip, case):
     e_scores = torch_ref.score_samples(x, means, covs, w, cov)
     tol = 1e-5 if dt == torch.float32 else 2e-3
     torch.testing.assert_close(scores.cpu(), e_scores, rtol=tol, atol=tol * float(e_scores.abs().mean()))
-    assert_labels(labels, x, means, covs, w, cov, 1e-5 if dt == torch.float32 else 1e-3)
+    assert_labels(labels, x, means, covs, w, cov)
     e_proba = torch_ref.predict_proba(x, means, covs, w, cov)
     torch.testing.assert_close(proba.cpu(), e_proba, rtol=0, atol=2e-4 if dt == torch.float32 else 2e-2)
     torch.testing.assert_close(proba.sum(-1).cpu(), torch.ones(b, n), rtol=0, atol=1e-4)
+    # one E-step for both (gmmxx_hip_predict_proba_score): the same values
+    proba2, scores2 = hip.predict_proba_score(cov, xd, to_dev(means), to_dev(covs), to_dev(w))
+    torch.testing.assert_close(proba2, proba, rtol=0, atol=1e-6)
+    torch.testing.assert_close(scores2.cpu(), e_scores, rtol=tol, atol=tol * float(e_scores.abs().mean()))
 
 
 @pytest.mark.parametrize("case", CASES, ids=_id)
@@ -151,16 +177,15 @@ def test_em_step_matches_oracle_step(hip, case):
     gram = hip.gram(xd) if cov == "tied" else None
     lb = torch.zeros(1, device=DEV)
     ll_tol = 1e-5 if dt == torch.float32 else 2e-3
-    ptol = 1e-4 if dt == torch.float32 else 2e-3
     for it in range(4):
         e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, cov, means, covs, w)
         m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
         hip.em_step(cov, xd, m_d, c_d, w_d, lb, gram_xx=gram)
         torch.cuda.synchronize()
         assert float(lb) == pytest.approx(e_lb, rel=ll_tol), f"iteration {it}"
-        torch.testing.assert_close(m_d.cpu(), e_m, rtol=ptol, atol=ptol * float(e_m.abs().max()))
-        torch.testing.assert_close(c_d.cpu(), e_c, rtol=ptol, atol=ptol * float(e_c.abs().max()))
-        torch.testing.assert_close(w_d.cpu(), e_w, rtol=ptol, atol=ptol * float(e_w.abs().max()))
+        assert_params(m_d, e_m, "means", x, dt)
+        assert_params(c_d, e_c, "covs", x, dt)
+        assert_params(w_d, e_w, "weights", x, dt)
         means, covs, w = e_m, e_c, e_w
 
 
@@ -176,18 +201,17 @@ def test_em_trajectory_matches_oracle(hip, case):
     x, means, covs, w = make_problem(cov, b, n, d, k, seed=13, dtype=dt)
     from gmmxx_amd import em
     labels, m, c, wt, info = em.fit(to_dev(x, dt), k, cov, max_iters=10, tol=0.0, init_means=means,
-                                    init_covs=covs, init_weights=w)
+                                    init_covs=covs, init_weights=w, record_all_lower_bounds=True)
     e_lab, e_m, e_c, e_w, e_info = torch_ref.fit(x, k, cov, max_iters=10, tol=0.0, init_means=means,
                                                  init_covs=covs, init_weights=w)
     ll_tol = 1e-5 if dt == torch.float32 else 2e-3
     assert info["n_iter"] == e_info["n_iter"] == 10
     for got, exp in zip(info["lower_bound_history"], e_info["lower_bound_history"]):
         assert got == pytest.approx(exp, rel=ll_tol)
-    ptol = 1e-4 if dt == torch.float32 else 2e-3
-    torch.testing.assert_close(m.cpu(), e_m, rtol=ptol, atol=ptol * float(e_m.abs().max()))
-    torch.testing.assert_close(c.cpu(), e_c, rtol=ptol, atol=ptol * float(e_c.abs().max()))
-    torch.testing.assert_close(wt.cpu(), e_w, rtol=ptol, atol=ptol * float(e_w.abs().max()))
-    assert_labels(labels, x, e_m, e_c, e_w, cov, 1e-5 if dt == torch.float32 else 1e-3)
+    assert_params(m, e_m, "means", x, dt)
+    assert_params(c, e_c, "covs", x, dt)
+    assert_params(wt, e_w, "weights", x, dt)
+    assert_labels(labels, x, e_m, e_c, e_w, cov)
 
 
 def _mean_ll64(cov, x, means, covs, w):

@@ -78,7 +78,8 @@ def test_topk_fit_matches_oracle(hip, case):
     x, means, covs, w = make_problem(cov, b, n, d, k, seed=42, dtype=dt)
     iters = 4
     _, m, c, wt, info = em.fit(to_dev(x, dt), k, cov, max_iters=iters, tol=0.0, init_means=means,
-                               init_covs=covs, init_weights=w, approx_top_k=top_k, compute_labels=False)
+                               init_covs=covs, init_weights=w, approx_top_k=top_k, compute_labels=False,
+                               record_all_lower_bounds=True)
     torch.cuda.synchronize()
     _, e_m, e_c, e_w, e_info = torch_ref.fit(x, k, cov, max_iters=iters, tol=0.0, init_means=means,
                                              init_covs=covs, init_weights=w, approx_top_k=top_k,
@@ -101,7 +102,8 @@ def test_topk_fit_row_chunks(hip, monkeypatch, cov):
     for budget in (1 << 30, 24 * 4 * 2 * 4096):
         monkeypatch.setattr(em, "_TOPK_LOGIT_BYTES", budget)
         _, m, c, wt, info = em.fit(to_dev(x), 24, cov, max_iters=3, tol=0.0, init_means=means,
-                                   init_covs=covs, init_weights=w, approx_top_k=3, compute_labels=False)
+                                   init_covs=covs, init_weights=w, approx_top_k=3, compute_labels=False,
+                                   record_all_lower_bounds=True)
         out.append((m.cpu(), c.cpu(), wt.cpu(), info["lower_bound_history"]))
     assert em.topk_chunk_rows(2, 9000, 24) == 4096
     (m1, c1, w1, l1), (m2, c2, w2, l2) = out
@@ -148,7 +150,7 @@ def test_topk_estimator_and_streaming(hip):
                                                    chunk_size_N=5000, init_means=means, init_covs=covs,
                                                    init_weights=wt, approx_top_k=2)
     _, m_m, c_m, w_m, info_m = em.fit(x.to(DEV), 6, "diag", max_iters=3, tol=0.0, init_means=means,
-                                      init_covs=covs, init_weights=wt, approx_top_k=2)
+                                      init_covs=covs, init_weights=wt, approx_top_k=2, record_all_lower_bounds=True)
     assert info_s["approximate_em_enabled"] and info_s["approx_top_k"] == 2
     for a, e in zip(info_s["lower_bound_history"], info_m["lower_bound_history"]):
         assert a == pytest.approx(e, rel=1e-5)
