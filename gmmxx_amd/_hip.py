@@ -81,6 +81,7 @@ def _declare(lib):
         "gmmxx_hip_take_status": (ctypes.c_int, [P, vp, i64, vp, vp]),
         "gmmxx_hip_workspace_bytes": (i64, [P]),
         "gmmxx_hip_em_step": (ctypes.c_int, [P, vp, vp, vp, vp, vp, f64, f64, vp, vp, i64, vp]),
+        "gmmxx_hip_em_step_noalloc": (ctypes.c_int, [P, vp, vp, vp, vp, vp, f64, f64, vp, vp]),
         "gmmxx_hip_em_phase": (ctypes.c_int, [P, ctypes.c_int, vp, vp, vp, vp, vp, f64, f64, vp, vp, i64, vp]),
         "gmmxx_hip_estep_stats": (ctypes.c_int, [P, vp, vp, vp, vp, f64, f64, vp, vp, vp, vp, vp, i64, vp]),
         "gmmxx_hip_score": (ctypes.c_int, [P, vp, vp, vp, vp, vp, vp, vp, i64, vp]),
@@ -103,7 +104,8 @@ def _declare(lib):
 
 def exported_symbols() -> Tuple[str, ...]:
     return ("gmmxx_hip_abi_version", "gmmxx_hip_last_error", "gmmxx_hip_canary",
-            "gmmxx_hip_supported", "gmmxx_hip_device_info", "gmmxx_hip_take_status", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_phase",
+            "gmmxx_hip_supported", "gmmxx_hip_device_info", "gmmxx_hip_take_status", "gmmxx_hip_workspace_bytes", "gmmxx_hip_em_step", "gmmxx_hip_em_step_noalloc",
+            "gmmxx_hip_em_phase",
             "gmmxx_hip_estep_stats", "gmmxx_hip_score", "gmmxx_hip_predict_proba",
             "gmmxx_hip_predict_proba_score",
             "gmmxx_hip_gram", "gmmxx_hip_finalize_stats", "gmmxx_hip_topk_workspace_bytes",
@@ -319,6 +321,32 @@ def em_step(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: to
     _check(_lib.gmmxx_hip_em_step(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
                                   _ptr(gram_xx), float(reg_covar), float(min_weight), _ptr(lower_bound_out),
                                   ws.ptr, ws.nbytes, _stream(x.device)), "gmmxx_hip_em_step")
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
+
+def em_step_noalloc(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
+                    weights: torch.Tensor, lower_bound_out: torch.Tensor, *, reg_covar: float = 1e-6,
+                    min_weight: float = 1e-8, gram_xx: Optional[torch.Tensor] = None) -> None:
+    """em_step on the library's static device scratch (gmmxx_hip_em_step_noalloc):
+    no workspace is allocated; problems needing more than 64 MiB of workspace
+    are refused.  Calls on one device share the scratch and must not overlap."""
+    require_hip()
+    x = _device_tensor(x, "x")
+    B, N, D, K = _shape(x, means)
+    for t, nm in ((means, "means"), (covs, "covariances"), (weights, "weights"), (lower_bound_out, "lower_bound")):
+        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
+            raise ValueError(f"{nm} must be a contiguous float32 GPU tensor")
+    _check_params(covariance_type, means, covs, weights, B, K, D)
+    if covariance_type == "tied" and gram_xx is None:
+        raise ValueError("tied EM needs gram_xx = XᵀX")
+    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    with torch.cuda.device(x.device):
+        _check(_lib.gmmxx_hip_em_step_noalloc(ctypes.byref(prob), _ptr(x), _ptr(means), _ptr(covs), _ptr(weights),
+                                              _ptr(gram_xx), float(reg_covar), float(min_weight),
+                                              _ptr(lower_bound_out), _stream(x.device)),
+               "gmmxx_hip_em_step_noalloc")
 
 
 EM_PHASES = ("prepare", "lse_tile", "combine", "stats_tile", "reduce", "finalize")

@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
@@ -23,6 +24,17 @@ namespace {
 using namespace gx;
 
 thread_local std::string g_last_error;
+
+// Device scratch of the no-allocation entry point (gmmxx_hip_em_step_noalloc):
+// the workspace of problems up to kScratchBytes, one copy per device for the
+// life of the process.  In host code `scratch` names a host-side stand-in:
+// its device address comes from hipGetSymbolAddress, once per device, and
+// only that address is handed to kernels.
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
 int fail(int code, const std::string& msg) {
   g_last_error = msg;
@@ -435,6 +447,25 @@ int begin(const gmmxx_problem* p, Plan* pl, const void* x, void* ws, int64_t ws_
   return check_ws(*pl, ws, ws_bytes);
 }
 
+// The scratch's device address on the current device (looked up once per device).
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return check_hip("hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(GMMXX_ERR_UNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return fail(GMMXX_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GMMXX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -584,6 +615,26 @@ int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float
     if (rc) return rc;
   }
   return GMMXX_OK;
+}
+
+int gmmxx_hip_em_step_noalloc(const gmmxx_problem* p, const void* x, float* means, float* covs, float* weights,
+                              const float* gram, double reg_covar, double min_weight, float* lower_bound,
+                              void* stream) {
+  Plan pl;
+  int rc = plan_problem(p, &pl);
+  if (rc) return rc;
+  if ((int64_t)pl.total > kScratchBytes)
+    return fail(GMMXX_ERR_WORKSPACE, "problem needs " + std::to_string(pl.total) +
+                                         " bytes of scratch, above the no-allocation limit of " +
+                                         std::to_string(kScratchBytes) + " bytes; use gmmxx_hip_em_step");
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  // The status words are the only scratch bytes read before a call writes them
+  // (the coop launcher zeroes its exchange words itself): clear them with a
+  // kernel, which a caller may also capture in a graph.
+  launch_zero_words(at<unsigned>(ws, pl.o_flags), 2, (hipStream_t)stream);
+  return gmmxx_hip_em_step(p, x, means, covs, weights, gram, reg_covar, min_weight, lower_bound, ws, kScratchBytes,
+                           stream);
 }
 
 int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* means, const float* covs,

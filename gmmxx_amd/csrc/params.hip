@@ -871,6 +871,15 @@ __global__ void take_status_kernel(unsigned* sticky, uint32_t* out) {
   }
 }
 
+__global__ void zero_words_kernel(unsigned* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+void launch_zero_words(unsigned* p, int n, hipStream_t s) {
+  zero_words_kernel<<<(n + 255) / 256, 256, 0, s>>>(p, n);
+}
+
 void launch_take_status(unsigned* sticky, uint32_t* out, hipStream_t s) {
   take_status_kernel<<<1, 64, 0, s>>>(sticky, out);
 }

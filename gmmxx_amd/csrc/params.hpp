@@ -93,6 +93,8 @@ void launch_unpack(const UnpackArgs& a, int B, hipStream_t s);
 void launch_pack(const PackArgs& a, int B, hipStream_t s);
 void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
                  hipStream_t s);
+// p[0..n) = 0 (a kernel, not a memset: safe inside captured graphs).
+void launch_zero_words(unsigned* p, int n, hipStream_t s);
 // *out = *sticky; *sticky = 0.
 void launch_take_status(unsigned* sticky, uint32_t* out, hipStream_t s);
 void launch_canary(const int32_t* in, int32_t* out, int64_t n, int32_t offset, hipStream_t s);

@@ -109,6 +109,20 @@ int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float
 int gmmxx_hip_take_status(const gmmxx_problem* p, void* workspace, int64_t workspace_bytes,
                           uint32_t* status_out, void* stream);
 
+/* gmmxx_hip_em_step without a caller workspace: the same kernels run on a
+ * static device scratch array of the library (64 MiB per device, held for
+ * the life of the process), so the call allocates nothing and takes no
+ * workspace arguments.  Problems whose gmmxx_hip_workspace_bytes exceeds
+ * 64 MiB are refused with GMMXX_ERR_WORKSPACE before any launch.  Every call
+ * on one device shares that device's scratch: calls that overlap on one
+ * device (two streams, two threads) race and must be ordered by the caller.
+ * Call with the stream's device current.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). */
+int gmmxx_hip_em_step_noalloc(const gmmxx_problem* p, const void* x, float* means, float* covariances,
+                              float* weights, const float* gram, double reg_covar, double min_weight,
+                              float* lower_bound, void* stream);
+
 /* The six phases of gmmxx_hip_em_step, for callers that time or interleave
  * them; gmmxx_hip_em_step(...) == phases PREPARE..FINALIZE in order with the
  * same arguments and workspace.  PREPARE: iteration prelude, Cholesky
