@@ -12,11 +12,15 @@ orders -- and weights 1e-7).
 Where EM is ill-conditioned (rows split between two near-equal components,
 variances collapsing onto a few points) a one-ulp difference in a logit
 moves a responsibility, and any two fp32 implementations part by more than
-the bar; the oracle itself then differs from float64 by as much.  A value
-outside the bar is therefore accepted when it is at least as close to the
-float64 result from the same inputs (``f64_em``) as the oracle's value is,
-within a factor 4: the HIP result is then as accurate as the reference's own
-arithmetic, and the difference is the problem's conditioning, not an error.
+the bar; the oracle itself then differs from float64 by as much.  A tensor
+outside the bar is therefore accepted when the HIP result is at least as
+accurate as the oracle's, judged against the float64 result from the same
+inputs (``f64_em``): its largest error relative to the bar, measured from
+the float64 value, is at most 4 times the oracle's largest (or within the
+bar).  The HIP result is then as accurate as the reference's own arithmetic
+and the difference is the problem's conditioning, not an error.  (Per
+element the comparison would hinge on where the oracle happens to round
+luckily; over the tensor it compares the two implementations' accuracy.)
 """
 
 import torch
@@ -35,9 +39,10 @@ def param_band(kind, x, bf16):
 
 
 def judge_params(got, exp, kind, x, bf16=False, truth_fn=None):
-    """Counts of elements outside the bar and of those the float64 truth does
-    not explain; ``truth_fn()`` returns the float64 value (called only when
-    some element is outside the bar)."""
+    """Elements outside the bar, the largest error relative to the bar, and
+    whether the tensor fails (``unexplained``: 0 or the count of elements
+    outside the bar); ``truth_fn()`` returns the float64 value (called only
+    when some element is outside the bar)."""
     got = got.detach().cpu().double()
     exp = exp.detach().cpu().double()
     rtol, floor = param_band(kind, x, bf16)
@@ -48,11 +53,16 @@ def judge_params(got, exp, kind, x, bf16=False, truth_fn=None):
     out = (got - exp).abs() > band
     res = {"kind": kind, "elements": int(exp.numel()), "outside_bar": int(out.sum()),
            "worst_ratio": float(((got - exp).abs() / band).max()), "unexplained": 0}
-    if res["outside_bar"] and truth_fn is not None:
-        t = truth_fn().detach().cpu().double()
-        ok = (got - t).abs() <= torch.maximum(FACTOR * (exp - t).abs(), rtol * t.abs() + floor)
-        res["unexplained"] = int((out & ~ok).sum())
-    elif res["outside_bar"]:
+    if not res["outside_bar"]:
+        return res
+    if truth_fn is None:
+        res["unexplained"] = res["outside_bar"]
+        return res
+    t = truth_fn().detach().cpu().double()
+    band_t = rtol * t.abs() + floor
+    res["hip_vs_float64"] = float(((got - t).abs() / band_t).max())
+    res["oracle_vs_float64"] = float(((exp - t).abs() / band_t).max())
+    if res["hip_vs_float64"] > max(FACTOR * res["oracle_vs_float64"], 1.0):
         res["unexplained"] = res["outside_bar"]
     return res
 
