@@ -391,8 +391,8 @@ int stats_pass(const Plan& pl, const void* x, void* ws, hipStream_t s) {
 // the row count per batch that divides N_k into the weights.
 // skip: a nonzero word there leaves the parameters unchanged (a timed-out
 // cooperative pass), or null.
-void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, double min_weight, int64_t n_rows,
-              float* means, float* covs, float* weights, hipStream_t s, const unsigned* skip = nullptr) {
+FinalizeArgs finalize_args(const Plan& pl, void* ws, const float* gram, double reg_covar, double min_weight,
+                           int64_t n_rows, float* means, float* covs, float* weights, const unsigned* skip) {
   FinalizeArgs f{};
   f.cov = pl.cov;
   f.B = pl.B;
@@ -413,7 +413,12 @@ void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, dou
   f.covs = covs;
   f.weights = weights;
   f.skip = skip;
-  launch_finalize(f, s);
+  return f;
+}
+
+void finalize(const Plan& pl, void* ws, const float* gram, double reg_covar, double min_weight, int64_t n_rows,
+              float* means, float* covs, float* weights, hipStream_t s, const unsigned* skip = nullptr) {
+  launch_finalize(finalize_args(pl, ws, gram, reg_covar, min_weight, n_rows, means, covs, weights, skip), s);
 }
 
 // Approximate top-k EM: each row's threshold logit and index, per-block
@@ -592,10 +597,11 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
       return check_hip("statistics tile kernel");
     }
-    case GMMXX_PHASE_REDUCE:
+    case GMMXX_PHASE_REDUCE: {
       launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                            at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
       return check_hip("statistics reduction");
+    }
     case GMMXX_PHASE_FINALIZE:
       // A cooperative pass that timed out leaves the parameters as they were.
       finalize(pl, ws, gram, reg_covar, min_weight, pl.N, means, covs, weights, s,

