@@ -201,7 +201,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_pstats = take((size_t)std::max({q.slices, q.fslices, q.cspb}) * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
   // (+B: the tied EM iteration's per-batch log-likelihood shift, after the row partials)
-  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices}) + 1) * 8);
+  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices}) + q.D + 1) * 8);
   q.o_xch = take(q.coop ? (size_t)q.cNG * kRing * q.cG * kBN * 8 : 0);
   // [0] status of the last cooperative pass (zeroed by its launcher), [1] sticky
   // status since the last gmmxx_hip_take_status
@@ -319,10 +319,20 @@ int64_t red_tmp_floats(const Plan& pl) { return (int64_t)std::max(pl.ktiles, pl.
 int ll_parts(const Plan& pl) {
   return pl.B * (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.single ? pl.slices : pl.cblocks)));
 }
+// Where an EM iteration's tied -½ tr(P XᵀX) terms go: after the log-likelihood
+// partials of its log-normaliser pass (the single-pass or the combine kernel's),
+// so the one reduction sums both; null where no pass leaves the row forms out.
+double* tied_shift(const Plan& pl, void* ws) {
+  if (pl.cov != TIED || pl.fused || pl.coop) return nullptr;
+  return at<double>(ws, pl.o_ll) + (pl.single ? ll_parts(pl) : pl.B * pl.cblocks);
+}
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
+// gram/shift (tied EM without the row forms): the parameter packing also writes
+// the -½ tr(P XᵀX) terms, D per problem, to shift.
 int prepare(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights,
-            double reg, double minw, int prelude, void* ws, hipStream_t s, bool rowquad = true) {
+            double reg, double minw, int prelude, void* ws, hipStream_t s, bool rowquad = true,
+            const float* gram = nullptr, double* shift = nullptr) {
   float* prec = nullptr;
   float* logdet = nullptr;
   if (pl.cov == TIED || pl.cov == FULL) {
@@ -352,6 +362,8 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
   a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
+  a.gram = shift ? gram : nullptr;
+  a.shift = gram ? shift : nullptr;
   launch_prep(a, s);
   if (pl.cov == TIED && rowquad)
     launch_rowquad(reinterpret_cast<const float*>(x), pl.B, pl.N, pl.D, prec, at<float>(ws, pl.o_rowq), s);
@@ -550,7 +562,8 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
   const hipStream_t s = (hipStream_t)stream;
   switch (phase) {
     case GMMXX_PHASE_PREPARE:
-      return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s, /*rowquad=*/false);
+      return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s, /*rowquad=*/false, gram,
+                     tied_shift(pl, ws));
     case GMMXX_PHASE_LSE_TILE: {
       if (pl.coop) return run_coop(pl, x, ws, s);
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
@@ -565,10 +578,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     case GMMXX_PHASE_COMBINE: {
       if (pl.fused || pl.coop || pl.single) {  // the single pass already produced per-slice log-likelihoods
         int parts = ll_parts(pl);
-        if (pl.single && pl.cov == TIED) {   // -½ tr(P XᵀX) per batch after the slice partials
-          launch_tied_ll_shift(at<float>(ws, pl.o_prec), gram, pl.B, pl.D, at<double>(ws, pl.o_ll) + parts, s);
-          parts += pl.B;
-        }
+        if (tied_shift(pl, ws)) parts += pl.B * pl.D;   // -½ tr(P XᵀX) rows, from the prepare phase
         launch_ll_reduce(at<double>(ws, pl.o_ll), parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
         if (pl.coop) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), lower_bound, s);
         return check_hip("log-likelihood reduction");
@@ -583,10 +593,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       c.ll_part = at<double>(ws, pl.o_ll);
       launch_combine(c, s);
       int parts = pl.B * pl.cblocks;
-      if (pl.cov == TIED) {   // -½ tr(P XᵀX) per batch after the row partials
-        launch_tied_ll_shift(at<float>(ws, pl.o_prec), gram, pl.B, pl.D, at<double>(ws, pl.o_ll) + parts, s);
-        parts += pl.B;
-      }
+      if (tied_shift(pl, ws)) parts += pl.B * pl.D;   // -½ tr(P XᵀX) rows, from the prepare phase
       launch_ll_reduce(at<double>(ws, pl.o_ll), parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
       return check_hip("combine");
     }

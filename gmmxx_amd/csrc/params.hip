@@ -142,6 +142,20 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
     colq = wave_sum(mpm);
     ca = -0.5f * kLog2e;
     cb = (lw - 0.5f * (log2pi_d + a.logdet[b])) * kLog2e;
+    if (a.shift) {
+      // The tied EM logits leave out each row's xᵀPx, so the row log-normalisers
+      // are each ½ xᵀPx too large; their sum, -½ Σ_n x_nᵀ P x_n = -½ Σ_rj P_rj
+      // (XᵀX)_rj, is added back as D log-likelihood parts per problem, row r of
+      // the trace from the blocks k ≡ r (mod K), in double.
+      const float* G = a.gram + (size_t)b * D * D;
+      for (int r = k; r < D; r += K) {
+        double t = 0.0;
+        for (int j = lane; j < D; j += 64) t = fma((double)P[r * D + j], (double)G[r * D + j], t);
+#pragma unroll
+        for (int off = 32; off >= 1; off /= 2) t += __shfl_xor(t, off);
+        if (lane == 0) a.shift[(size_t)b * D + r] = -0.5 * t;
+      }
+    }
   } else {
     // FULL: W_k = [packed P_k with doubled off-diagonal | -2 P_k μ_k]  (torch_fallback.py:418-432)
     const float* P = a.prec + bk * D * D;
@@ -173,15 +187,19 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
 //              (level 0 = no jitter, level i = 1e-6 * 10^(i-1), i = 1..6; 7 = none),
 //              and that factor
 // chol_level:  the batch-global level: the largest first level (every matrix
-//              factorises there)
+//              factorises there); read by chol_finish's waves themselves for
+//              batches of at most kCholLevelInline matrices
 // chol_finish: the factor at the global level (the stored one when it is the
 //              matrix's own first level, else refactorised), X = L^-1,
 //              P = XᵀX = L^-T L^-1 and log det = 2 Σ log L_jj.
-// One wave per matrix, lane i = row i, the matrix padded to DP x DP with the
-// identity; each lane keeps its row of the factor (and then its column of the
-// inverse) in registers and reads other lanes' entries with readlane, so the
-// dependency chains of the factorisation and the inverse run within the wave
-// without LDS round trips; P = XᵀX runs on fp32 MFMA from a per-wave LDS tile.
+// chol_one:    all three in one launch for a batch that fits one workgroup
+//              (tied covariances of a few problems).
+// One wave per matrix, the matrix padded to DP x DP with the identity: the
+// factorisation and the inverse are blocked in 16 x 16 tiles, with the
+// off-panel work (trailing updates, off-diagonal inverse blocks, P = XᵀX) on
+// fp32 MFMA from per-wave LDS tiles and only the 16-wide panels' dependency
+// chains on the VALU, within the wave (readlane and wavefront-scope LDS, no
+// workgroup barrier).
 // ---------------------------------------------------------------------------
 
 constexpr int kMaxCholD = 64;
@@ -204,14 +222,24 @@ template <int DP>
 constexpr int chol_rs() { return DP + 4; }
 
 // Lane i's row i of sym(C) + jitter·I into registers (identity outside D x D).
+// Every load is unconditional (indices clamped into the matrix, the padding
+// selected afterwards), so the 2·DP loads issue back to back; the column reads
+// C[c][i] are coalesced across the wave.
 template <int DP>
 __device__ __forceinline__ void chol_row(const float* C, int D, float jitter, float (&a)[DP]) {
   const int i = threadIdx.x & 63;
+  const int ic = min(i, D - 1);
+  float r[DP], t[DP];
 #pragma unroll
   for (int c = 0; c < DP; ++c) {
-    float v = (i == c) ? 1.f : 0.f;
-    if (i < D && c < D) v = (i == c) ? C[i * D + i] + jitter : 0.5f * (C[i * D + c] + C[c * D + i]);
-    a[c] = v;
+    const int cc = min(c, D - 1);
+    r[c] = C[ic * D + cc];
+    t[c] = C[cc * D + ic];
+  }
+#pragma unroll
+  for (int c = 0; c < DP; ++c) {
+    const float v = (i == c) ? r[c] + jitter : 0.5f * (r[c] + t[c]);
+    a[c] = (i < D && c < D) ? v : ((i == c) ? 1.f : 0.f);
   }
 }
 
@@ -219,46 +247,181 @@ __device__ __forceinline__ float lane_val(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Left-looking factorisation with every row in registers: lane i keeps row i
-// (a, becoming L's row i); step j reads row j from lane j with readlane (a
-// scalar broadcast, no LDS): t_i = A_ij - Σ_{c<j} L_ic L_jc, the pivot t_j,
-// L_jj = sqrt(t_j), L_ij = t_i · (1 / L_jj) for i > j (the reciprocal scaling
-// of LAPACK's potf2), 0 above the diagonal.  Fully unrolled, so every register
-// index and lane is a constant.  Returns success (uniform across the wave).
+// Per-wave LDS of the factorisation: the finished factor L and the inverse X
+// (DP x chol_rs rows each, row-major) and a staging tile S (DP x kCholSRS).
+constexpr int kCholSRS = 20;   // 16 panel columns + 4: 16-byte rows, lanes i and i + 1 four banks apart
+
 template <int DP>
-__device__ bool chol_regs(float (&a)[DP]) {
-  const int i = threadIdx.x & 63;
+struct CholLds {
+  float L[DP * chol_rs<DP>()];
+  float X[DP * chol_rs<DP>()];
+  float S[DP * kCholSRS];
+};
+
+// Waves (matrices) per workgroup: the LDS above is 40 KB per wave at DP = 64.
+template <int DP>
+constexpr int chol_waves() { return DP == 64 ? 2 : 4; }
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Blocked left-looking factorisation, panels of 16 columns (LAPACK potrf's
+// blocking with potf2 on the panel).  Lane i keeps row i of A in a.  For panel
+// J (columns J0..J0+15) the update A[:, J] -= L[:, <J0] · L[J, <J0]ᵀ runs on
+// fp32 MFMA 16x16x4 from the finished panels in sh.L (row blocks I >= J),
+// staged through sh.S back into the lanes' rows; the panel is then factorised
+// in registers, left-looking within it: t_i = A_ij - Σ_{J0<=c<j} L_ic L_jc
+// (row j of the panel read from lane j with readlane), L_jj = sqrt(t_j),
+// L_ij = t_i · (1 / L_jj) below the diagonal, 0 above (hardware v_sqrt_f32 and
+// v_rcp_f32, 1 ulp), and written to sh.L.  Returns success (every pivot > 0),
+// uniform across the wave; sh.L and a hold the factor.
+template <int DP>
+__device__ __forceinline__ bool chol_blocked(float (&a)[DP], CholLds<DP>& sh) {
+  constexpr int RS = chol_rs<DP>(), NB = DP / 16;
+  const int i = threadIdx.x & 63, g = i / 16, li = i % 16;
+  const int ri = min(i, DP - 1);
   bool ok = true;
 #pragma unroll
-  for (int j = 0; j < DP; ++j) {
-    float t[4] = {a[j], 0.f, 0.f, 0.f};
+  for (int J = 0; J < NB; ++J) {
+    const int J0 = 16 * J;
+    if (J > 0) {
 #pragma unroll
-    for (int c = 0; c < j; ++c) t[c & 3] = fmaf(-a[c], lane_val(a[c], j), t[c & 3]);
-    const float tj = (t[0] + t[1]) + (t[2] + t[3]);
-    const float d = lane_val(tj, j);
-    ok = ok && (d > 0.f);
-    const float ljj = sqrtf(d);
-    const float inv = 1.f / ljj;
-    a[j] = (i < j) ? 0.f : ((i == j) ? ljj : tj * inv);
+      for (int I = J; I < NB; ++I) {
+        const int I0 = 16 * I;
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k0 = 0; k0 < J0; k0 += 4) acc = mfma4(sh.L[(I0 + li) * RS + k0 + g], sh.L[(J0 + li) * RS + k0 + g], acc);
+        // acc[v] = (L Lᵀ)[I0 + 4g + v][J0 + li]
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sh.S[(I0 + 4 * g + v) * kCholSRS + li] = acc[v];
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int q = 0; q < 16; q += 4) {
+        const f32x4 u = *reinterpret_cast<const f32x4*>(&sh.S[ri * kCholSRS + q]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) a[J0 + q + v] -= (i >= J0) ? u[v] : 0.f;   // rows above: zeroed below
+      }
+    }
+#pragma unroll
+    for (int j = J0; j < J0 + 16; ++j) {
+      float t[4] = {a[j], 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = J0; c < j; ++c) t[c & 3] = fmaf(-a[c], lane_val(a[c], j), t[c & 3]);
+      const float tj = (t[0] + t[1]) + (t[2] + t[3]);
+      const float d = lane_val(tj, j);
+      ok = ok && (d > 0.f);
+      const float ljj = __builtin_amdgcn_sqrtf(d);
+      const float inv = __builtin_amdgcn_rcpf(ljj);
+      a[j] = (i < j) ? 0.f : ((i == j) ? ljj : tj * inv);
+    }
+    if (i < DP) {
+#pragma unroll
+      for (int q = 0; q < 16; q += 4)
+        *reinterpret_cast<f32x4*>(&sh.L[i * RS + J0 + q]) = f32x4{a[J0 + q], a[J0 + q + 1], a[J0 + q + 2], a[J0 + q + 3]};
+    }
+    wave_lds_sync();
   }
   return ok;
 }
 
-constexpr int kCholWaves = 4;   // matrices (waves) per workgroup
-
+// The first jitter level (0..6) at which the matrix factorises, 7 for none;
+// a and sh.L hold that factor (or the last attempt).
 template <int DP>
-__global__ __launch_bounds__(64 * kCholWaves) void chol_try_kernel(const float* cov, int D, int M, int* first_ok,
-                                                                   float* lbuf) {
-  const int w = threadIdx.x / 64, i = threadIdx.x & 63;
-  const int m = blockIdx.x * kCholWaves + w;
-  if (m >= M) return;   // whole wave
-  const float* C = cov + (size_t)m * D * D;
-  float a[DP];
-  int level = 7;
+__device__ __forceinline__ int chol_first(const float* C, int D, float (&a)[DP], CholLds<DP>& sh) {
   for (int lv = 0; lv < 7; ++lv) {
     chol_row<DP>(C, D, jitter_of(lv), a);
-    if (chol_regs<DP>(a)) { level = lv; break; }
+    if (chol_blocked<DP>(a, sh)) return lv;
   }
+  return 7;
+}
+
+// From the factor in sh.L: log det = 2 Σ_{i<D} log L_ii into *logdet, the
+// inverse X = L^-1 into sh.X and P = XᵀX = L^-T L^-1 into Pm (D x D).
+//   diagonal blocks X_GG = L_GG^-1, all four at once: lane (G, c) = (i / 16,
+//     i % 16) owns column c, x_r = -(Σ_{c<=k<r} L_rk x_k) / L_rr, x_c = 1 / L_cc,
+//     0 above, L_GG's rows read from sh.L (one broadcast address per group);
+//   off-diagonal blocks by distance from the diagonal, on fp32 MFMA:
+//     X_IJ = -X_II · Σ_{J<=K<I} L_IK X_KJ (the sum staged in sh.S);
+//   P_IJ = Σ_{K>=I} X_KIᵀ X_KJ for I >= J (X is block lower triangular), each
+//     entry i >= j written to both (i, j) and (j, i), so P is exactly symmetric.
+template <int DP>
+__device__ __forceinline__ void chol_inverse(int D, CholLds<DP>& sh, float* Pm, float* logdet) {
+  constexpr int RS = chol_rs<DP>(), NB = DP / 16;
+  const int i = threadIdx.x & 63, g = i / 16, li = i % 16;
+  float ld = (i < D) ? logf(sh.L[i * RS + i]) : 0.f;
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) ld += __shfl_xor(ld, off);
+  if (i == 0) *logdet = 2.f * ld;
+  {
+    const int G0 = 16 * min(g, NB - 1), c = li;
+    float x[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float* Lr = &sh.L[(G0 + r) * RS + G0];
+      float t[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = 0; k0 < r; k0 += 4) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(Lr + k0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (k0 + v < r) t[v] = fmaf(l4[v], x[k0 + v], t[v]);
+      }
+      const float inv = __builtin_amdgcn_rcpf(Lr[r]);
+      x[r] = (r < c) ? 0.f : ((r == c) ? inv : -((t[0] + t[1]) + (t[2] + t[3])) * inv);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sh.X[(G0 + r) * RS + G0 + c] = x[r];
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int dd = 1; dd < NB; ++dd)
+#pragma unroll
+    for (int J = 0; J + dd < NB; ++J) {
+      const int I = J + dd, I0 = 16 * I, J0 = 16 * J;
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = J0; k0 < I0; k0 += 4) acc = mfma4(sh.L[(I0 + li) * RS + k0 + g], sh.X[(k0 + g) * RS + J0 + li], acc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sh.S[(4 * g + v) * kCholSRS + li] = acc[v];
+      wave_lds_sync();
+      f32x4 acc2 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = 0; k0 < 16; k0 += 4) acc2 = mfma4(sh.X[(I0 + li) * RS + I0 + k0 + g], sh.S[(k0 + g) * kCholSRS + li], acc2);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sh.X[(I0 + 4 * g + v) * RS + J0 + li] = -acc2[v];
+      wave_lds_sync();
+    }
+#pragma unroll
+  for (int I = 0; I < NB; ++I)
+#pragma unroll
+    for (int J = 0; J <= I; ++J) {
+      const int I0 = 16 * I, J0 = 16 * J;
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = I0; k0 < DP; k0 += 4) acc = mfma4(sh.X[(k0 + g) * RS + I0 + li], sh.X[(k0 + g) * RS + J0 + li], acc);
+      // acc[v] = P[I0 + 4g + v][J0 + li]
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int pi = I0 + 4 * g + v, pj = J0 + li;
+        if (pi >= pj && pi < D && pj < D) {
+          Pm[(size_t)pi * D + pj] = acc[v];
+          Pm[(size_t)pj * D + pi] = acc[v];
+        }
+      }
+    }
+}
+
+template <int DP>
+__global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_try_kernel(const float* cov, int D, int M,
+                                                                         int* first_ok, float* lbuf) {
+  __shared__ __align__(16) CholLds<DP> sh[chol_waves<DP>()];
+  const int w = threadIdx.x / 64, i = threadIdx.x & 63;
+  const int m = blockIdx.x * chol_waves<DP>() + w;
+  if (m >= M) return;   // whole wave
+  float a[DP];
+  const int level = chol_first<DP>(cov + (size_t)m * D * D, D, a, sh[w]);
   if (i == 0) first_ok[m] = level;
   if (i < DP) {
     float* Lg = lbuf + ((size_t)m * DP + i) * DP;
@@ -281,77 +444,77 @@ __global__ void chol_level_kernel(const int* first_ok, int M, int* level) {
   if (threadIdx.x == 0) *level = min(red[0], 6);
 }
 
+// The batch level read by each wave itself (small batches: first_ok has at
+// most kCholLevelInline entries), so no separate level launch is needed.
+constexpr int kCholLevelInline = 512;
+
+__device__ int wave_level(const int* first_ok, int M) {
+  int v = 0;
+  for (int m = threadIdx.x & 63; m < M; m += 64) v = max(v, first_ok[m]);
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) v = max(v, __shfl_xor(v, off));
+  return min(v, 6);
+}
+
+// level == nullptr: the batch level is computed from first_ok here (M <= kCholLevelInline).
 template <int DP>
-__global__ __launch_bounds__(64 * kCholWaves) void chol_finish_kernel(const float* cov, int D, int M,
-                                                                      const int* first_ok, const int* level,
-                                                                      const float* lbuf, float* prec, float* logdet) {
+__global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_finish_kernel(const float* cov, int D, int M,
+                                                                            const int* first_ok, const int* level,
+                                                                            const float* lbuf, float* prec,
+                                                                            float* logdet) {
   constexpr int RS = chol_rs<DP>();
-  __shared__ __align__(16) float Xsh[kCholWaves][DP * RS];
+  __shared__ __align__(16) CholLds<DP> sh[chol_waves<DP>()];
   const int w = threadIdx.x / 64, i = threadIdx.x & 63;
-  const int m = blockIdx.x * kCholWaves + w;
+  const int m = blockIdx.x * chol_waves<DP>() + w;
   if (m >= M) return;   // whole wave
-  float* X = Xsh[w];
-  const int lv = *level;
-  float a[DP];
+  const int lv = level ? *level : wave_level(first_ok, M);
   if (first_ok[m] == lv) {
-    const float* Lg = lbuf + ((size_t)m * DP + (i < DP ? i : 0)) * DP;
+    if (i < DP) {
+      const float* Lg = lbuf + ((size_t)m * DP + i) * DP;
 #pragma unroll
-    for (int c = 0; c < DP; c += 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(Lg + c);
-      a[c] = v[0]; a[c + 1] = v[1]; a[c + 2] = v[2]; a[c + 3] = v[3];
+      for (int c = 0; c < DP; c += 4)
+        *reinterpret_cast<f32x4*>(&sh[w].L[i * RS + c]) = *reinterpret_cast<const f32x4*>(Lg + c);
     }
+    wave_lds_sync();
   } else {
+    float a[DP];
     chol_row<DP>(cov + (size_t)m * D * D, D, jitter_of(lv), a);
-    chol_regs<DP>(a);
+    chol_blocked<DP>(a, sh[w]);
   }
-  // log det = 2 Σ_{i<D} log L_ii (lane i holds L_ii in a[i]: select it by index)
-  float lii = 1.f;
-#pragma unroll
-  for (int c = 0; c < DP; ++c) lii = (i == c) ? a[c] : lii;
-  float ld = (i < D) ? logf(lii) : 0.f;
-#pragma unroll
-  for (int off = 32; off >= 1; off /= 2) ld += __shfl_xor(ld, off);
-  if (i == 0) logdet[m] = 2.f * ld;
-  // X = L^-1 by columns, lane c owning column c (x): x_r = -(Σ_{k<r} L_rk x_k) / L_rr
-  // for r > c, x_c = 1 / L_cc, 0 above; row r of L comes from lane r (readlane).
-  const int c = i;
-  float x[DP];
-#pragma unroll
-  for (int r = 0; r < DP; ++r) {
-    float t[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < r; ++k) t[k & 3] = fmaf(lane_val(a[k], r), x[k], t[k & 3]);
-    const float inv = 1.f / lane_val(a[r], r);
-    x[r] = (r < c) ? 0.f : ((r == c) ? inv : -((t[0] + t[1]) + (t[2] + t[3])) * inv);
+  chol_inverse<DP>(D, sh[w], prec + (size_t)m * D * D, logdet + m);
+}
+
+// Whole batch in one workgroup (M <= chol_waves): factor, batch level through
+// LDS, inverse, in a single launch.  first_ok and level are still written.
+template <int DP>
+__global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const float* cov, int D, int M,
+                                                                         int* first_ok, int* level, float* prec,
+                                                                         float* logdet) {
+  constexpr int NW = chol_waves<DP>();
+  __shared__ __align__(16) CholLds<DP> sh[NW];
+  __shared__ int lev[NW];
+  const int w = threadIdx.x / 64, i = threadIdx.x & 63;
+  const bool active = w < M;
+  const float* C = cov + (size_t)w * D * D;
+  float a[DP];
+  int first = 0;
+  if (active) first = chol_first<DP>(C, D, a, sh[w]);
+  if (i == 0) {
+    lev[w] = first;
+    if (active) first_ok[w] = first;
   }
-  // Column c of X as row c of the tile, then P = XᵀX (P_ij = Σ_r X_ri X_rj =
-  // Xsh[i]·Xsh[j]) on fp32 MFMA 16x16x4: lower tiles only, each entry i >= j
-  // written to both (i, j) and (j, i), so P is exactly symmetric.
-  if (i < DP) {
+  __syncthreads();
+  int lv = 0;
 #pragma unroll
-    for (int r = 0; r < DP; r += 4) *reinterpret_cast<f32x4*>(X + i * RS + r) = f32x4{x[r], x[r + 1], x[r + 2], x[r + 3]};
+  for (int u = 0; u < NW; ++u) lv = max(lv, lev[u]);
+  lv = min(lv, 6);
+  if (threadIdx.x == 0) *level = lv;
+  if (!active) return;   // whole wave
+  if (first != lv) {
+    chol_row<DP>(C, D, jitter_of(lv), a);
+    chol_blocked<DP>(a, sh[w]);
   }
-  wave_lds_sync();
-  const int g = i / 16, li = i % 16;
-  float* Pm = prec + (size_t)m * D * D;
-#pragma unroll
-  for (int I = 0; I < DP; I += 16)
-#pragma unroll
-    for (int J = 0; J <= I; J += 16) {
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k0 = 0; k0 < DP; k0 += 4)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(X[(I + li) * RS + k0 + g], X[(J + li) * RS + k0 + g], acc, 0, 0, 0);
-      // acc[v] = P[I + 4g + v][J + li]
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int pi = I + 4 * g + v, pj = J + li;
-        if (pi >= pj && pi < D && pj < D) {
-          Pm[(size_t)pi * D + pj] = acc[v];
-          Pm[(size_t)pj * D + pi] = acc[v];
-        }
-      }
-    }
+  chol_inverse<DP>(D, sh[w], prec + (size_t)w * D * D, logdet + w);
 }
 
 // ---------------------------------------------------------------------------
@@ -549,19 +712,6 @@ void launch_topk_select(const float* logits, int B, int64_t N, int K, int top_k,
     topk_select_kernel<<<grid, block, 0, s>>>(logits, N, K, top_k, lse2, thr2, thr_idx, ll_part);
 }
 
-// Tied EM iteration: the logits leave out the per-row xᵀPx, so the row
-// log-normalisers are each too large by ½ xᵀPx; their sum is taken back here
-// as -½ Σ_n x_nᵀ P x_n = -½ Σ_ij P_ij (XᵀX)_ij.
-__global__ void tied_ll_shift_kernel(const float* prec, const float* gram, int D, double* out) {
-  __shared__ double scratch[32];
-  const int b = blockIdx.x;
-  const float* P = prec + (size_t)b * D * D;
-  const float* G = gram + (size_t)b * D * D;
-  double s = 0.0;
-  for (int i = threadIdx.x; i < D * D; i += blockDim.x) s += (double)P[i] * (double)G[i];
-  const double t = block_sum(s, scratch);
-  if (threadIdx.x == 0) out[b] = -0.5 * t;
-}
 
 // Mean log-likelihood over all B*N rows (lower bound of the iteration).
 __global__ void ll_reduce_kernel(const double* ll_part, int count, double inv_total, float* out) {
@@ -658,22 +808,30 @@ __global__ __launch_bounds__(64 * kFinWaves) void finalize_kernel(FinalizeArgs a
 // One block per (row d, batch b), one thread per column e; four partial sums
 // over the components keep the loads in flight.  s_de is formed with the same
 // products in the same order for (d, e) and (e, d), so the result is symmetric.
-__global__ void finalize_tied_kernel(FinalizeArgs a) {
-  const int b = blockIdx.y, d = blockIdx.x, e = threadIdx.x;
+constexpr int kTiedWaves = 4;   // waves per covariance row, splitting the components
+
+__global__ __launch_bounds__(64 * kTiedWaves) void finalize_tied_kernel(FinalizeArgs a) {
+  __shared__ float red[kTiedWaves][64];
+  const int b = blockIdx.y, d = blockIdx.x, w = threadIdx.x / 64, e = threadIdx.x & 63;
+  if (a.skip && *a.skip != 0u) return;   // uniform over the grid
   const int K = a.K, D = a.D, JP = a.JP;
-  if (e >= D || (a.skip && *a.skip != 0u)) return;
+  const int ec = min(e, D - 1);
   const float* st = a.stats + (size_t)b * K * JP + a.nk_col;
   const float* mu = a.means + (size_t)b * K * D;
+  // Σ_k N_k μ_kd μ_ke over k ≡ w (mod kTiedWaves), four chains
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  int k = 0;
-  for (; k + 4 <= K; k += 4) {
-    s0 = fmaf(st[(size_t)k * JP], mu[k * D + d] * mu[k * D + e], s0);
-    s1 = fmaf(st[(size_t)(k + 1) * JP], mu[(k + 1) * D + d] * mu[(k + 1) * D + e], s1);
-    s2 = fmaf(st[(size_t)(k + 2) * JP], mu[(k + 2) * D + d] * mu[(k + 2) * D + e], s2);
-    s3 = fmaf(st[(size_t)(k + 3) * JP], mu[(k + 3) * D + d] * mu[(k + 3) * D + e], s3);
+  int k = w;
+  for (; k + 3 * kTiedWaves < K; k += 4 * kTiedWaves) {
+    s0 = fmaf(st[(size_t)k * JP], mu[k * D + d] * mu[k * D + ec], s0);
+    s1 = fmaf(st[(size_t)(k + 4) * JP], mu[(k + 4) * D + d] * mu[(k + 4) * D + ec], s1);
+    s2 = fmaf(st[(size_t)(k + 8) * JP], mu[(k + 8) * D + d] * mu[(k + 8) * D + ec], s2);
+    s3 = fmaf(st[(size_t)(k + 12) * JP], mu[(k + 12) * D + d] * mu[(k + 12) * D + ec], s3);
   }
-  for (; k < K; ++k) s0 = fmaf(st[(size_t)k * JP], mu[k * D + d] * mu[k * D + e], s0);
-  const float sde = (s0 + s1) + (s2 + s3);
+  for (; k < K; k += kTiedWaves) s0 = fmaf(st[(size_t)k * JP], mu[k * D + d] * mu[k * D + ec], s0);
+  red[w][e] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (w != 0 || e >= D) return;
+  const float sde = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
   const float* G = a.gram + (size_t)b * D * D;
   const float ade = (G[d * D + e] - sde) / (float)a.N;
   const float aed = (G[e * D + d] - sde) / (float)a.N;
@@ -828,19 +986,23 @@ void launch_prep(const PrepArgs& a, hipStream_t s) {
   prep_kernel<<<dim3(a.K, a.B), 64, 0, s>>>(a);
 }
 
-void launch_tied_ll_shift(const float* prec, const float* gram, int B, int D, double* out, hipStream_t s) {
-  tied_ll_shift_kernel<<<B, 256, 0, s>>>(prec, gram, D, out);
-}
 
 int chol_dp(int D) { return D <= 16 ? 16 : (D <= 32 ? 32 : 64); }
 
 template <int DP>
 static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
                            float* logdet, hipStream_t s) {
-  const int blocks = (M + kCholWaves - 1) / kCholWaves;
-  chol_try_kernel<DP><<<blocks, 64 * kCholWaves, 0, s>>>(cov, D, M, first_ok, lbuf);
-  chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
-  chol_finish_kernel<DP><<<blocks, 64 * kCholWaves, 0, s>>>(cov, D, M, first_ok, level, lbuf, prec, logdet);
+  constexpr int NW = chol_waves<DP>();
+  if (M <= NW) {
+    chol_one_kernel<DP><<<1, 64 * NW, 0, s>>>(cov, D, M, first_ok, level, prec, logdet);
+    return;
+  }
+  const int blocks = (M + NW - 1) / NW;
+  chol_try_kernel<DP><<<blocks, 64 * NW, 0, s>>>(cov, D, M, first_ok, lbuf);
+  const bool inline_level = M <= kCholLevelInline;
+  if (!inline_level) chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
+  chol_finish_kernel<DP><<<blocks, 64 * NW, 0, s>>>(cov, D, M, first_ok, inline_level ? nullptr : level,
+                                                    lbuf, prec, logdet);
 }
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
@@ -915,7 +1077,7 @@ void launch_take_status(unsigned* sticky, uint32_t* out, hipStream_t s) {
 
 void launch_finalize(const FinalizeArgs& a, hipStream_t s) {
   finalize_kernel<<<dim3((a.K + kFinWaves - 1) / kFinWaves, a.B), 64 * kFinWaves, 0, s>>>(a);
-  if (a.cov == TIED) finalize_tied_kernel<<<dim3(a.D, a.B), 64, 0, s>>>(a);
+  if (a.cov == TIED) finalize_tied_kernel<<<dim3(a.D, a.B), 64 * kTiedWaves, 0, s>>>(a);
   if (a.cov == FULL) finalize_full_kernel<<<dim3(a.K, a.B), 256, 0, s>>>(a);
 }
 

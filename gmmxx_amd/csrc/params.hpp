@@ -20,6 +20,8 @@ struct PrepArgs {
   void* w_lo;              // [B][K][EP] (bf16 path)
   void* w_aug;             // [B][K][32] (spherical bf16 path)
   float4* cconst;          // [B][K]
+  const float* gram;       // tied EM: XᵀX [B][D][D] (or null)
+  double* shift;           // with gram: [B][D] row terms -½ Σ_j P_rj (XᵀX)_rj
 };
 
 struct CombineArgs {
@@ -82,8 +84,6 @@ void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, 
 int launch_combine(const CombineArgs& a, hipStream_t s);  // returns the per-batch block count
 int combine_blocks(int64_t N);
 void launch_ll_reduce(const double* ll_part, int count, double inv_total, float* out, hipStream_t s);
-// out[b] = -½ Σ_ij P_b[i][j] G_b[i][j] = -½ Σ_n x_nᵀ P_b x_n (G = XᵀX), in double.
-void launch_tied_ll_shift(const float* prec, const float* gram, int B, int D, double* out, hipStream_t s);
 // out = Σ over slices of part[slice][M], in a fixed order; tmp (optional, tmp_floats
 // long) lets many slices be summed in parallel groups first.
 void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s,
