@@ -337,7 +337,7 @@ def _api(covariance_type):
                    compute_labels=compute_labels, generator=generator, approx_top_k=approx_top_k,
                    kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol,
                    record_all_lower_bounds=record_all_lower_bounds)
-    run.__name__ = f"batch_gmm_{covariance_type.capitalize()}_hip"
+    run.__name__ = f"batch_gmm_{ {'diag': 'Diagonal'}.get(covariance_type, covariance_type.capitalize()) }_hip"
     run.__doc__ = (f"{covariance_type} soft EM on the HIP engine; signature and return value of "
                    f"the reference's batch_gmm_*_torch_native (chunk/Triton knobs are accepted and ignored).")
     return run
@@ -347,3 +347,45 @@ batch_gmm_Spherical_hip = _api("spherical")
 batch_gmm_Diagonal_hip = _api("diag")
 batch_gmm_Tied_hip = _api("tied")
 batch_gmm_Full_hip = _api("full")
+
+
+# The reference's names for the same entry points (gmmxx/torch_fallback.py:3339-3520):
+# the batch_gmm_* wrappers and their *_torch_native bodies both run the HIP engine here.
+batch_gmm_Spherical = batch_gmm_Spherical_torch_native = batch_gmm_spherical = batch_gmm_Spherical_hip
+batch_gmm_Diagonal = batch_gmm_Diagonal_torch_native = batch_gmm_diagonal = batch_gmm_diag = batch_gmm_Diagonal_hip
+batch_gmm_Tied = batch_gmm_Tied_torch_native = batch_gmm_tied = batch_gmm_Tied_hip
+batch_gmm_Full = batch_gmm_Full_torch_native = batch_gmm_full = batch_gmm_Full_hip
+
+
+def _chunked(covariance_type, what):
+    """<cov>_<assign|score_samples|predict_proba>_torch_native_chunked
+    (gmmxx/torch_fallback.py:780-1345) on the HIP kernels: (x, means, covariances,
+    weights) on the GPU; chunk sizes are accepted and ignored (the library tiles
+    rows and components itself).  bf16/fp16 x is computed in fp32, as the
+    reference's chunked functions do."""
+    def run(x, means, variances, weights, *, chunk_size_N=32768, chunk_size_K=1024):
+        xd = x if x.dtype == torch.float32 else x.to(torch.float32)
+        args = (covariance_type, xd, means, variances, weights)
+        if what == "assign":
+            return _hip.score(*args, want_scores=False, want_labels=True)[1]
+        if what == "score_samples":
+            return _hip.score(*args, want_scores=True, want_labels=False)[0]
+        return _hip.predict_proba(*args)
+    prefix = {"diag": "diagonal"}.get(covariance_type, covariance_type)
+    run.__name__ = f"{prefix}_{what}_torch_native_chunked"
+    run.__doc__ = _chunked.__doc__
+    return run
+
+
+spherical_assign_torch_native_chunked = _chunked("spherical", "assign")
+spherical_score_samples_torch_native_chunked = _chunked("spherical", "score_samples")
+spherical_predict_proba_torch_native_chunked = _chunked("spherical", "predict_proba")
+diagonal_assign_torch_native_chunked = _chunked("diag", "assign")
+diagonal_score_samples_torch_native_chunked = _chunked("diag", "score_samples")
+diagonal_predict_proba_torch_native_chunked = _chunked("diag", "predict_proba")
+tied_assign_torch_native_chunked = _chunked("tied", "assign")
+tied_score_samples_torch_native_chunked = _chunked("tied", "score_samples")
+tied_predict_proba_torch_native_chunked = _chunked("tied", "predict_proba")
+full_assign_torch_native_chunked = _chunked("full", "assign")
+full_score_samples_torch_native_chunked = _chunked("full", "score_samples")
+full_predict_proba_torch_native_chunked = _chunked("full", "predict_proba")

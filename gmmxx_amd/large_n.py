@@ -330,3 +330,66 @@ def predict_proba_large_n(x_cpu, means, covs, weights, covariance_type, *, devic
                           compute_dtype=None):
     """Responsibilities (1, N, K) fp32 on the host (gmmxx/large_n.py:2259-2502)."""
     return _infer(x_cpu, means, covs, weights, covariance_type, device, chunk_size_N, "proba", compute_dtype)
+
+
+# ---------------------------------------------------------------------------
+# The reference module's function names (gmmxx/large_n.py:866, :1907, :2078,
+# :2259) over the functions above.  ``dtype`` is the compute dtype request
+# (bf16 selects the spherical bf16 engine, anything else fp32; float64 raises);
+# the Triton/backend knobs and chunk_size_K are accepted and ignored: every
+# chunk runs on the HIP kernels.  ``chunk_size_N`` is the streamed chunk.
+# ---------------------------------------------------------------------------
+
+_IGNORED = {"chunk_size_K", "kmeans_use_triton", "gmm_use_triton", "use_triton", "backend", "legacy_no_triton"}
+
+
+def _reject_unknown(kw):
+    for key in kw:
+        if key not in _IGNORED:
+            raise TypeError(f"unexpected keyword argument {key!r}")
+
+
+def batch_gmm_largeN_cpu(x_cpu, n_components, *, covariance_type, device, dtype, max_iters=100, tol=1e-4,
+                         verbose=False, init_params="kmeans", reg_covar=1e-6, chunk_size_N=1 << 20,
+                         kmeans_init_iters=10, kmeans_init_tol=1e-4, min_weight=1e-8, compute_labels=True,
+                         max_init_samples=65536, approx_top_k=None, seed=0, **ignored):
+    """fit_large_n under the reference's name and keyword set (gmmxx/large_n.py:866-890)."""
+    _reject_unknown(ignored)
+    return fit_large_n(x_cpu, n_components, covariance_type, device=device, max_iters=max_iters, tol=tol,
+                       verbose=verbose, init_params=init_params, reg_covar=reg_covar, chunk_size_N=chunk_size_N,
+                       min_weight=min_weight, compute_labels=compute_labels, max_init_samples=max_init_samples,
+                       seed=seed, approx_top_k=approx_top_k, kmeans_init_iters=kmeans_init_iters,
+                       kmeans_init_tol=kmeans_init_tol, compute_dtype=dtype)
+
+
+def _ref_infer(fn, x_cpu, means, variances, weights, covariance_type, device, dtype, chunk_size_N,
+               return_triton_used, return_backend_used, ignored):
+    _reject_unknown(ignored)
+    out = fn(x_cpu, means, variances, weights, covariance_type, device=device, chunk_size_N=chunk_size_N,
+             compute_dtype=dtype)
+    if return_backend_used:
+        return out, "hip"
+    if return_triton_used:
+        return out, False
+    return out
+
+
+def large_n_predict_cpu(x_cpu, means, variances, weights, *, covariance_type, device, dtype, chunk_size_N=1 << 20,
+                        return_triton_used=False, return_backend_used=False, **ignored):
+    """predict_large_n under the reference's name (gmmxx/large_n.py:1907-1923)."""
+    return _ref_infer(predict_large_n, x_cpu, means, variances, weights, covariance_type, device, dtype,
+                      chunk_size_N, return_triton_used, return_backend_used, ignored)
+
+
+def large_n_score_samples_cpu(x_cpu, means, variances, weights, *, covariance_type, device, dtype,
+                              chunk_size_N=1 << 20, return_triton_used=False, return_backend_used=False, **ignored):
+    """score_samples_large_n under the reference's name (gmmxx/large_n.py:2078)."""
+    return _ref_infer(score_samples_large_n, x_cpu, means, variances, weights, covariance_type, device, dtype,
+                      chunk_size_N, return_triton_used, return_backend_used, ignored)
+
+
+def large_n_predict_proba_cpu(x_cpu, means, variances, weights, *, covariance_type, device, dtype,
+                              chunk_size_N=1 << 20, return_triton_used=False, return_backend_used=False, **ignored):
+    """predict_proba_large_n under the reference's name (gmmxx/large_n.py:2259)."""
+    return _ref_infer(predict_proba_large_n, x_cpu, means, variances, weights, covariance_type, device, dtype,
+                      chunk_size_N, return_triton_used, return_backend_used, ignored)

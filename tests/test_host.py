@@ -346,3 +346,50 @@ def test_estimator_routes_long_host_input_to_streaming():
     gm = GMMXX(n_components=3, backend="hip", device="cuda", chunk_size_data_cpu=100)
     assert gm._is_large_cpu_stream_input(torch.zeros((1, 101, 2)))
     assert not gm._is_large_cpu_stream_input(torch.zeros((1, 100, 2)))
+
+
+# The reference package's function-level names in this build's scope
+# (gmmxx/__init__.py:1-34, cuda_ops.py:11-87): every one must exist here.
+REFERENCE_NAMES = [
+    "GMMXX", "batch_gmm_Spherical", "batch_gmm_Spherical_torch_native", "batch_gmm_Diagonal",
+    "batch_gmm_Diagonal_torch_native", "batch_gmm_Full", "batch_gmm_Full_torch_native", "batch_gmm_Tied",
+    "batch_gmm_Tied_torch_native", "batch_gmm_spherical", "batch_gmm_diagonal", "batch_gmm_diag",
+    "batch_gmm_full", "batch_gmm_tied", "diagonal_assign_torch_native_chunked",
+    "diagonal_predict_proba_torch_native_chunked", "diagonal_score_samples_torch_native_chunked",
+    "full_assign_torch_native_chunked", "full_predict_proba_torch_native_chunked",
+    "full_score_samples_torch_native_chunked", "tied_assign_torch_native_chunked",
+    "tied_predict_proba_torch_native_chunked", "tied_score_samples_torch_native_chunked",
+    "batch_gmm_largeN_cpu", "large_n_predict_cpu", "large_n_score_samples_cpu", "large_n_predict_proba_cpu",
+]
+REFERENCE_OPS = [
+    "canary_add_offset", "spherical_assign", "spherical_logsumexp", "spherical_resp", "soft_update_spherical",
+    "finalize_spherical", "fused_spherical", "approx_topk_update_spherical", "diag_assign", "diag_logsumexp",
+    "diag_resp", "finalize_diag", "tied_assign", "tied_logsumexp", "tied_resp", "full_assign",
+    "full_logsumexp", "full_resp",
+]
+
+
+def test_reference_function_names_exported():
+    import gmmxx_amd
+    missing = [n for n in REFERENCE_NAMES if not callable(getattr(gmmxx_amd, n, None))]
+    assert not missing
+    assert set(REFERENCE_NAMES) <= set(gmmxx_amd.__all__)
+    # the aliases are the HIP engine's entry points
+    assert gmmxx_amd.batch_gmm_diag is gmmxx_amd.batch_gmm_Diagonal_hip
+    assert gmmxx_amd.batch_gmm_Full_torch_native is gmmxx_amd.batch_gmm_Full_hip
+
+
+def test_hip_ops_mirrors_cuda_ops_names():
+    from gmmxx_amd import hip_ops
+    missing = [n for n in REFERENCE_OPS if not callable(getattr(hip_ops, n, None))]
+    assert not missing
+    assert set(REFERENCE_OPS) <= set(hip_ops.__all__)
+    assert hip_ops.HipRuntimeFallback.__mro__[1].__name__ == "HipRuntimeError"
+
+
+def test_reference_named_wrappers_reject_unknown_keywords():
+    import gmmxx_amd
+    with pytest.raises(TypeError):
+        gmmxx_amd.large_n_predict_cpu(torch.zeros(1, 4, 2), torch.zeros(1, 2, 2), torch.ones(1, 2),
+                                      torch.ones(1, 2) / 2, covariance_type="spherical", device="cpu",
+                                      dtype=torch.float32, not_a_knob=1)
