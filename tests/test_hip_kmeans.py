@@ -111,3 +111,24 @@ def test_em_fit_default_init_is_kmeans(hip):
     _, m2, _, _, info2 = em.fit(to_dev(x), 7, "diag", max_iters=3, tol=0.0, init_params="random")
     assert info2["init_source"] == "random"
     assert math.isfinite(info["lower_bound"]) and info["lower_bound"] >= info2["lower_bound"] - 1.0
+
+
+def test_lloyd_stop_rule_mid_run_vs_float64(hip):
+    """The HIP Lloyd loop stops at the same iteration as a float64 brute force
+    for a tol that falls between two consecutive moves (see
+    tests/test_oracle_kmeans.py), with the same centres."""
+    from tests.test_oracle_kmeans import _lloyd_f64
+    import math
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn((2, 300, 3), generator=g)
+    x[:, :150] += 1.5
+    seeds = x[:, :5].clone()
+    _, _, shifts, _ = _lloyd_f64(x, seeds, 12, 0.0)
+    i = [i for i in range(2, len(shifts) - 1) if shifts[i] < 0.5 * shifts[i - 1] and shifts[i] > 1e-3][0]
+    tol = math.sqrt(shifts[i] * shifts[i - 1])
+    e_c, e_it, _, _ = _lloyd_f64(x, seeds, 12, tol)
+    print(f"[lloyd stop rule] tol {tol:.4g}, float64 stops at {e_it}", flush=True)
+    xd = x.to(DEV)
+    means, nk, sx, sq, it = kmeans.lloyd(xd, "spherical", seeds.to(DEV), 12, tol, kmeans._HardStats(xd, "spherical", 5))
+    assert it == e_it
+    torch.testing.assert_close(means.cpu().double(), torch.from_numpy(e_c), rtol=1e-5, atol=1e-5)

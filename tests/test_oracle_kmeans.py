@@ -144,3 +144,58 @@ def test_hard_label_init_stats_vs_float64(cov):
             else:
                 exp = (dj.T @ dj / len(dj) if len(dj) else gcov) + reg * np.eye(d)
             np.testing.assert_allclose(c[bi, j].double().numpy(), exp, rtol=1e-5, atol=1e-5)
+
+
+def _lloyd_f64(x, c, max_iters, tol):
+    """float64 numpy Lloyd: assignment to the nearest centre (first on ties),
+    centre = mean of its rows (empty keeps its place); stop after max_iters, or
+    once tol > 0 and the largest centre move is below tol.  Returns (centres,
+    iterations, per-iteration largest moves, per-iteration k-means objective)."""
+    xn, cn = x.double().numpy(), c.double().numpy().copy()
+    bsz, k = cn.shape[0], cn.shape[1]
+    shifts, objs = [], []
+    for it in range(1, max_iters + 1):
+        new = cn.copy()
+        obj = 0.0
+        for b in range(bsz):
+            dist = ((xn[b][:, None, :] - cn[b][None, :, :]) ** 2).sum(-1)
+            lab = dist.argmin(-1)
+            obj += float(dist[np.arange(len(lab)), lab].sum())
+            for j in range(k):
+                if (lab == j).any():
+                    new[b, j] = xn[b][lab == j].mean(0)
+        shift = float(np.sqrt(((new - cn) ** 2).sum(-1)).max())
+        cn = new
+        shifts.append(shift)
+        objs.append(obj)
+        if tol > 0.0 and shift < tol:
+            return cn, it, shifts, objs
+    return cn, max_iters, shifts, objs
+
+
+def test_lloyd_stop_rule_mid_run_vs_float64():
+    """The stop rule as implemented: on overlapping clusters Lloyd moves for
+    several iterations; a tol between two consecutive float64 moves (far from
+    both) must stop the oracle at the same iteration with the same centres, the
+    k-means objective never increases, and tol = 0 runs every iteration.  (The
+    rule itself is flash-kmeans'; that package is not in the reference tree, so
+    its agreement with flash-kmeans is not pinned -- see the module docstring of
+    gmmxx_amd/kmeans.py.)"""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn((2, 300, 3), generator=g)
+    x[:, :150] += 1.5
+    seeds = x[:, :5].clone()
+    _, _, shifts, objs = _lloyd_f64(x, seeds, 12, 0.0)
+    assert all(b <= a + 1e-9 for a, b in zip(objs, objs[1:])), "objective must not increase"
+    # a stopping point in the middle of the run, tol halfway (geometric) between two moves
+    cand = [i for i in range(2, len(shifts) - 1) if shifts[i] < 0.5 * shifts[i - 1] and shifts[i] > 1e-3]
+    assert cand, f"no well-separated consecutive moves in {shifts}"
+    i = cand[0]
+    tol = math.sqrt(shifts[i] * shifts[i - 1])
+    e_c, e_it, _, _ = _lloyd_f64(x, seeds, 12, tol)
+    assert 1 < e_it < 12
+    labels, means, it = torch_ref.lloyd(x, seeds, max_iters=12, tol=tol)
+    assert it == e_it
+    np.testing.assert_allclose(means.double().numpy(), e_c, rtol=1e-5, atol=1e-5)
+    _, means0, it0 = torch_ref.lloyd(x, seeds, max_iters=7, tol=0.0)
+    assert it0 == 7
