@@ -245,11 +245,17 @@ def single_pass(cfg):
         if cfg["D"] == 128 and 256 < cfg["K"] <= 1024 and os.environ.get("GMMXX_HIP_NO_COOP") != "1":
             return "sph_bf16_coop_kernel"
         return None
-    # fp32 x: one tile pass when a workgroup (8 waves of CW components) holds all K
+    # fp32 x: one tile pass when a workgroup (8 waves of CW components) holds all K;
+    # with 2..4 such component tiles (spherical, tied, diag at D <= 64) the tiles
+    # exchange row partials in one cooperative pass
     cw = 16 if cfg["cov"] == "full" or (cfg["cov"] == "diag" and cfg["D"] > 64) else 32
     one_tile = cfg["K"] <= 8 * cw and not (cfg["cov"] == "diag" and cfg["D"] > 64)
     if one_tile and os.environ.get("GMMXX_HIP_NO_SINGLE") != "1":
         return "em_tile_kernel"
+    xch = (8 * cw < cfg["K"] <= 32 * cw and (cfg["cov"] in ("spherical", "tied") or
+                                             (cfg["cov"] == "diag" and cfg["D"] <= 64)))
+    if xch and os.environ.get("GMMXX_HIP_NO_XCH") != "1":
+        return "em_tile_kernel (exchange)"
     return None
 
 

@@ -49,6 +49,9 @@ struct Plan {
   bool fused = false;        // EM iteration as one fused pass (small K; em_fused.hip)
   bool coop = false;         // EM iteration as one cooperative pass (spherical bf16, D = 128; em_coop.hip)
   bool single = false;       // EM iteration as one tile pass (fp32 x, all K in one workgroup; MODE_STATS_LSE)
+  bool xch = false;          // EM iteration as one tile pass whose 2..4 component tiles exchange row partials
+  int xslices = 0;           // xch: row slices per batch (grid xslices·ktiles x B, all resident)
+  int64_t xrows = 0;         // xch: rows per slice
   int cG = 0, cNG = 0, cspb = 0;   // coop: workgroups per group, groups, row items per batch
   int64_t crows = 0;         // coop: rows per item
   int fslices = 0;           // fused: one wave per row slice
@@ -174,6 +177,23 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   // the two passes.
   const char* no_single = getenv("GMMXX_HIP_NO_SINGLE");
   q.single = !sph_bf && q.ktiles == 1 && !(q.cov == DIAG && q.DP >= 128) && !(no_single && no_single[0] == '1');
+  // Exchange single pass (fp32 spherical, tied, diag at D <= 64; 2..4 component
+  // tiles of 8 waves): the workgroups of a row slice swap per-row (max, sum)
+  // partials, so x is read once per iteration.  They must be co-resident: the
+  // grid is at most the device's resident capacity of that kernel.
+  // GMMXX_HIP_NO_XCH=1 selects the two passes.
+  const char* no_xch = getenv("GMMXX_HIP_NO_XCH");
+  q.xch = !q.bf && (q.cov == SPH || q.cov == TIED || (q.cov == DIAG && q.DP <= 64)) && q.ktiles >= 2 &&
+          q.ktiles <= kMaxCoopGroup && q.nw == 8 && !(no_xch && no_xch[0] == '1');
+  if (q.xch) {
+    int64_t xs = tile_xch_capacity(q.cov, q.DP) / ((int64_t)q.ktiles * q.B);
+    xs = std::min(xs, std::max<int64_t>(1, row_blocks / kMinBlocksPerSlice));
+    q.xch = xs >= 1;
+    if (q.xch) {
+      q.xrows = ((q.N + xs - 1) / xs + kBN - 1) / kBN * kBN;
+      q.xslices = (int)((q.N + q.xrows - 1) / q.xrows);
+    }
+  }
   // XᵀX: about 512 workgroups in all, slices of whole 16-row groups (the kernel's
   // four waves take four rows at a time).
   int64_t gs = std::max<int64_t>(1, std::min<int64_t>((512 + q.B - 1) / q.B, (q.N + 255) / 256));
@@ -198,11 +218,12 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_rowaux = take(sph_bf && q.DP >= 128 ? BN * 16 : 0);
   q.o_pms = take((size_t)std::max(q.ktiles, q.lktiles) * BN * 8);
   q.o_pidx = take((size_t)q.ktiles * BN * 4);
-  q.o_pstats = take((size_t)std::max({q.slices, q.fslices, q.cspb}) * BK * q.JP * 4);
+  q.o_pstats = take((size_t)std::max({q.slices, q.fslices, q.cspb, q.xslices}) * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
   // (+B: the tied EM iteration's per-batch log-likelihood shift, after the row partials)
-  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices}) + q.D + 1) * 8);
-  q.o_xch = take(q.coop ? (size_t)q.cNG * kRing * q.cG * kBN * 8 : 0);
+  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices, q.xslices}) + q.D + 1) * 8);
+  q.o_xch = take(q.coop ? (size_t)q.cNG * kRing * q.cG * kBN * 8
+                        : (q.xch ? (size_t)q.B * q.xslices * kRing * q.ktiles * kBN * 8 : 0));
   // [0] status of the last cooperative pass (zeroed by its launcher), [1] sticky
   // status since the last gmmxx_hip_take_status
   q.o_flags = take(8);
@@ -309,22 +330,39 @@ int run_coop(const Plan& pl, const void* x, void* ws, hipStream_t s) {
   if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no cooperative kernel for this shape");
   return check_hip("cooperative single-pass kernel");
 }
+// Exchange single pass: partial statistics per row slice and partial log-likelihoods.
+// em: the EM iteration's pass (tied logits without the row forms, as tile_args).
+int run_xch(const Plan& pl, const void* x, void* ws, hipStream_t s, bool em = true) {
+  TileArgs t = tile_args(pl, x, ws, em);
+  t.rows_per_slice = pl.xrows;
+  t.xch = at<uint64_t>(ws, pl.o_xch);
+  t.status = at<unsigned>(ws, pl.o_flags);
+  t.spin_limit = 1 << 20;   // as the cooperative pass (GMMXX_HIP_COOP_SPIN_LIMIT overrides)
+  if (const char* sl = getenv("GMMXX_HIP_COOP_SPIN_LIMIT")) t.spin_limit = atoi(sl);
+  const int64_t nwords = (int64_t)pl.B * pl.xslices * kRing * pl.ktiles * kBN;
+  const int rc = launch_tile_xch(pl.cov, pl.DP, t, dim3(pl.xslices * pl.ktiles, pl.B), nwords, s);
+  if (rc == -2) return fail(GMMXX_ERR_HIP, "cooperative launch of the exchange pass failed");
+  if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no exchange tile kernel for this shape");
+  return check_hip("exchange single-pass kernel");
+}
 const unsigned* coop_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags); }
 unsigned* sticky_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags) + 1; }
-int stat_slices(const Plan& pl) { return pl.fused ? pl.fparts : (pl.coop ? pl.cspb : pl.slices); }
+int stat_slices(const Plan& pl) {
+  return pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.xch ? pl.xslices : pl.slices));
+}
 // The tile-partial buffer is free once the statistics are being reduced: it is
 // the scratch of the grouped slice reduction.
 float* red_tmp(const Plan& pl, void* ws) { return at<float>(ws, pl.o_pms); }
 int64_t red_tmp_floats(const Plan& pl) { return (int64_t)std::max(pl.ktiles, pl.lktiles) * pl.B * pl.N * 2; }
 int ll_parts(const Plan& pl) {
-  return pl.B * (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.single ? pl.slices : pl.cblocks)));
+  return pl.B * (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.xch ? pl.xslices : (pl.single ? pl.slices : pl.cblocks))));
 }
 // Where an EM iteration's tied -½ tr(P XᵀX) terms go: after the log-likelihood
 // partials of its log-normaliser pass (the single-pass or the combine kernel's),
 // so the one reduction sums both; null where no pass leaves the row forms out.
 double* tied_shift(const Plan& pl, void* ws) {
   if (pl.cov != TIED || pl.fused || pl.coop) return nullptr;
-  return at<double>(ws, pl.o_ll) + (pl.single ? ll_parts(pl) : pl.B * pl.cblocks);
+  return at<double>(ws, pl.o_ll) + ((pl.single || pl.xch) ? ll_parts(pl) : pl.B * pl.cblocks);
 }
 
 // Prelude / parameter packing, Cholesky (tied, full) and the tied row forms.
@@ -566,6 +604,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
                      tied_shift(pl, ws));
     case GMMXX_PHASE_LSE_TILE: {
       if (pl.coop) return run_coop(pl, x, ws, s);
+      if (pl.xch) return run_xch(pl, x, ws, s, /*em=*/true);
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if (pl.single) {
         if (run_tile(pl, MODE_STATS_LSE, t, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
@@ -576,11 +615,11 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip(pl.fused ? "fused tile kernel" : "log-normaliser tile kernel");
     }
     case GMMXX_PHASE_COMBINE: {
-      if (pl.fused || pl.coop || pl.single) {  // the single pass already produced per-slice log-likelihoods
+      if (pl.fused || pl.coop || pl.single || pl.xch) {  // the single pass already produced per-slice log-likelihoods
         int parts = ll_parts(pl);
         if (tied_shift(pl, ws)) parts += pl.B * pl.D;   // -½ tr(P XᵀX) rows, from the prepare phase
         launch_ll_reduce(at<double>(ws, pl.o_ll), parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
-        if (pl.coop) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), lower_bound, s);
+        if (pl.coop || pl.xch) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), lower_bound, s);
         return check_hip("log-likelihood reduction");
       }
       CombineArgs c{};
@@ -598,7 +637,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip("combine");
     }
     case GMMXX_PHASE_STATS_TILE: {
-      if (pl.fused || pl.coop || pl.single) return GMMXX_OK;  // statistics came out of the single pass
+      if (pl.fused || pl.coop || pl.single || pl.xch) return GMMXX_OK;  // statistics came out of the single pass
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if (run_tile(pl, MODE_STATS, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
@@ -612,7 +651,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     case GMMXX_PHASE_FINALIZE:
       // A cooperative pass that timed out leaves the parameters as they were.
       finalize(pl, ws, gram, reg_covar, min_weight, pl.N, means, covs, weights, s,
-               pl.coop ? coop_status(pl, ws) : nullptr);
+               (pl.coop || pl.xch) ? coop_status(pl, ws) : nullptr);
       return check_hip("finalize");
     default:
       return fail(GMMXX_ERR_INVALID_ARGUMENT, "unknown phase");
@@ -662,9 +701,11 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
-  if (pl.fused || pl.coop || pl.single) {
+  if (pl.fused || pl.coop || pl.single || pl.xch) {
     if (pl.coop) {
       if ((rc = run_coop(pl, x, ws, s))) return rc;
+    } else if (pl.xch) {
+      if ((rc = run_xch(pl, x, ws, s, /*em=*/false))) return rc;
     } else if (pl.single) {
       if (run_tile(pl, MODE_STATS_LSE, tile_args(pl, x, ws), s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");
@@ -672,7 +713,7 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
       return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
     }
     launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0, ll_sum, s);
-    if (pl.coop) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), ll_sum, s);
+    if (pl.coop || pl.xch) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), ll_sum, s);
     launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                          at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
     if ((rc = check_hip("fused statistics pass"))) return rc;

@@ -15,9 +15,11 @@ enum Cov { SPH = 0, DIAG = 1, TIED = 2, FULL = 3 };
 // rest zero, against the top-k log-normaliser.
 // MODE_STATS_LSE / MODE_PROBA_LSE: the statistics / responsibility pass with the
 // row log-normalisers formed inside the workgroup (every component is in it).
+// MODE_STATS_XCH: the statistics pass with the row log-normalisers merged across
+// the workgroups that hold a row slice's component tiles (exchanged partials).
 enum Mode {
   MODE_LSE = 0, MODE_STATS = 1, MODE_PROBA = 2, MODE_LSE_IDX = 3, MODE_STATS_TOPK = 4, MODE_STATS_LSE = 5,
-  MODE_PROBA_LSE = 6
+  MODE_PROBA_LSE = 6, MODE_STATS_XCH = 7
 };
 
 constexpr float kLog2e = 1.4426950408889634f;

@@ -154,7 +154,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr bool LSE = (MODE == MODE_LSE || MODE == MODE_LSE_IDX);
   constexpr bool WANT_IDX = MODE == MODE_LSE_IDX;
   constexpr bool SLSE = MODE == MODE_STATS_LSE || MODE == MODE_PROBA_LSE;
-  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK || MODE == MODE_STATS_LSE;
+  constexpr bool XCH = MODE == MODE_STATS_XCH;
+  constexpr bool STATS = MODE == MODE_STATS || MODE == MODE_STATS_TOPK || MODE == MODE_STATS_LSE || XCH;
   constexpr bool TOPK = MODE == MODE_STATS_TOPK;
   using Dm = Dims<COV, DP, BF>;
   constexpr int EP = Dm::EP, JP = Dm::JP, J = Dm::J, S = Dm::S;
@@ -176,7 +177,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   // barrier per block.  Full covariance stages three 176-column parts per row and
   // keeps a single buffer (a second barrier per block) so that two workgroups of
   // two waves fit a CU's LDS twice over.
-  constexpr int NB = (COV == FULL) ? 1 : PD + 1;
+  // The exchange pass keeps block i-1 staged for its M-GEMM while block i is
+  // computed and block i+1 loads: one more buffer.
+  constexpr int NB = (COV == FULL) ? 1 : PD + 1 + (XCH ? 1 : 0);
   constexpr int XS = DP + (BF ? 8 : 4);                  // staged-row stride, elements
   constexpr int QS = kBN + 8;                            // ψᵀ row stride, bf16 elements
   using FT = typename std::conditional<BF, __bf16, float>::type;
@@ -205,9 +208,9 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   __shared__ float lse_s[NB * kBN];
   __shared__ float thr_s[TOPK ? NB * kBN : 1];     // top-k threshold logit and index per row
   __shared__ int thri_s[TOPK ? NB * kBN : 1];
-  __shared__ float red_m[(LSE || SLSE) ? 2 * kBN * 8 : 1];   // [parity][row][wave]
-  __shared__ float red_s[(LSE || SLSE) ? 2 * kBN * 8 : 1];
-  __shared__ __align__(16) float lsw[SLSE ? 8 * kBN : 4];     // [wave][row] merged log-normalisers
+  __shared__ float red_m[(LSE || SLSE || XCH) ? 2 * kBN * 8 : 1];   // [parity][row][wave]
+  __shared__ float red_s[(LSE || SLSE || XCH) ? 2 * kBN * 8 : 1];
+  __shared__ __align__(16) float lsw[(SLSE || XCH) ? 8 * kBN : 4];   // [wave][row] merged log-normalisers
   __shared__ int red_i[WANT_IDX ? 2 * kBN * 8 : 1];
 
   const int tid = threadIdx.x;
@@ -468,8 +471,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
       } else {
         if (cc == 0) rowq_s[buf * kBN + r] = 0.f;
       }
-      if constexpr (!LSE) {
-        if (cc == 0 && !SLSE) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
+      if constexpr (!LSE && !SLSE && !XCH) {
+        if (cc == 0) lse_s[buf * kBN + r] = (n < rend) ? a.lse2[(size_t)b * N + n] : INFINITY;
       }
       if constexpr (TOPK) {
         if (cc == 0) {
@@ -638,6 +641,57 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     }
   };
 
+  // M-GEMM on split bf16 operands (fp32 x): r in three parts (A element j = 4rt + v
+  // is data row 16rt + 4g + v), ψ tiles read from the staged split φ rows of
+  // buffer bx with the transposing load (rows 4g..4g+3 and 16+4g..16+4g+3, the
+  // same order).
+  auto mgemm_x3 = [&](const float (&rr)[CT][2][4], int bx) {
+    if constexpr (STATS && X3) {
+        bf16x8 ra[3][CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          uint32_t q[3][4];
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int v = 0; v < 4; v += 2)
+              split3x2(rr[ct][rt][v], rr[ct][rt][v + 1], q[0][2 * rt + v / 2], q[1][2 * rt + v / 2],
+                       q[2][2 * rt + v / 2]);
+#pragma unroll
+          for (int p = 0; p < 3; ++p) ra[p][ct] = __builtin_bit_cast(bf16x8, make_uint4(q[p][0], q[p][1], q[p][2], q[p][3]));
+        }
+        // ψ tile jt = 16 consecutive φ columns (diag: x then x², spherical/tied: x) or the
+        // augmented columns at EP.
+        // Full: ψ = [x | products | 1] from φ = [products | x]; the last tile holds
+        // products 128..135 (column groups 0, 1) and the constant chunk at EP
+        // (groups 2, 3, whose lane offsets are 8 and 12).
+        auto psi_col = [&](int jt) {
+          constexpr int XT16 = DP / 16;
+          if constexpr (COV == DIAG) return jt < XT16 ? DP + 16 * jt : (jt < 2 * XT16 ? 16 * (jt - XT16) : EP);
+          else if constexpr (COV == FULL) return jt == 0 ? S : (jt < JT - 1 ? 16 * (jt - 1) : ((li & 3) < 2 ? S - 8 : EP - 8));
+          else return jt < XT16 ? 16 * jt : EP;
+        };
+        const __bf16* tb = phx + (bx * kBN + 4 * g + (li >> 2)) * EPS + 4 * (li & 3);
+#pragma unroll
+        for (int jt = 0; jt < JT; ++jt) {
+          const int c0 = psi_col(jt);
+          bf16x8 bq[3];
+#pragma unroll
+          for (int p = 0; p < 3; ++p)
+            bq[p] = cat_v4s(tr16(tb + p * X3P + c0), tr16(tb + p * X3P + 16 * EPS + c0));
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[2], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[2][ct], bq[0], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[1][ct], bq[1], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[1], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[1][ct], bq[0], acc[ct][jt]);
+            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[0], acc[ct][jt]);
+          }
+        }
+    }
+  };
+
   auto epilogue = [&](const Acc& A, int bx, int pb, int64_t n0) {
     if constexpr (LSE) {
       // Per data row: wave max (and first argmax) by max-only lane swaps, then one
@@ -759,51 +813,7 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
           }
       }
       if constexpr (STATS && X3) {
-        // M-GEMM on split bf16 operands: r in three parts (A element j = 4rt + v is
-        // data row 16rt + 4g + v), ψ tiles read from the staged split φ rows with the
-        // transposing load (rows 4g..4g+3 and 16+4g..16+4g+3, the same order).
-        bf16x8 ra[3][CT];
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          uint32_t q[3][4];
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int v = 0; v < 4; v += 2)
-              split3x2(rr[ct][rt][v], rr[ct][rt][v + 1], q[0][2 * rt + v / 2], q[1][2 * rt + v / 2],
-                       q[2][2 * rt + v / 2]);
-#pragma unroll
-          for (int p = 0; p < 3; ++p) ra[p][ct] = __builtin_bit_cast(bf16x8, make_uint4(q[p][0], q[p][1], q[p][2], q[p][3]));
-        }
-        // ψ tile jt = 16 consecutive φ columns (diag: x then x², spherical/tied: x) or the
-        // augmented columns at EP.
-        // Full: ψ = [x | products | 1] from φ = [products | x]; the last tile holds
-        // products 128..135 (column groups 0, 1) and the constant chunk at EP
-        // (groups 2, 3, whose lane offsets are 8 and 12).
-        auto psi_col = [&](int jt) {
-          constexpr int XT16 = DP / 16;
-          if constexpr (COV == DIAG) return jt < XT16 ? DP + 16 * jt : (jt < 2 * XT16 ? 16 * (jt - XT16) : EP);
-          else if constexpr (COV == FULL) return jt == 0 ? S : (jt < JT - 1 ? 16 * (jt - 1) : ((li & 3) < 2 ? S - 8 : EP - 8));
-          else return jt < XT16 ? 16 * jt : EP;
-        };
-        const __bf16* tb = phx + (bx * kBN + 4 * g + (li >> 2)) * EPS + 4 * (li & 3);
-#pragma unroll
-        for (int jt = 0; jt < JT; ++jt) {
-          const int c0 = psi_col(jt);
-          bf16x8 bq[3];
-#pragma unroll
-          for (int p = 0; p < 3; ++p)
-            bq[p] = cat_v4s(tr16(tb + p * X3P + c0), tr16(tb + p * X3P + 16 * EPS + c0));
-#pragma unroll
-          for (int ct = 0; ct < CT; ++ct) {
-            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[2], acc[ct][jt]);
-            acc[ct][jt] = mfma_bf16(ra[2][ct], bq[0], acc[ct][jt]);
-            acc[ct][jt] = mfma_bf16(ra[1][ct], bq[1], acc[ct][jt]);
-            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[1], acc[ct][jt]);
-            acc[ct][jt] = mfma_bf16(ra[1][ct], bq[0], acc[ct][jt]);
-            acc[ct][jt] = mfma_bf16(ra[0][ct], bq[0], acc[ct][jt]);
-          }
-        }
+        mgemm_x3(rr, bx);
       } else if constexpr (STATS) {
         // M-GEMM: each ψ fragment is loaded once and used by every component tile.
         if constexpr (BF) {
@@ -871,7 +881,157 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   if constexpr (PIPE) {
     if (nblk > 0) cur = egemm(0);
   }
-  for (int64_t ib = 0; ib < nblk; ++ib) {
+  if constexpr (XCH) {
+    // The a.ktiles workgroups of row slice `slice` (members ktile = 0..ktiles-1,
+    // consecutive logical ids, so one XCD when the grid allows) each hold one
+    // component tile; per block they swap this workgroup's per-row (max, sum)
+    // through global memory, as the cooperative spherical kernel does
+    // (em_coop.hip: one 64-bit relaxed agent-scope word (max, ±sum) per row, the
+    // sign of the sum carrying the round parity (j / kRing) & 1, a ring of kRing
+    // slots, bounded waits that set *status and stop).  Lag one block: block i's
+    // partials are published after its E-GEMM, and block i-1 -- whose logits wait
+    // in registers and whose staged rows wait in the extra LDS buffer -- is
+    // finished (log-normalisers merged in member order, responsibilities,
+    // M-GEMM) after that, when the partners' words for it are a block old.
+    // Every wave merges the partials itself, so the only barriers are the two a
+    // one-tile pass has.  A slot is rewritten kRing blocks later, after the
+    // partners' words of two blocks later have been seen, by which time every
+    // wave of every partner has read it.
+    const int gm = a.ktiles;
+    uint64_t* const gw = a.xch + ((size_t)b * (gridDim.x / gm) + slice) * kRing * gm * kBN;
+    float l2p[CT][2][4];
+    float Mp = 0.f, Sp = 0.f;     // this workgroup's (max, sum) of the previous block (lanes < 32)
+    uint64_t words[kMaxCoopGroup];
+    bool dead = false;            // a wait timed out: no further waits
+    auto load_words = [&](int64_t j) {
+      const uint64_t* src = gw + (j % kRing) * gm * kBN + lane;
+#pragma unroll
+      for (int p = 0; p < kMaxCoopGroup; ++p)
+        words[p] = (p < gm && p != ktile && lane < kBN)
+                       ? __hip_atomic_load(src + p * kBN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : 0;
+    };
+    auto finish = [&](int64_t j, int bxp, int64_t n0p) {
+      const bool odd = (j / kRing) & 1;
+      auto ready = [&]() {
+        bool ok = true;
+#pragma unroll
+        for (int p = 0; p < kMaxCoopGroup; ++p) {
+          const float t = __uint_as_float((uint32_t)(words[p] >> 32));
+          if (p < gm && p != ktile && lane < kBN) ok = ok && (odd ? t < 0.f : t > 0.f);
+        }
+        return ok;
+      };
+      int spins = 0;
+      while (!dead && (a.spin_limit < 0 || __ballot(!ready()) != 0)) {
+        if (++spins > a.spin_limit ||
+            ((spins & 63) == 0 && __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+          dead = true;
+          if (lane == 0) __hip_atomic_fetch_or(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        load_words(j);
+      }
+      float M = -INFINITY, S = 0.f;
+#pragma unroll
+      for (int p = 0; p < kMaxCoopGroup; ++p) {
+        if (p < gm) {
+          const float vm = p == ktile ? Mp : __uint_as_float((uint32_t)words[p]);
+          const float vs = p == ktile ? Sp : fabsf(__uint_as_float((uint32_t)(words[p] >> 32)));
+          const float Mn = fmaxf(M, vm);
+          S = S * fast_exp2(M - Mn) + vs * fast_exp2(vm - Mn);
+          M = Mn;
+        }
+      }
+      if (lane < kBN) {
+        const bool valid = n0p + lane < rend;
+        const float l = M + __log2f(S);
+        lsw[wave * kBN + lane] = valid ? l : INFINITY;
+        if (ktile == 0 && wave == 0 && valid) ll_acc += (double)l;
+      }
+      // The wave's own LDS writes above are read back by its other lanes below.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float rr[CT][2][4];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const f32x4 lv = ld16<f32x4>(&lsw[wave * kBN + 16 * rt + 4 * g]);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) rr[ct][rt][v] = fast_exp2(l2p[ct][rt][v] - lv[v]);
+      }
+      mgemm_x3(rr, bxp);
+    };
+    for (int64_t ib = 0; ib < nblk; ++ib) {
+      const int bx = (int)(ib % NB);
+      const int64_t n0 = rbeg + ib * kBN;
+      const bool ahead = ib + PD < nblk;
+      if (ahead) fetch(n0 + PD * kBN);
+      // E-GEMM of block ib: its logits and this wave's (max, Σ 2^(l2 - max)) per row
+      const Acc A = egemm(bx);
+      float l2c[CT][2][4];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            l2c[ct][rt][v] = logit(cS[ct], A.t[ct][rt][v], rowq_s[bx * kBN + 16 * rt + 4 * g + v]);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float m = kLogFloor;
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) m = fmaxf(m, l2c[ct][rt][v]);
+          m = group_max<16>(m);
+          float sm = 0.f;
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) sm += fast_exp2(l2c[ct][rt][v] - m);
+          sm = group_sum<16>(sm);
+          if (li == 0) {
+            red_m[(16 * rt + 4 * g + v) * 8 + wave] = m;
+            red_s[(16 * rt + 4 * g + v) * 8 + wave] = sm;
+          }
+        }
+      // The partners' words of block ib - 1, loaded after the E-GEMM: loaded at
+      // the top of the iteration they were often not there yet and the reloads
+      // cost more (measured at C3: 3.15 against 3.34 ms per pass).
+      if (ib > 0 && !dead) load_words(ib - 1);
+      __syncthreads();
+      // This workgroup's (max, sum) per row of block ib (lanes < 32), merged by
+      // every wave; wave 0 publishes it to the group.
+      float M = kLogFloor, S = 0.f;
+      if (lane < kBN) {
+        for (int w = 0; w < nw; ++w) M = fmaxf(M, red_m[lane * 8 + w]);
+        for (int w = 0; w < nw; ++w) S += red_s[lane * 8 + w] * fast_exp2(red_m[lane * 8 + w] - M);
+      }
+      if (wave == 0 && lane < kBN && gm > 1) {
+        const float tagged = ((ib / kRing) & 1) ? -S : S;
+        const uint64_t word = (uint64_t)__float_as_uint(M) | ((uint64_t)__float_as_uint(tagged) << 32);
+        __hip_atomic_store(gw + ((ib % kRing) * gm + ktile) * kBN + lane, word, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (ib > 0) finish(ib - 1, (int)((ib - 1) % NB), n0 - kBN);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) l2p[ct][rt][v] = l2c[ct][rt][v];
+      Mp = M;
+      Sp = S;
+      if (ahead) stash((int)((ib + PD) % NB), n0 + PD * kBN);
+      __syncthreads();
+    }
+    if (nblk > 0) {
+      if (!dead) load_words(nblk - 1);
+      finish(nblk - 1, (int)((nblk - 1) % NB), rbeg + (nblk - 1) * kBN);
+    }
+  }
+  for (int64_t ib = 0; ib < (XCH ? 0 : nblk); ++ib) {
     const int bx = (int)(ib % NB), pb = (int)(ib & 1);
     const int64_t n0 = rbeg + ib * kBN;
     const bool ahead = ib + PD < nblk;
@@ -913,9 +1073,10 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         }
       }
   }
-  if constexpr (MODE == MODE_STATS_LSE) {
-    // This workgroup's rows: Σ lse (natural log), one partial per (batch, slice).
-    if (wave == 0) {
+  if constexpr (MODE == MODE_STATS_LSE || XCH) {
+    // This workgroup's rows: Σ lse (natural log), one partial per (batch, slice)
+    // (exchange pass: from the first member of the group).
+    if (wave == 0 && ktile == 0) {
       double t = ll_acc;
 #pragma unroll
       for (int off = 32; off >= 1; off /= 2) t += __shfl_xor(t, off);
@@ -957,6 +1118,67 @@ static int launch_tile_dp(int dp, int mode, const TileArgs& a, dim3 grid, int nw
     case 128: return launch_tile_t<COV, XT, 128>(mode, a, grid, nw, s);
     default: return -1;
   }
+}
+
+// ---- exchange pass (MODE_STATS_XCH): cooperative launch, all workgroups resident ----
+
+__global__ void xch_zero_kernel(uint64_t* w, int64_t n, unsigned* status) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) w[i] = 0;
+  if (i == 0) *status = 0u;
+}
+
+template <int COV, int DP>
+static const void* xch_fn() {
+  return reinterpret_cast<const void*>(em_tile_kernel<COV, float, DP, cw_for<COV, DP, false>(), MODE_STATS_XCH>);
+}
+
+static const void* xch_kernel(int cov, int dp) {
+  switch (cov) {
+    case SPH:
+      return dp == 16 ? xch_fn<SPH, 16>() : dp == 32 ? xch_fn<SPH, 32>() : dp == 64 ? xch_fn<SPH, 64>()
+                                          : dp == 128 ? xch_fn<SPH, 128>() : nullptr;
+    case DIAG:
+      return dp == 16 ? xch_fn<DIAG, 16>() : dp == 32 ? xch_fn<DIAG, 32>() : dp == 64 ? xch_fn<DIAG, 64>() : nullptr;
+    case TIED:
+      return dp == 16 ? xch_fn<TIED, 16>() : dp == 32 ? xch_fn<TIED, 32>() : dp == 64 ? xch_fn<TIED, 64>() : nullptr;
+    default:
+      return nullptr;
+  }
+}
+
+int tile_xch_capacity(int cov, int dp) {
+  const void* fn = xch_kernel(cov, dp);
+  if (!fn) return 0;
+  static int cache[64][4][8] = {};
+  int ndev = 0, dev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0 || hipGetDevice(&dev) != hipSuccess || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;   // no device visible: workspace sizing only
+  }
+  int& c = cache[dev][cov & 3][(dp / 16) & 7];
+  if (c > 0) return c;
+  int cus = 0, per = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, 64 * 8, 0) != hipSuccess || cus <= 0 || per <= 0) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  c = cus * per;
+  return c;
+}
+
+int launch_tile_xch(int cov, int dp, const TileArgs& a, dim3 grid, int64_t nwords, hipStream_t s) {
+  const void* fn = xch_kernel(cov, dp);
+  if (!fn) return -1;
+  xch_zero_kernel<<<(unsigned)((nwords + 255) / 256 + 1), 256, 0, s>>>(a.xch, nwords, a.status);
+  TileArgs args = a;
+  void* params[] = {&args};
+  if (hipLaunchCooperativeKernel(fn, grid, dim3(64 * 8), params, 0, s) != hipSuccess) {
+    (void)hipGetLastError();
+    return -2;
+  }
+  return 0;
 }
 
 int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s) {

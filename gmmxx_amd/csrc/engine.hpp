@@ -31,6 +31,9 @@ struct TileArgs {
   const float* thr2;           // [B][N] STATS_TOPK: each row's k-th largest logit (log2)
   const int* thr_idx;          // [B][N] STATS_TOPK: its component index (ties: lower index first)
   int hard;                    // STATS_TOPK with k = 1: r = 1 for component thr_idx, else 0
+  uint64_t* xch;               // STATS_XCH: [B][slices][kRing][ktiles][32] (max, ±sum) words, zeroed by the launcher
+  unsigned* status;            // STATS_XCH: nonzero after a timed-out wait (zeroed by the launcher)
+  int spin_limit;              // STATS_XCH: polls per wait (negative: give up at once)
 };
 
 // Approximate top-k EM (params.hip): per row of the (B, N, K) log2 logits, the
@@ -43,6 +46,12 @@ int topk_select_blocks(int64_t N);
 
 int tile_cw(int cov, int dp, int bf);
 int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s);
+// MODE_STATS_XCH (fp32 spherical / diag (DP <= 64) / tied, 8 waves): resident
+// workgroups per device (0 when the instance does not exist), and the
+// cooperative launch (zeroes the exchange words and status first); -2 when the
+// cooperative launch fails.
+int tile_xch_capacity(int cov, int dp);
+int launch_tile_xch(int cov, int dp, const TileArgs& a, dim3 grid, int64_t nwords, hipStream_t s);
 // Spherical bf16 kernel (em_sph_bf16.hip): dp in {32, 64} with nw in {2, 4, 8};
 // dp 128 with nw 8 (and 16 for MODE_LSE).
 int launch_sph_bf16(int dp, int nw, int mode, const TileArgs& a, dim3 grid, hipStream_t s);
