@@ -43,7 +43,7 @@ class HipRuntimeFallback(HipRuntimeError):
     raises this, unless ``GMMXX_HIP_NO_FALLBACK=1``, in which case the plain
     HipRuntimeError propagates.  Nothing in this package catches it -- there is
     no CPU or PyTorch path to fall to; a dispatcher that has one (the
-    reference's) catches it and re-resolves."""
+    reference's dispatch_kernel) catches it and re-resolves to torch."""
 
 
 def no_fallback() -> bool:
