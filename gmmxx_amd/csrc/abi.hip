@@ -346,7 +346,23 @@ int run_xch(const Plan& pl, const void* x, void* ws, hipStream_t s, bool em = tr
   return check_hip("exchange single-pass kernel");
 }
 const unsigned* coop_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags); }
+bool single_pass(const Plan& pl) { return pl.fused || pl.coop || pl.single || pl.xch; }
 unsigned* sticky_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags) + 1; }
+// The log-likelihood sum of a single pass, folded into the slice reduction;
+// cooperative and exchange passes also carry their status (a timed-out wait
+// makes the value NaN and is added to the sticky word).
+LlFold ll_fold(const Plan& pl, void* ws, int parts, double inv_total, float* out) {
+  LlFold ll{};
+  ll.part = at<double>(ws, pl.o_ll);
+  ll.count = parts;
+  ll.inv_total = inv_total;
+  ll.out = out;
+  if (pl.coop || pl.xch) {
+    ll.status = at<unsigned>(ws, pl.o_flags);
+    ll.sticky = at<unsigned>(ws, pl.o_flags) + 1;
+  }
+  return ll;
+}
 int stat_slices(const Plan& pl) {
   return pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.xch ? pl.xslices : pl.slices));
 }
@@ -615,13 +631,9 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip(pl.fused ? "fused tile kernel" : "log-normaliser tile kernel");
     }
     case GMMXX_PHASE_COMBINE: {
-      if (pl.fused || pl.coop || pl.single || pl.xch) {  // the single pass already produced per-slice log-likelihoods
-        int parts = ll_parts(pl);
-        if (tied_shift(pl, ws)) parts += pl.B * pl.D;   // -½ tr(P XᵀX) rows, from the prepare phase
-        launch_ll_reduce(at<double>(ws, pl.o_ll), parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound, s);
-        if (pl.coop || pl.xch) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), lower_bound, s);
-        return check_hip("log-likelihood reduction");
-      }
+      // A single pass already produced per-slice log-likelihoods: they are summed
+      // by the reduce phase's launch (one launch fewer per iteration).
+      if (single_pass(pl)) return GMMXX_OK;
       CombineArgs c{};
       c.B = pl.B;
       c.ktiles = pl.lktiles;
@@ -644,8 +656,15 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip("statistics tile kernel");
     }
     case GMMXX_PHASE_REDUCE: {
+      LlFold ll{};
+      if (single_pass(pl)) {
+        int parts = ll_parts(pl);
+        if (tied_shift(pl, ws)) parts += pl.B * pl.D;   // -½ tr(P XᵀX) rows, from the prepare phase
+        ll = ll_fold(pl, ws, parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound);
+      }
       launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
-                           at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
+                           at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl),
+                           single_pass(pl) ? &ll : nullptr);
       return check_hip("statistics reduction");
     }
     case GMMXX_PHASE_FINALIZE:
@@ -712,10 +731,9 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
     } else if (run_fused(pl, tile_args(pl, x, ws), s) != 0) {
       return fail(GMMXX_ERR_UNSUPPORTED, "no fused kernel for this shape");
     }
-    launch_ll_reduce(at<double>(ws, pl.o_ll), ll_parts(pl), 1.0, ll_sum, s);
-    if (pl.coop || pl.xch) launch_coop_check(coop_status(pl, ws), sticky_status(pl, ws), ll_sum, s);
+    const LlFold ll = ll_fold(pl, ws, ll_parts(pl), 1.0, ll_sum);
     launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
-                         at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
+                         at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl), &ll);
     if ((rc = check_hip("fused statistics pass"))) return rc;
   } else {
     if ((rc = lse_pass(pl, x, ws, nullptr, nullptr, true, s))) return rc;

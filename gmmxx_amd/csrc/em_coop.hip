@@ -127,15 +127,6 @@ __global__ void coop_zero_kernel(unsigned* p, int n, unsigned* status) {
   if (i == n) *status = 0u;
 }
 
-// After a pass: a timed-out wait turns *value into NaN and is added to the
-// sticky status word, which gmmxx_hip_take_status reads and clears.
-__global__ void coop_check_kernel(const unsigned* status, unsigned* sticky, float* value) {
-  if (threadIdx.x == 0 && *status != 0u) {
-    *value = __builtin_nanf("");
-    *sticky |= *status;
-  }
-}
-
 }  // namespace
 
 // KG: largest group size the instance handles (G <= KG); the partners' words of
@@ -568,10 +559,6 @@ int coop_capacity() {
   }
   cache[dev] = cus * per;
   return cache[dev];
-}
-
-void launch_coop_check(const unsigned* status, unsigned* sticky, float* value, hipStream_t s) {
-  coop_check_kernel<<<1, 64, 0, s>>>(status, sticky, value);
 }
 
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s) {

@@ -90,9 +90,6 @@ struct CoopArgs {
 // Resident workgroups of the cooperative kernel on the current device.
 int coop_capacity();
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s);
-// *value = NaN when the cooperative pass reported a timed-out wait (status != 0),
-// and *sticky |= status.
-void launch_coop_check(const unsigned* status, unsigned* sticky, float* value, hipStream_t s);
 
 // Greedy k-means++ seeding (kmeans.hip).  Row sample [B][S][D] fp32; the first
 // centre's row index per batch and T uniform draws per later centre are inputs.

@@ -727,9 +727,26 @@ __global__ void ll_reduce_kernel(const double* ll_part, int count, double inv_to
 // added in wave order.
 constexpr int kRedWaves = 16;
 // blockIdx.y selects a group of `per` consecutive slices (written to out + y*M).
+// ll.out != null: the grid has one more workgroup (the last), which does the
+// log-likelihood reduction of LlFold instead.
 __global__ __launch_bounds__(64 * kRedWaves) void reduce_slices_kernel(const float* part, int slices, int64_t M,
-                                                                       float* out, int per) {
+                                                                       float* out, int per, LlFold ll) {
   __shared__ float red[kRedWaves][64];
+  if (ll.out && blockIdx.x == gridDim.x - 1) {
+    __shared__ double scratch[32];
+    double t = 0.0;
+    for (int i = threadIdx.x; i < ll.count; i += blockDim.x) t += ll.part[i];
+    t = block_sum(t, scratch);
+    if (threadIdx.x == 0) {
+      float v = (float)(t * ll.inv_total);
+      if (ll.status && *ll.status != 0u) {
+        v = __builtin_nanf("");
+        *ll.sticky |= *ll.status;
+      }
+      ll.out[0] = v;
+    }
+    return;
+  }
   const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
   const int64_t i = (int64_t)blockIdx.x * 64 + lane;
   part += (size_t)blockIdx.y * per * M;
@@ -1037,7 +1054,7 @@ void launch_ll_reduce(const double* ll_part, int count, double inv_total, float*
 }
 
 void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s, float* tmp,
-                          int64_t tmp_floats) {
+                          int64_t tmp_floats, const LlFold* ll) {
   // Many slices over few outputs: first sum groups of slices in parallel into
   // tmp (fixed grouping, so the result stays deterministic), then the groups.
   const int64_t blocks = (M + 63) / 64;
@@ -1045,14 +1062,17 @@ void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, 
   while (groups < 64 && blocks * groups < 512 && slices / (2 * groups) >= 4 * kRedWaves &&
          (int64_t)(2 * groups) * M <= tmp_floats)
     groups *= 2;
+  const LlFold none{};
+  const LlFold lf = ll ? *ll : none;
+  const unsigned last = (unsigned)blocks + (ll ? 1u : 0u);
   if (groups == 1 || !tmp) {
-    reduce_slices_kernel<<<(unsigned)blocks, 64 * kRedWaves, 0, s>>>(part, slices, M, out, slices);
+    reduce_slices_kernel<<<last, 64 * kRedWaves, 0, s>>>(part, slices, M, out, slices, lf);
     return;
   }
   const int per = (slices + groups - 1) / groups;
   groups = (slices + per - 1) / per;  // every group non-empty
-  reduce_slices_kernel<<<dim3((unsigned)blocks, groups), 64 * kRedWaves, 0, s>>>(part, slices, M, tmp, per);
-  reduce_slices_kernel<<<(unsigned)blocks, 64 * kRedWaves, 0, s>>>(tmp, groups, M, out, groups);
+  reduce_slices_kernel<<<dim3((unsigned)blocks, groups), 64 * kRedWaves, 0, s>>>(part, slices, M, tmp, per, none);
+  reduce_slices_kernel<<<last, 64 * kRedWaves, 0, s>>>(tmp, groups, M, out, groups, lf);
 }
 
 __global__ void take_status_kernel(unsigned* sticky, uint32_t* out) {

@@ -86,8 +86,20 @@ int combine_blocks(int64_t N);
 void launch_ll_reduce(const double* ll_part, int count, double inv_total, float* out, hipStream_t s);
 // out = Σ over slices of part[slice][M], in a fixed order; tmp (optional, tmp_floats
 // long) lets many slices be summed in parallel groups first.
+// A log-likelihood reduction folded into the last slice-reduction launch (one
+// more workgroup): *out = Σ part[0 .. count) · inv_total; with status set
+// (cooperative / exchange passes) a nonzero *status turns *out into NaN and is
+// added to *sticky.
+struct LlFold {
+  const double* part;
+  int count;
+  double inv_total;
+  float* out;
+  const unsigned* status;
+  unsigned* sticky;
+};
 void launch_reduce_slices(const float* part, int slices, int64_t M, float* out, hipStream_t s,
-                          float* tmp = nullptr, int64_t tmp_floats = 0);
+                          float* tmp = nullptr, int64_t tmp_floats = 0, const LlFold* ll = nullptr);
 void launch_finalize(const FinalizeArgs& a, hipStream_t s);
 void launch_unpack(const UnpackArgs& a, int B, hipStream_t s);
 void launch_pack(const PackArgs& a, int B, hipStream_t s);
