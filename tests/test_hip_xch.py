@@ -113,3 +113,22 @@ def test_xch_timed_out_wait_keeps_parameters_and_raises(hip, monkeypatch):
     assert float(lb) == pytest.approx(e_lb, rel=1e-5)
     assert int(hip.take_status(ws).item()) == 0
     assert_params(m_d, e_m, "means", x, torch.float32)
+
+
+@pytest.mark.parametrize("n", [1, 20, 33, 385, 1000])
+def test_xch_short_slices_match_oracle(hip, n):
+    """Row slices of one or a few 32-row blocks (the pipeline's first block is
+    also its last; padded rows), two and three component tiles."""
+    for cov, d, k in (("diag", 20, 300), ("spherical", 32, 700)):
+        print(f"[xch short] {cov} N={n} D={d} K={k}", flush=True)
+        x, means, covs, w = make_problem(cov, 1, n, d, k, seed=64 + n)
+        xd = to_dev(x)
+        m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
+        lb = torch.zeros(1, device=DEV)
+        hip.em_step(cov, xd, m_d, c_d, w_d, lb)
+        e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, cov, means, covs, w)
+        torch.cuda.synchronize()
+        assert float(lb) == pytest.approx(e_lb, rel=1e-5)
+        assert_params(m_d, e_m, "means", x, torch.float32)
+        assert_params(c_d, e_c, "covs", x, torch.float32)
+        assert_params(w_d, e_w, "weights", x, torch.float32)
