@@ -17,9 +17,13 @@
 //               with the transposing load as the A operand of the M-GEMM
 //               acc += rᵀ·ψ (ψ = the staged row [x | augmented columns]).
 //
-// The two-block lag hides the exchange: wave 0 publishes block i-1 at the top
-// of iteration i and collects the partners' partials of block i-1 at its end,
-// after a whole block of MFMA work.  Members of one group must run at the same
+// The two-block lag hides the exchange: wave 1 publishes block i-1 at the top
+// of iteration i, and wave 0 collects the group's partials of block i-1 (its own
+// workgroup's word included) at its end, after a whole block of MFMA work.  The
+// two roles sit on different waves (and SIMDs) because every wave waits at the
+// block's barrier for the slowest one: split, they cost the larger of the two
+// instead of their sum (measured 4.57 -> 4.15 ms per C2 pass).  Members of one
+// group must run at the same
 // time, so the kernel launches cooperatively (all workgroups co-resident); every
 // wait is bounded (spin limit), and a wait that times out sets *status and
 // stops waiting, so the kernel always drains.  Used for 2 <= G <= 4: with one
@@ -314,9 +318,13 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
         ar[ct] = cat(tr16(rw + tr * kRS + rswz(tr, 16 * ct + c0)),
                      tr16(rw + (tr + 16) * kRS + rswz(tr + 16, 16 * ct + c0)));
       const __bf16* xr = xs + bx * kBN * XS + tr * XS + c0;
+      // B operands are read one feature tile ahead of their MFMAs, so the LDS
+      // latency of tile jt + 1 hides behind the MFMAs of tile jt.
+      bf16x8 bn = cat(tr16(xr), tr16(xr + 16 * XS));
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) {
-        const bf16x8 bq = cat(tr16(xr + 16 * jt), tr16(xr + 16 * XS + 16 * jt));
+        const bf16x8 bq = bn;
+        if (jt + 1 < JT) bn = cat(tr16(xr + 16 * (jt + 1)), tr16(xr + 16 * XS + 16 * (jt + 1)));
 #pragma unroll
         for (int ct = 0; ct < kCT; ++ct) acc[ct][jt] = mfma_bf16(ar[ct], bq, acc[ct][jt]);
       }
@@ -389,11 +397,12 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       const int r0 = i * kBN;                     // first row of block i in the item
       const bool ahead = i + 2 < nblk;
       if (ahead) fetch(r0 + 2 * kBN);
-      const bool xchg = wave == 0 && i >= 1 && i <= nblk;   // wave 0 owns block i-1's exchange
+      const bool xchg = wave == 0 && i >= 1 && i <= nblk;   // wave 0 collects block i-1
+      const bool pubw = wave == 1 && i >= 1 && i <= nblk;   // wave 1 publishes block i-1
 
-      // ---- wave 0: this workgroup's partials of block i-1, published to the group ----
+      // ---- wave 1: this workgroup's partials of block i-1, published to the group ----
       float ownM = 0.f, ownS = 0.f;
-      if (xchg) {
+      if (pubw) {
         if (lane < kBN) {
           constexpr int qb = PB ^ 1;              // parity of block i-1
           float M = red_m[(qb * kNW) * RR + lane];
@@ -420,15 +429,16 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       if constexpr (FIN) prep_r(PB_, r0 - 2 * kBN, nrows);
       if constexpr (EGM) egemm(i % kNB, T);
 
-      // ---- wave 0: the partners' words of block i-1 (published at the top of
-      // this iteration), loaded now and checked after the second half ----
+      // ---- wave 0: the group's words of block i-1 (published at the top of this
+      // iteration; this workgroup's own included), loaded now and checked after
+      // the second half ----
       uint64_t words[KG];
       const unsigned jx = seq + i - 1;
       const uint64_t* src = gxch + (jx % kRing) * G * kBN + lane;
       auto load_words = [&]() {
 #pragma unroll
         for (int p = 0; p < KG; ++p)
-          words[p] = (p < G && p != mem && lane < kBN)
+          words[p] = (p < G && lane < kBN)
                          ? __hip_atomic_load(src + p * kBN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                          : 0;
       };
@@ -459,7 +469,7 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
 #pragma unroll
             for (int p = 0; p < KG; ++p) {
               const float t = __uint_as_float((uint32_t)(words[p] >> 32));
-              if (p < G && p != mem && lane < kBN) ok = ok && (odd ? t < 0.f : t > 0.f);
+              if (p < G && lane < kBN) ok = ok && (odd ? t < 0.f : t > 0.f);
             }
             return ok;
           };
@@ -476,19 +486,17 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
             __builtin_amdgcn_s_sleep(1);
             load_words();
           }
-          // Running merge in member order, so every member gets the same bits.
+          // Every member merges the same words in member order: the same bits.
           M = -INFINITY;
+#pragma unroll
+          for (int p = 0; p < KG; ++p)
+            if (p < G) M = fmaxf(M, __uint_as_float((uint32_t)words[p]));
           S = 0.f;
 #pragma unroll
-          for (int p = 0; p < KG; ++p) {
-            if (p < G) {
-              const float vm = p == mem ? ownM : __uint_as_float((uint32_t)words[p]);
-              const float vs = p == mem ? ownS : fabsf(__uint_as_float((uint32_t)(words[p] >> 32)));
-              const float Mn = fmaxf(M, vm);
-              S = S * fast_exp2(M - Mn) + vs * fast_exp2(vm - Mn);
-              M = Mn;
-            }
-          }
+          for (int p = 0; p < KG; ++p)
+            if (p < G)
+              S += fabsf(__uint_as_float((uint32_t)(words[p] >> 32))) *
+                   fast_exp2(__uint_as_float((uint32_t)words[p]) - M);
         }
         if (lane < kBN) {
           const float l2 = M + __log2f(S);
