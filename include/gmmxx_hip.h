@@ -219,8 +219,8 @@ int gmmxx_hip_predict_proba(const gmmxx_problem* p, const void* x, const float* 
  * log-normaliser pass writes the scores and the responsibility pass reuses its
  * log-normalisers.  Replaces the estimator's predict_proba + score_samples pair
  * (gmmxx/interface.py:2138-2203, :2412-2467), each of which runs its own
- * streamed log-normaliser (gmmxx/torch_fallback.py:1279-1345, :1094-1130), and
- * the survey's fused full_proba_score. */
+ * streamed log-normaliser (gmmxx/torch_fallback.py:1279-1345, :1094-1130); one
+ * entry for every covariance type, the full-covariance pair included. */
 int gmmxx_hip_predict_proba_score(const gmmxx_problem* p, const void* x, const float* means,
                                   const float* covariances, const float* weights, float* proba,
                                   float* scores, void* workspace, int64_t workspace_bytes, void* stream);
