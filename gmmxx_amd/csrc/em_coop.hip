@@ -8,6 +8,12 @@
 // row block's per-row (max, scaled sum) partials through global memory, so the
 // E-GEMM runs once per (row, component) and its exponentials are reused:
 //
+// Both GEMMs run on the 32x32x16 bf16 MFMA (as em_fused.hip): a wave's E-GEMM
+// output is one 32-component x 32-row tile whose lane l holds 16 components of
+// row l % 32 (lane l ^ 32 the other 16), so the row maxima and sums are in-lane
+// work plus one lane swap (measured 2 % faster per C2 pass than 16x16x32 tiles,
+// whose rows spread over four lanes).
+//
 //   block i:    E-GEMM (logits l2, log2 units, as in em_sph_bf16.hip)
 //               m_w = wave row max, e = 2^(l2 - m_w) (kept in LDS as bf16), s_w = Σ e
 //               workgroup partials (M, S) per row -> published to the group
@@ -59,13 +65,17 @@ constexpr int kAug = 32;           // augmented k-chunk width (bf16 columns)
 constexpr float kHuge = 1e30f;     // "minus infinity" that stays finite through MFMA
 constexpr int kNW = 8;             // waves per workgroup
 constexpr int kCW = 32;            // components per wave
-constexpr int kCT = 2;             // 16-wide component tiles per wave
 constexpr int kNB = 5;             // staged row blocks: i-2 .. i+2
 constexpr int kRS = 48;            // r row stride (bf16): 32 components + padding
 
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
 
 template <typename T>
 __device__ __forceinline__ T ld16(const void* p) { return *reinterpret_cast<const T*>(p); }
@@ -137,11 +147,11 @@ __global__ void coop_zero_kernel(unsigned* p, int n, unsigned* status) {
 // a block are loaded together into KG registers.
 template <int DP, int KG>
 __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
-  constexpr int ECH = DP / 32;                   // x chunks of the E-GEMM
-  constexpr int XS = 176;                        // staged row stride (bf16), as em_sph_bf16.hip at D = 128
+  constexpr int XK = DP / 16;                    // 16-deep k-steps over the x columns (E-GEMM)
+  constexpr int XT = DP / 32;                    // 32-wide x tiles of ψ (M-GEMM)
+  constexpr int XS = 176;                        // staged row stride (bf16)
   static_assert(DP + kAug <= XS, "row does not fit the staging stride");
-  constexpr int JT = DP / 16 + 1;                // ψ = [x | augmented columns 0..15]
-  constexpr int JP = 16 * JT;
+  constexpr int JP = DP + 16;                    // statistics columns: x | augmented 0..15
   constexpr int CPR = DP / 8;                    // 16-byte chunks per row
   constexpr int NCH = kBN * CPR;                 // chunks per row block
   constexpr int NTHR = 64 * kNW;
@@ -155,16 +165,16 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
   __shared__ float red_s[2 * kNW * RR];
   __shared__ float lse_s[2 * kBN];
   // e = 2^(l2 - m_w) of the two blocks in flight, per wave and block parity, in
-  // the accumulator layout (four bf16 per lane and (ct, row tile)); kept in LDS,
+  // the accumulator layout (sixteen bf16 per lane: its components of row lr); kept in LDS,
   // which leaves the registers to the W operands and the statistics.  e is
   // rounded to bf16 here and r = e·2^(m_w - lse2) again before the M-GEMM (r is a
   // bf16 MFMA operand in any case): half the LDS bytes of fp32 e, measured 3 %
   // faster at K = 1024, with the sums and the log-normalisers still from fp32 e.
-  __shared__ uint2 es[kNW * 2 * kCT * 2 * 64];
+  __shared__ uint4 es[kNW * 2 * 2 * 64];
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
-  const int g = lane / 16, li = lane % 16;
+  const int lr = lane % 32, hf = lane / 32;     // 32x32 MFMA: row / component of a tile, k half
   const int64_t N = a.N;
   const int K = a.K, G = a.G;
 
@@ -191,11 +201,11 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     const uint4 w = make_uint4(ch == 1 ? pack2((__bf16)1.f, (__bf16)0.f) : 0u, 0u, 0u, 0u);
     *reinterpret_cast<uint4*>(xs + row * XS + DP + 8 * ch) = w;
   }
-  for (int i = tid; i < kNW * 2 * kCT * 2 * 64; i += NTHR) es[i] = make_uint2(0u, 0u);
+  for (int i = tid; i < kNW * 2 * 2 * 64; i += NTHR) es[i] = make_uint4(0u, 0u, 0u, 0u);
 
-  bf16x8 whi[kCT][ECH], wlo[kCT][ECH], waug[kCT];
-  f32x4 acc[kCT][JT];
-  float mw[2][2];          // wave row maxima of the two blocks in flight: [block parity][row tile]
+  bf16x8 whi[XK], wlo[XK], waug;
+  f32x16 accx[XT], acca;
+  float mw[2];             // wave row maxima of the two blocks in flight (row lr), per block parity
   unsigned seq = 0;        // blocks this group has exchanged before the current item
   bool dead = false;       // wave 0: a wait timed out; no further waits
 
@@ -206,29 +216,29 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     const int64_t rend = (rbeg + a.rows_per_item < N) ? rbeg + a.rows_per_item : N;
     const int nblk = (rend > rbeg) ? (int)((rend - rbeg + kBN - 1) / kBN) : 0;
 
-    // ---- resident component operands (A side of the E-GEMM): lane (li, g) holds
-    // component kbase + 16ct + li, k-group g; padding components get C = -1e30. ----
-#pragma unroll
-    for (int ct = 0; ct < kCT; ++ct) {
-      const int kk = kbase + 16 * ct + li;
+    // ---- resident component operands (A side of the E-GEMM): lane (lr, hf) holds
+    // component kbase + lr, k half hf; padding components get C = -1e30. ----
+    {
+      const int kk = kbase + lr;
       if (kk < K) {
         const size_t bk = (size_t)b * K + kk;
 #pragma unroll
-        for (int ec = 0; ec < ECH; ++ec) {
-          whi[ct][ec] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_hi) + bk * DP + 32 * ec + 8 * g);
-          wlo[ct][ec] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_lo) + bk * DP + 32 * ec + 8 * g);
+        for (int t = 0; t < XK; ++t) {
+          whi[t] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_hi) + bk * DP + 16 * t + 8 * hf);
+          wlo[t] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_lo) + bk * DP + 16 * t + 8 * hf);
         }
-        waug[ct] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * g);
+        waug = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * hf);
       } else {
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int e = 0; e < 8; ++e) {
 #pragma unroll
-          for (int ec = 0; ec < ECH; ++ec) { whi[ct][ec][s] = (__bf16)0.f; wlo[ct][ec][s] = (__bf16)0.f; }
-          waug[ct][s] = (__bf16)((8 * g + s) == 6 ? -kHuge : 0.f);
+          for (int t = 0; t < XK; ++t) { whi[t][e] = (__bf16)0.f; wlo[t][e] = (__bf16)0.f; }
+          waug[e] = (__bf16)((8 * hf + e) == 6 ? -kHuge : 0.f);
         }
       }
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt) acc[ct][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int xt = 0; xt < XT; ++xt) accx[xt] = f32x16{};
+      acca = f32x16{};
     }
     double ll = 0.0;
 
@@ -282,106 +292,86 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
 
     // Responsibilities of block i-2 (parity pb, first row rf): r = e · 2^(m_w - lse2)
     // with e read back (bf16) from this wave's LDS slot, rounded to bf16 and staged
-    // row-major for the transposing reads of the M-GEMM.
+    // row-major for the transposing reads of the M-GEMM.  Lane (lr, hf) holds
+    // components 8u + 4hf + (0..3), u = 0..3, of row lr.
     auto prep_r = [&](auto PB_, int rf, int nr) {
       constexpr int pb = decltype(PB_)::value;
-      float f[2];
+      const float l2 = lse_s[pb * kBN + lr];     // read unconditionally: no branch around the LDS load
+      const float f = (rf + lr < nr) ? fast_exp2(mw[pb] - l2) : 0.f;
+      const uint4* ew = es + ((wave * 2 + pb) * 2) * 64 + lane;
+      __bf16* rrow = rs + wave * kBN * kRS + lr * kRS;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int r = 16 * h + li;
-        const float l2 = lse_s[pb * kBN + r];   // read unconditionally: no branch around the LDS load
-        f[h] = (rf + r < nr) ? fast_exp2(mw[pb][h] - l2) : 0.f;
-      }
-      __bf16* rw = rs + wave * kBN * kRS;
-      const uint2* ew = es + ((wave * 2 + pb) * kCT * 2) * 64 + lane;
+      for (int hq = 0; hq < 2; ++hq) {
+        const uint4 q = ew[hq * 64];
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-      for (int ct = 0; ct < kCT; ++ct)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const uint2 q = ew[(ct * 2 + h) * 64];
-          const f32x2 e01 = __builtin_convertvector(__builtin_bit_cast(bf16x2, q.x), f32x2);
-          const f32x2 e23 = __builtin_convertvector(__builtin_bit_cast(bf16x2, q.y), f32x2);
-          const f32x4 e = f32x4{e01[0], e01[1], e23[0], e23[1]};
-          const int r = 16 * h + li;
-          const uint2 pk = make_uint2(cvt2(e[0] * f[h], e[1] * f[h]), cvt2(e[2] * f[h], e[3] * f[h]));
-          *reinterpret_cast<uint2*>(rw + r * kRS + rswz(r, 16 * ct + 4 * g)) = pk;
+        for (int uu = 0; uu < 2; ++uu) {
+          const f32x2 e01 = __builtin_convertvector(__builtin_bit_cast(bf16x2, w4[2 * uu]), f32x2);
+          const f32x2 e23 = __builtin_convertvector(__builtin_bit_cast(bf16x2, w4[2 * uu + 1]), f32x2);
+          const uint2 pk = make_uint2(cvt2(e01[0] * f, e01[1] * f), cvt2(e23[0] * f, e23[1] * f));
+          *reinterpret_cast<uint2*>(rrow + rswz(lr, 8 * (2 * hq + uu) + 4 * hf)) = pk;
         }
+      }
     };
-    // M-GEMM of a staged block: A = r[component 16ct + li][rows 4g..4g+3, 16+4g..16+4g+3],
-    // B = ψ of the same rows, feature 16jt + li (the k order of both operands matches).
+    // Transposing-read addresses of the 32x32x16 operands: lane i of 16-lane group
+    // G reads rows 8 (G / 2) + i / 4 (+4) of a k-step and columns 16 (G % 2) + 4 (i % 4).
+    const int G16 = lane / 16, i16 = lane % 16;
+    const int trow = 8 * (G16 >> 1) + (i16 >> 2), tcol = 16 * (G16 & 1) + 4 * (i16 & 3);
+    // M-GEMM of a staged block in two k-steps of 16 rows: acc += rᵀ·ψ, ψ = the staged
+    // rows [x | augmented columns 0..31].
     auto mgemm = [&](int bx) {
       const __bf16* rw = rs + wave * kBN * kRS;
-      bf16x8 ar[kCT];
-      const int tr = 4 * g + (li >> 2), c0 = 4 * (li & 3);
+      const __bf16* xw = xs + bx * kBN * XS;
 #pragma unroll
-      for (int ct = 0; ct < kCT; ++ct)
-        ar[ct] = cat(tr16(rw + tr * kRS + rswz(tr, 16 * ct + c0)),
-                     tr16(rw + (tr + 16) * kRS + rswz(tr + 16, 16 * ct + c0)));
-      const __bf16* xr = xs + bx * kBN * XS + tr * XS + c0;
-      // B operands are read one feature tile ahead of their MFMAs, so the LDS
-      // latency of tile jt + 1 hides behind the MFMAs of tile jt.
-      bf16x8 bn = cat(tr16(xr), tr16(xr + 16 * XS));
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int r0 = 16 * s2 + trow;
+        const bf16x8 ar = cat(tr16(rw + r0 * kRS + rswz(r0, tcol)), tr16(rw + (r0 + 4) * kRS + rswz(r0 + 4, tcol)));
+        bf16x8 bn = cat(tr16(xw + r0 * XS + tcol), tr16(xw + (r0 + 4) * XS + tcol));
 #pragma unroll
-      for (int jt = 0; jt < JT; ++jt) {
-        const bf16x8 bq = bn;
-        if (jt + 1 < JT) bn = cat(tr16(xr + 16 * (jt + 1)), tr16(xr + 16 * XS + 16 * (jt + 1)));
-#pragma unroll
-        for (int ct = 0; ct < kCT; ++ct) acc[ct][jt] = mfma_bf16(ar[ct], bq, acc[ct][jt]);
+        for (int xt = 0; xt <= XT; ++xt) {
+          const bf16x8 bq = bn;
+          if (xt + 1 <= XT) bn = cat(tr16(xw + r0 * XS + 32 * (xt + 1) + tcol), tr16(xw + (r0 + 4) * XS + 32 * (xt + 1) + tcol));
+          if (xt < XT) accx[xt] = mfma32(ar, bq, accx[xt]);
+          else acca = mfma32(ar, bq, acca);
+        }
       }
     };
-    // E-GEMM C = W·φᵀ of a staged block: lane (li, g) gets components 16ct + 4g + v
-    // of row 16h + li.
-    auto egemm = [&](int bx, f32x4 (&T)[kCT][2]) {
-      const __bf16* xr = xs + bx * kBN * XS + li * XS + 8 * g;
+    // E-GEMM C = W·φᵀ of a staged block: lane (lr, hf), register v holds component
+    // 8(v/4) + 4hf + v%4 of row lr.
+    auto egemm = [&](int bx) -> f32x16 {
+      const __bf16* xr = xs + bx * kBN * XS + lr * XS + 8 * hf;
+      f32x16 T = mfma32(waug, ld16<bf16x8>(xr + DP), f32x16{});
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bf16x8 xa = ld16<bf16x8>(xr + 16 * h * XS + DP);
-#pragma unroll
-        for (int ct = 0; ct < kCT; ++ct) T[ct][h] = mfma_bf16(waug[ct], xa, f32x4{0.f, 0.f, 0.f, 0.f});
+      for (int t = 0; t < XK; ++t) {
+        const bf16x8 xv = ld16<bf16x8>(xr + 16 * t);
+        T = mfma32(whi[t], xv, T);
+        T = mfma32(wlo[t], xv, T);
       }
-#pragma unroll
-      for (int ec = 0; ec < ECH; ++ec) {
-        bf16x8 xv[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) xv[h] = ld16<bf16x8>(xr + 16 * h * XS + 32 * ec);
-#pragma unroll
-        for (int ct = 0; ct < kCT; ++ct)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) T[ct][h] = mfma_bf16(whi[ct][ec], xv[h], T[ct][h]);
-#pragma unroll
-        for (int ct = 0; ct < kCT; ++ct)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) T[ct][h] = mfma_bf16(wlo[ct][ec], xv[h], T[ct][h]);
-      }
+      return T;
     };
     // Wave row maxima m_w, e = 2^(l2 - m_w) (kept in this wave's LDS slot of the
-    // block parity) and the wave's row sums for the workgroup combine.
-    auto lse_epilogue = [&](const f32x4 (&T)[kCT][2], auto PB_) {
+    // block parity) and the wave's row sums for the workgroup combine: a row's 32
+    // components sit in lanes lr and lr + 32.
+    auto lse_epilogue = [&](const f32x16& T, auto PB_) {
       constexpr int pb = decltype(PB_)::value;
-      uint2* ew = es + ((wave * 2 + pb) * kCT * 2) * 64 + lane;
+      float m = T[0];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float m = T[0][h][0];
+      for (int v = 1; v < 16; ++v) m = fmaxf(m, T[v]);
+      m = lanes_op<32, true>(m);
+      float e[16];
 #pragma unroll
-        for (int ct = 0; ct < kCT; ++ct)
+      for (int v = 0; v < 16; ++v) e[v] = fast_exp2(T[v] - m);
+      float ps[4];
 #pragma unroll
-          for (int v = 0; v < 4; ++v) m = fmaxf(m, T[ct][h][v]);
-        m = lanes_op<32, true>(lanes_op<16, true>(m));
-        float sum = 0.f;
-#pragma unroll
-        for (int ct = 0; ct < kCT; ++ct) {
-          f32x4 e;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) e[v] = fast_exp2(T[ct][h][v] - m);
-          sum += (e[0] + e[1]) + (e[2] + e[3]);
-          ew[(ct * 2 + h) * 64] = make_uint2(cvt2(e[0], e[1]), cvt2(e[2], e[3]));
-        }
-        sum = lanes_op<32, false>(lanes_op<16, false>(sum));
-        mw[pb][h] = m;
-        // The four lanes of a row hold the same values: all of them store (no branch).
-        red_m[(pb * kNW + wave) * RR + 16 * h + li] = m;
-        red_s[(pb * kNW + wave) * RR + 16 * h + li] = sum;
-      }
+      for (int u = 0; u < 4; ++u) ps[u] = (e[4 * u] + e[4 * u + 1]) + (e[4 * u + 2] + e[4 * u + 3]);
+      const float sum = lanes_op<32, false>((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      uint4* ew = es + ((wave * 2 + pb) * 2) * 64 + lane;
+      ew[0] = make_uint4(cvt2(e[0], e[1]), cvt2(e[2], e[3]), cvt2(e[4], e[5]), cvt2(e[6], e[7]));
+      ew[64] = make_uint4(cvt2(e[8], e[9]), cvt2(e[10], e[11]), cvt2(e[12], e[13]), cvt2(e[14], e[15]));
+      mw[pb] = m;
+      // Both lanes of a row hold the same values: both store (no branch).
+      red_m[(pb * kNW + wave) * RR + lr] = m;
+      red_s[(pb * kNW + wave) * RR + lr] = sum;
     };
     if (nblk > 0) { fetch(0); stash(0); }
     if (nblk > 1) { fetch(kBN); stash(1); }
@@ -425,9 +415,9 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       }
 
       // ---- responsibilities of block i-2 with the E-GEMM of block i ----
-      f32x4 T[kCT][2];
+      f32x16 T;
       if constexpr (FIN) prep_r(PB_, r0 - 2 * kBN, nrows);
-      if constexpr (EGM) egemm(i % kNB, T);
+      if constexpr (EGM) T = egemm(i % kNB);
 
       // ---- wave 0: the group's words of block i-1 (published at the top of this
       // iteration; this workgroup's own included), loaded now and checked after
@@ -528,19 +518,18 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     else { step(T_{}, F_{}, P0{}, i); step(T_{}, F_{}, P1{}, i + 1); }
     seq += (unsigned)nblk;
 
-    // ---- the item's partial statistics (lane (li, g): component 4g + v of the
-    // tile, feature 16jt + li) and log-likelihood (natural log) ----
+    // ---- the item's partial statistics (lane (lr, hf), register v: component
+    // 8(v/4) + 4hf + v%4 of the wave, feature 32xt + lr) and log-likelihood ----
 #pragma unroll
-    for (int ct = 0; ct < kCT; ++ct)
+    for (int v = 0; v < 16; ++v) {
+      const int kk = kbase + 8 * (v / 4) + 4 * hf + (v % 4);
+      if (kk < K) {
+        float* dst = a.part_stats + (((size_t)sl * a.B + b) * K + kk) * JP;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int kk = kbase + 16 * ct + 4 * g + v;
-        if (kk < K) {
-          float* dst = a.part_stats + (((size_t)sl * a.B + b) * K + kk) * JP;
-#pragma unroll
-          for (int jt = 0; jt < JT; ++jt) dst[16 * jt + li] = acc[ct][jt][v];
-        }
+        for (int xt = 0; xt < XT; ++xt) dst[32 * xt + lr] = accx[xt][v];
+        if (lr < 16) dst[DP + lr] = acca[v];
       }
+    }
     if (mem == 0 && wave == 0) {
       for (int off = 32; off >= 1; off /= 2) ll += __shfl_xor(ll, off);
       if (lane == 0) a.ll_part[(size_t)b * a.spb + sl] = ll * (double)kLn2;
