@@ -454,14 +454,19 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
         float M = ownM, S = ownS;
         if (KG > 1 && G > 1) {
           const bool odd = (jx / kRing) & 1;
+          // A word is ready when its tag (the sum's sign) matches the round and its
+          // sum is neither zero (the slots start at zero) nor NaN: the same test as
+          // odd ? t < 0 : t > 0 on the float t.
+          const uint32_t want = odd ? 0x80000000u : 0u;
           auto ready = [&]() {
-            bool ok = true;
+            uint32_t bad = 0u;
 #pragma unroll
             for (int p = 0; p < KG; ++p) {
-              const float t = __uint_as_float((uint32_t)(words[p] >> 32));
-              if (p < G && lane < kBN) ok = ok && (odd ? t < 0.f : t > 0.f);
+              const uint32_t hi = (uint32_t)(words[p] >> 32);
+              const uint32_t b = ((hi ^ want) >> 31) | (((hi << 1) - 1u) >= 0xFF000000u ? 1u : 0u);
+              bad |= (p < G) ? b : 0u;
             }
-            return ok;
+            return lane >= kBN || bad == 0u;
           };
           // A negative spin limit gives up at the first wait (the host's way to
           // exercise the timeout path without a stalled partner).
