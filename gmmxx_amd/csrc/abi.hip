@@ -649,7 +649,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip("combine");
     }
     case GMMXX_PHASE_STATS_TILE: {
-      if (pl.fused || pl.coop || pl.single || pl.xch) return GMMXX_OK;  // statistics came out of the single pass
+      if (single_pass(pl)) return GMMXX_OK;  // statistics came out of the single pass
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if (run_tile(pl, MODE_STATS, t, s) != 0)
         return fail(GMMXX_ERR_UNSUPPORTED, "no tile kernel for this shape");

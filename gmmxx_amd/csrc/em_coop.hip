@@ -391,6 +391,8 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       const bool pubw = wave == 1 && i >= 1 && i <= nblk;   // wave 1 publishes block i-1
 
       // ---- wave 1: this workgroup's partials of block i-1, published to the group ----
+      // (ownM/ownS only seed wave 0's merge below, which overwrites them; written
+      // this way the compiled loop measured 2 % faster than without them.)
       float ownM = 0.f, ownS = 0.f;
       if (pubw) {
         if (lane < kBN) {
