@@ -148,6 +148,28 @@ __device__ __forceinline__ int lanes_min_i(int v) {
 
 // Packed upper-triangle index -> (d, e) for the full covariance (DP = 16).
 
+// (max, Σ s·2^(m - max)) over the nw (1, 2 or 4) wave partials of a row,
+// unrolled for each count.
+template <int NW>
+__device__ __forceinline__ void merge_waves_n(const float* rm, const float* rsum, float& M, float& S) {
+  float m[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) m[w] = rm[w];
+  M = m[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, m[w]);
+  S = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) S += rsum[w] * fast_exp2(m[w] - M);
+}
+__device__ __forceinline__ void merge_waves(int nw, const float* rm, const float* rsum, float& M, float& S) {
+  switch (nw) {
+    case 4: merge_waves_n<4>(rm, rsum, M, S); break;
+    case 2: merge_waves_n<2>(rm, rsum, M, S); break;
+    default: merge_waves_n<1>(rm, rsum, M, S); break;
+  }
+}
+
 template <int COV, typename XT, int DP, int CW, int MODE>
 __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
   constexpr bool BF = sizeof(XT) == 2;
@@ -769,10 +791,15 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
           }
         __syncthreads();
         if (lane < kBN) {
-          float M = kLogFloor;
-          for (int w = 0; w < nw; ++w) M = fmaxf(M, red_m[lane * 8 + w]);
-          float S = 0.f;
-          for (int w = 0; w < nw; ++w) S += red_s[lane * 8 + w] * fast_exp2(red_m[lane * 8 + w] - M);
+          // Two or four waves (small K): unrolled per count (C5 pass 3 % faster);
+          // eight: the loop, which measured faster there (C4).
+          float M = kLogFloor, S = 0.f;
+          if (nw <= 4) {
+            merge_waves(nw, red_m + lane * 8, red_s + lane * 8, M, S);
+          } else {
+            for (int w = 0; w < nw; ++w) M = fmaxf(M, red_m[lane * 8 + w]);
+            for (int w = 0; w < nw; ++w) S += red_s[lane * 8 + w] * fast_exp2(red_m[lane * 8 + w] - M);
+          }
           const bool valid = n0 + lane < rend;
           const float l = M + __log2f(S);
           lsw[wave * kBN + lane] = valid ? l : INFINITY;
