@@ -465,9 +465,12 @@ def kmeans_pp(sample: torch.Tensor, n_components: int, first_idx: torch.Tensor, 
 def finalize_stats(covariance_type: str, nk: torch.Tensor, sum_x: torch.Tensor, sum_q: Optional[torch.Tensor],
                    means: torch.Tensor, covs: torch.Tensor, weights: torch.Tensor, n_rows: int, *,
                    gram_xx: Optional[torch.Tensor] = None, reg_covar: float = 1e-6,
-                   min_weight: float = 1e-8, ws: Optional[Workspace] = None) -> None:
+                   min_weight: float = 1e-8, ws: Optional[Workspace] = None,
+                   x_dtype: torch.dtype = torch.float32) -> None:
     """M-step in place on (means, covs, weights) from sufficient statistics summed
-    over row chunks (``estep_stats`` layout); ``n_rows`` is the total row count."""
+    over row chunks (``estep_stats`` layout); ``n_rows`` is the total row count.
+    ``x_dtype`` is the statistics' input dtype: spherical bf16 x stores the means
+    rounded to bf16, as ``em_step`` does."""
     require_hip()
     for t, nm in ((means, "means"), (covs, "covariances"), (weights, "weights")):
         if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
@@ -480,8 +483,8 @@ def finalize_stats(covariance_type: str, nk: torch.Tensor, sum_x: torch.Tensor, 
         sum_q = _device_tensor(sum_q, "sum_q", torch.float32)
     if gram_xx is not None:
         gram_xx = _device_tensor(gram_xx, "gram_xx", torch.float32)
-    prob = problem(covariance_type, torch.float32, B, int(n_rows), D, K)
-    ws = ws or Workspace(problem(covariance_type, torch.float32, B, 1, D, K), means.device)
+    prob = problem(covariance_type, x_dtype, B, int(n_rows), D, K)
+    ws = ws or Workspace(problem(covariance_type, x_dtype, B, 1, D, K), means.device)
     _check(_lib.gmmxx_hip_finalize_stats(ctypes.byref(prob), _ptr(nk), _ptr(sum_x), _ptr(sum_q), _ptr(gram_xx),
                                          float(reg_covar), float(min_weight), _ptr(means), _ptr(covs),
                                          _ptr(weights), ws.ptr, ws.nbytes, _stream(means.device)),

@@ -61,7 +61,7 @@ struct Plan {
   int gram_slices = 0;
   int64_t gram_rows = 0;
   int chol_m = 0;
-  size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
+  size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_wmu = 0, o_wsc = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
   size_t o_xch = 0, o_flags = 0;
   size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_lbuf = 0, o_prec = 0, o_logdet = 0,
          o_gram = 0, total = 0;
@@ -211,6 +211,8 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_whi = take(BK * q.EP * (q.bf ? 2 : 4));
   q.o_wlo = take(q.bf ? BK * q.EP * 2 : 0);
   q.o_waug = take(sph_bf ? BK * 32 * 2 : 0);
+  q.o_wmu = take(q.coop ? BK * q.DP * 2 : 0);
+  q.o_wsc = take(q.coop ? BK * 4 : 0);
   q.o_cconst = take(BK * 16);
   q.o_covs_used = take(q.cov == SPH ? BK * 4 : (q.cov == DIAG ? BK * q.D * 4 : 0));
   q.o_rowq = take(q.cov == TIED ? BN * 4 : 0);
@@ -310,8 +312,8 @@ int run_coop(const Plan& pl, const void* x, void* ws, hipStream_t s) {
   c.D = pl.D;
   c.K = pl.K;
   c.B = pl.B;
-  c.w_hi = at<void>(ws, pl.o_whi);
-  c.w_lo = at<void>(ws, pl.o_wlo);
+  c.w_mu = at<void>(ws, pl.o_wmu);
+  c.w_scale = at<float>(ws, pl.o_wsc);
   c.w_aug = at<void>(ws, pl.o_waug);
   c.G = pl.cG;
   c.NG = pl.cNG;
@@ -415,6 +417,8 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   a.w_hi = at<void>(ws, pl.o_whi);
   a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
   a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
+  a.w_mu = pl.coop ? at<void>(ws, pl.o_wmu) : nullptr;
+  a.w_scale = pl.coop ? at<float>(ws, pl.o_wsc) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
   a.gram = shift ? gram : nullptr;
   a.shift = gram ? shift : nullptr;
@@ -479,6 +483,7 @@ FinalizeArgs finalize_args(const Plan& pl, void* ws, const float* gram, double r
   f.covs = covs;
   f.weights = weights;
   f.skip = skip;
+  f.bf_means = pl.bf && pl.cov == SPH;
   return f;
 }
 

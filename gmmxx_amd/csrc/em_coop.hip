@@ -14,7 +14,10 @@
 // work plus one lane swap (measured 2 % faster per C2 pass than 16x16x32 tiles,
 // whose rows spread over four lanes).
 //
-//   block i:    E-GEMM (logits l2, log2 units, as in em_sph_bf16.hip)
+//   block i:    E-GEMM: logits l2 (log2 units) = (log2(e)/σ²)·(x·μ) + A·‖x‖² + C,
+//               the exact product of bf16 x and bf16 means on MFMA, scaled in
+//               fp32 (the two-pass kernels split -2·ca·μ into bf16 hi + lo
+//               instead: twice the MFMA work), the rest from the augmented chunk
 //               m_w = wave row max, e = 2^(l2 - m_w) (kept in LDS as bf16), s_w = Σ e
 //               workgroup partials (M, S) per row -> published to the group
 //   block i-2:  lse2 = merge of the group's partials (same order in every
@@ -203,7 +206,8 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
   }
   for (int i = tid; i < kNW * 2 * 2 * 64; i += NTHR) es[i] = make_uint4(0u, 0u, 0u, 0u);
 
-  bf16x8 whi[XK], wlo[XK], waug;
+  bf16x8 wmu[XK], waug;
+  float sc[16];            // log2(e)/σ² of the wave's output components (register v)
   f32x16 accx[XT], acca;
   float mw[2];             // wave row maxima of the two blocks in flight (row lr), per block parity
   unsigned seq = 0;        // blocks this group has exchanged before the current item
@@ -223,18 +227,21 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       if (kk < K) {
         const size_t bk = (size_t)b * K + kk;
 #pragma unroll
-        for (int t = 0; t < XK; ++t) {
-          whi[t] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_hi) + bk * DP + 16 * t + 8 * hf);
-          wlo[t] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_lo) + bk * DP + 16 * t + 8 * hf);
-        }
+        for (int t = 0; t < XK; ++t)
+          wmu[t] = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_mu) + bk * DP + 16 * t + 8 * hf);
         waug = ld16<bf16x8>(reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * hf);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
 #pragma unroll
-          for (int t = 0; t < XK; ++t) { whi[t][e] = (__bf16)0.f; wlo[t][e] = (__bf16)0.f; }
+          for (int t = 0; t < XK; ++t) wmu[t][e] = (__bf16)0.f;
           waug[e] = (__bf16)((8 * hf + e) == 6 ? -kHuge : 0.f);
         }
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int kv = kbase + 8 * (v / 4) + 4 * hf + (v % 4);
+        sc[v] = kv < K ? a.w_scale[(size_t)b * K + kv] : 0.f;
       }
 #pragma unroll
       for (int xt = 0; xt < XT; ++xt) accx[xt] = f32x16{};
@@ -336,17 +343,18 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
         }
       }
     };
-    // E-GEMM C = W·φᵀ of a staged block: lane (lr, hf), register v holds component
-    // 8(v/4) + 4hf + v%4 of row lr.
+    // E-GEMM of a staged block: lane (lr, hf), register v holds component
+    // 8(v/4) + 4hf + v%4 of row lr.  l2 = (log2(e)/σ²)·(x·μ) + [A·‖x‖² + C]: the
+    // product of the exact bf16 x and means accumulates in fp32, its factor is
+    // applied after the MFMA, and the augmented chunk carries the rest.
     auto egemm = [&](int bx) -> f32x16 {
       const __bf16* xr = xs + bx * kBN * XS + lr * XS + 8 * hf;
-      f32x16 T = mfma32(waug, ld16<bf16x8>(xr + DP), f32x16{});
+      const f32x16 A = mfma32(waug, ld16<bf16x8>(xr + DP), f32x16{});
+      f32x16 T = f32x16{};
 #pragma unroll
-      for (int t = 0; t < XK; ++t) {
-        const bf16x8 xv = ld16<bf16x8>(xr + 16 * t);
-        T = mfma32(whi[t], xv, T);
-        T = mfma32(wlo[t], xv, T);
-      }
+      for (int t = 0; t < XK; ++t) T = mfma32(wmu[t], ld16<bf16x8>(xr + 16 * t), T);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) T[v] = fmaf(sc[v], T[v], A[v]);
       return T;
     };
     // Wave row maxima m_w, e = 2^(l2 - m_w) (kept in this wave's LDS slot of the

@@ -74,8 +74,8 @@ struct CoopArgs {
   int vec_ok;
   int64_t N;
   int D, K, B;
-  const void* w_hi;            // [B][K][DP] bf16
-  const void* w_lo;
+  const void* w_mu;            // [B][K][DP] the means, bf16
+  const float* w_scale;        // [B][K] log2(e)/σ²
   const void* w_aug;           // [B][K][32] bf16
   int G;                       // workgroups per group
   int NG;                      // groups (grid = NG * G)

@@ -64,7 +64,9 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
   const float wk = a.prelude ? fmaxf(wrow[k], floor_v) / total : wrow[k];
   const float lw = logf(wk);
   const float* mu = a.means + bk * D;
-  for (int d = lane; d < D; d += 64) mus[d] = mu[d];
+  // bf16 x (spherical) computes with bf16 means, as the reference keeps them in
+  // x's dtype (torch_fallback.py:2295, :1451).
+  for (int d = lane; d < D; d += 64) mus[d] = a.bf ? (float)(__bf16)mu[d] : mu[d];
   __syncthreads();
   float colq, ca, cb;
   const float log2pi_d = (float)(kLog2Pi * (double)D);
@@ -102,6 +104,12 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
       const __bf16 cl = (__bf16)(cy - (float)ch - (float)cm);
       const __bf16 vals[9] = {ah, ah, ah, am, am, al, ch, cm, cl};
       if (lane < 32) reinterpret_cast<__bf16*>(a.w_aug)[bk * 32 + lane] = lane < 9 ? vals[lane] : (__bf16)0.f;
+      // Cooperative pass: the exact bf16 means and the factor -2·ca, applied to
+      // the fp32 product x·μ after the MFMA (no hi/lo split of the operand).
+      if (a.w_mu) {
+        for (int e = lane; e < DP; e += 64) reinterpret_cast<__bf16*>(a.w_mu)[bk * DP + e] = (__bf16)(e < D ? mus[e] : 0.f);
+        if (lane == 0) a.w_scale[bk] = -2.f * ca;
+      }
     } else {
       for (int e = lane; e < EP; e += 64) put_f32(e, e < D ? mus[e] : 0.f);
     }
@@ -792,7 +800,9 @@ __device__ void finalize_comp(const FinalizeArgs& a, int b, int k, float total) 
   float msq = 0.f;
   for (int d = lane; d < D; d += 64) {
     const float m = active ? sk[d] / nk_safe : mu[d];
-    mu[d] = m;
+    // bf16 x: the means are stored in bf16 (torch_fallback.py:2295); the variance
+    // below is formed from the unrounded mean.
+    mu[d] = a.bf_means ? (float)(__bf16)m : m;
     msq = fmaf(m, m, msq);
     if (a.cov == DIAG) {
       const float v = fmaxf(sk[a.DP + d] / nk_safe - m * m, a.reg_covar);

@@ -19,6 +19,8 @@ struct PrepArgs {
   void* w_hi;              // [B][K][EP]
   void* w_lo;              // [B][K][EP] (bf16 path)
   void* w_aug;             // [B][K][32] (spherical bf16 path)
+  void* w_mu;              // [B][K][DP] spherical bf16 cooperative pass: the bf16 means (or null)
+  float* w_scale;          // [B][K] with w_mu: log2(e)/σ², the factor of the product x·μ
   float4* cconst;          // [B][K]
   const float* gram;       // tied EM: XᵀX [B][D][D] (or null)
   double* shift;           // with gram: [B][D] row terms -½ Σ_j P_rj (XᵀX)_rj
@@ -49,6 +51,7 @@ struct FinalizeArgs {
   float* covs;
   float* weights;
   const unsigned* skip;    // nonzero *skip: leave the parameters unchanged (or null)
+  int bf_means;            // spherical bf16 x: store the means rounded to bf16
 };
 
 struct UnpackArgs {

@@ -8,14 +8,17 @@ iteration is one call of ``gmmxx_hip_em_step`` on the current stream; with
 
 Semantics follow the reference's soft EM.  fp32 input runs the fp32 algorithm
 (every product fp32-accurate).  bf16 input (spherical only) stays bf16 in HBM
-and is computed by the bf16 engine: exact bf16 x against a hi + lo bf16 split
-of each component's fp32 E-step operand (about 16 significand bits) with fp32
-accumulation, and the responsibilities rounded to bf16 before the M-step
-product -- more accurate than the reference's bf16 arithmetic on the same
-input, but not the fp32 algorithm (the bf16 bar is 2e-3 on the
-log-likelihood).  The estimator upcasts half-precision input to fp32 unless
-``dtype=torch.bfloat16`` is given, as the reference does.  Parameters are
-fp32.
+and is computed by the bf16 engine.  Its means are bf16, as the reference keeps
+them in x's dtype (torch_fallback.py:1451, :2295): the initial means and every
+M-step's means are rounded to bf16 (stored in fp32 tensors), while variances
+and weights stay fp32.  The E-step multiplies exact bf16 x by the bf16 means
+with fp32 accumulation (the cooperative kernel; the two-pass kernels use a
+hi + lo bf16 split of the fp32 operand -2·μ/σ², about 16 significand bits), and
+the responsibilities are rounded to bf16 before the M-step product -- more
+accurate than the reference's bf16 arithmetic on the same input, but not the
+fp32 algorithm (the bf16 bar is 2e-3 on the log-likelihood).  The estimator
+upcasts half-precision input to fp32 unless ``dtype=torch.bfloat16`` is given,
+as the reference does.
 """
 
 from __future__ import annotations
@@ -77,6 +80,12 @@ def global_tied_covariance(x: torch.Tensor, reg_covar: float) -> torch.Tensor:
     return (_sym(cov) + reg_covar * torch.eye(d, device=x.device)).contiguous()
 
 
+def _engine_means(means: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """bf16 x keeps its means in bf16 (torch_fallback.py:1451, :2295), stored
+    here as fp32 tensors holding bf16 values."""
+    return means.to(torch.bfloat16).to(torch.float32) if x.dtype == torch.bfloat16 else means
+
+
 def _init_weights(init_weights, bsz, k, device):
     w = (torch.full((bsz, k), 1.0 / float(k), device=device) if init_weights is None
          else _f32(init_weights, device))
@@ -116,7 +125,7 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
             means, covs, weights = kmeans.kmeans_initialize(
                 x, covariance_type, k, max_iters=kmeans_init_iters, tol=kmeans_init_tol, reg_covar=reg_covar,
                 generator=generator)
-            return means, covs, weights, "kmeans"
+            return _engine_means(means, x), covs, weights, "kmeans"
         idx = torch.randint(0, n, (bsz, k), device=dev, generator=generator)
         means = torch.gather(x, 1, idx[..., None].expand(-1, -1, d)).to(torch.float32).contiguous()
         source = "random"
@@ -143,7 +152,7 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
             raise ValueError("init_variances must have shape (B, K, D, D) for full covariance")
         covs = _sym(covs)
     weights = _init_weights(init_weights, bsz, k, dev)
-    return means.contiguous(), covs.contiguous(), weights, source
+    return _engine_means(means, x).contiguous(), covs.contiguous(), weights, source
 
 
 def resolve_approx_top_k(approx_top_k: Optional[int], n_components: int) -> Optional[int]:
@@ -181,7 +190,7 @@ class _TopkStep:
         # top-1 (hard assignment) keeps no logits: one chunk
         self.rows = n if top_k == 1 else topk_chunk_rows(bsz, n, k)
         self.ws: Dict[int, _hip.Workspace] = {}
-        self.fin_ws = _hip.Workspace(_hip.problem(covariance_type, torch.float32, bsz, 1, d, k), x.device)
+        self.fin_ws = _hip.Workspace(_hip.problem(covariance_type, x.dtype, bsz, 1, d, k), x.device)
 
     def chunks(self):
         for n0 in range(0, self.n, self.rows):
@@ -213,7 +222,7 @@ class _TopkStep:
     def step(self, means, covs, weights, lb_out, gram, reg_covar, min_weight):
         nk, sum_x, sum_q, ll = self.stats(means, covs, weights, reg_covar, min_weight)
         _hip.finalize_stats(self.cov, nk, sum_x, sum_q, means, covs, weights, self.n, gram_xx=gram,
-                            reg_covar=reg_covar, min_weight=min_weight, ws=self.fin_ws)
+                            reg_covar=reg_covar, min_weight=min_weight, ws=self.fin_ws, x_dtype=self.x.dtype)
         torch.div(ll, float(self.x.shape[0] * self.n), out=lb_out)
 
 

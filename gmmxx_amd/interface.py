@@ -16,10 +16,10 @@ point tensors, fitted attributes squeezed when the input was unbatched
 (:322-325, :401-424), half-precision inputs computed in fp32 unless ``dtype=``
 says otherwise (:426-433): bf16/fp16 input runs the fp32 algorithm.  With
 ``dtype=torch.bfloat16`` spherical input stays bf16 in HBM and runs the bf16
-engine (exact bf16 x against a hi + lo bf16 split of the fp32 component
-operands, fp32 accumulation, responsibilities rounded to bf16 before the
-M-step product): more accurate than the reference's bf16 arithmetic, held to
-the bf16 bar (2e-3 on the log-likelihood), not to the fp32 one.
+engine (bf16 means as the reference keeps them, products of exact bf16 values
+with fp32 accumulation, responsibilities rounded to bf16 before the M-step
+product): more accurate than the reference's bf16 arithmetic, held to the bf16
+bar (2e-3 on the log-likelihood), not to the fp32 one.
 """
 
 from __future__ import annotations

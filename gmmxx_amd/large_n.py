@@ -214,7 +214,7 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
     sub_rows = (min(n, chunk_size_N) if top_k == 1 else em.topk_chunk_rows(1, min(n, chunk_size_N), k)) \
         if top_k is not None else 0
     topk_wss = _Workspaces(covariance_type, dtype, d, k, device, top_k=top_k) if top_k is not None else None
-    fin_ws = _hip.Workspace(_hip.problem(covariance_type, torch.float32, 1, 1, d, k), device)
+    fin_ws = _hip.Workspace(_hip.problem(covariance_type, dtype, 1, 1, d, k), device)
 
     gram = None
     if covariance_type == "tied":   # XᵀX once per fit, summed over the chunks
@@ -253,7 +253,7 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
             for ws in wss.cache.values():
                 _hip.raise_on_status(_hip.take_status(ws), "streamed EM fit")
         _hip.finalize_stats(covariance_type, nk, sx, sq, means, covs, weights, n, gram_xx=gram,
-                            reg_covar=reg_covar, min_weight=min_weight, ws=fin_ws)
+                            reg_covar=reg_covar, min_weight=min_weight, ws=fin_ws, x_dtype=dtype)
         value = float(ll.item()) / float(n)
         history.append(value)
         n_iter = it + 1

@@ -13,7 +13,10 @@
  * Data layout: x is row-major (B, N, D) fp32 or bf16; every parameter array is
  * fp32 row-major in the reference's batched shapes: means (B, K, D), weights
  * (B, K), covariances spherical (B, K), diag (B, K, D), tied (B, D, D),
- * full (B, K, D, D).
+ * full (B, K, D, D).  With bf16 x (spherical) the means are bf16 values, as the
+ * reference keeps them in x's dtype (gmmxx/torch_fallback.py:2295): every call
+ * computes with the means rounded to bf16, and the M-step stores them rounded
+ * (the variance is formed from the unrounded mean).
  */
 #ifndef GMMXX_HIP_H_
 #define GMMXX_HIP_H_

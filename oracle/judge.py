@@ -28,8 +28,15 @@ import torch
 FACTOR = 4.0
 
 
+def bf16_ulp(v):
+    """The spacing of bf16 values at |v|: 2^(e-8) for |v| in [2^(e-1), 2^e)."""
+    _, e = torch.frexp(v)
+    return torch.ldexp(torch.ones_like(v), e - 8)
+
+
 def param_band(kind, x, bf16):
-    """(rtol, absolute floor) of the bar for one parameter kind."""
+    """(rtol, absolute floor) of the bar for one parameter kind (bf16 means:
+    ``judge_params`` adds one bf16 ulp, see there)."""
     if bf16:
         return 2e-3, None          # 2e-3 of the parameter's scale (the bf16 bar is the log-likelihood)
     xf = x.double()
@@ -42,7 +49,9 @@ def judge_params(got, exp, kind, x, bf16=False, truth_fn=None):
     """Elements outside the bar, the largest error relative to the bar, and
     whether the tensor fails (``unexplained``: 0 or the count of elements
     outside the bar); ``truth_fn()`` returns the float64 value (called only
-    when some element is outside the bar)."""
+    when some element is outside the bar).  bf16 x keeps its means in bf16 on
+    both sides, so their bar adds one bf16 ulp: fp32 means within the bar round
+    to bf16 values at most that much further apart."""
     got = got.detach().cpu().double()
     exp = exp.detach().cpu().double()
     rtol, floor = param_band(kind, x, bf16)
@@ -50,6 +59,8 @@ def judge_params(got, exp, kind, x, bf16=False, truth_fn=None):
         floor = rtol * float(exp.abs().max())
         rtol = 0.0
     band = rtol * exp.abs() + floor
+    if bf16 and kind == "means":
+        band = band + bf16_ulp(exp)
     out = (got - exp).abs() > band
     res = {"kind": kind, "elements": int(exp.numel()), "outside_bar": int(out.sum()),
            "worst_ratio": float(((got - exp).abs() / band).max()), "unexplained": 0}
@@ -59,7 +70,7 @@ def judge_params(got, exp, kind, x, bf16=False, truth_fn=None):
         res["unexplained"] = res["outside_bar"]
         return res
     t = truth_fn().detach().cpu().double()
-    band_t = rtol * t.abs() + floor
+    band_t = rtol * t.abs() + floor + (bf16_ulp(t) if bf16 and kind == "means" else 0.0)
     res["hip_vs_float64"] = float(((got - t).abs() / band_t).max())
     res["oracle_vs_float64"] = float(((exp - t).abs() / band_t).max())
     if res["hip_vs_float64"] > max(FACTOR * res["oracle_vs_float64"], 1.0):

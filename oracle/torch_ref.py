@@ -32,7 +32,10 @@ How each part is pinned (checked independently of this restatement):
     one seed per well-separated blob; Lloyd against a float64 brute force and
     the closed-form blob means; hard-label statistics against float64 loops
     (tests/test_oracle_kmeans.py).  The Lloyd stopping rule restates
-    flash-kmeans (absent here) and is not pinned.
+    flash-kmeans (absent here) and is not pinned;
+  * ``bf16_means`` (bf16 input): the rounded means are bf16 values within half
+    a bf16 ulp of the pinned fp32 iteration's, whose covariances and weights
+    it keeps unchanged (tests/test_oracle_pinned.py).
 
 Difference from the reference that is deliberate: the reference records the
 lower bound of non-final iterations as 0.0 for diag/tied/full when ``tol == 0``
@@ -568,7 +571,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         reg_covar: float = 1e-6, min_weight: float = 1e-8,
         chunk_size_N: int = DEFAULT_CHUNK_N, chunk_size_K: int = DEFAULT_CHUNK_K,
         compute_labels: bool = True, record_all_lower_bounds: bool = True,
-        approx_top_k: Optional[int] = None,
+        approx_top_k: Optional[int] = None, bf16_means: bool = False,
         ) -> Tuple[Optional[torch.Tensor], torch.Tensor, torch.Tensor, torch.Tensor, Dict]:
     """Soft EM with explicit initial parameters, for one covariance type.
 
@@ -576,6 +579,13 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
     batch_gmm_Diagonal_torch_native (:2401-2728) and
     _batch_gmm_matrix_torch_native (:2732-3244) on their CPU branch.
     Returns (labels, means, covariances, weights, info) like the reference.
+
+    ``bf16_means`` models bf16 input on fp32 arithmetic (pass x upcast to fp32):
+    the means are rounded to bf16 on entry and after every M-step, as the
+    reference's ``.to(x.dtype)`` keeps a bf16 input's means (:1451, :2295);
+    covariances and weights stay fp32, and the variance is formed from the
+    unrounded mean (the reference forms it from the rounded means in bf16
+    arithmetic, :2297-2299).
     """
     if x.ndim != 3:
         raise ValueError("x must have shape (B, N, D)")
@@ -595,6 +605,8 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
     x_sq_all = (x.to(torch.float32) ** 2).sum(dim=-1) if spherical else None
     means, covs, weights = init_user_parameters(x, covariance_type, init_means, init_covs,
                                                 init_weights, reg_covar, x_sq=x_sq_all)
+    if bf16_means:
+        means = _bf16_values(means)
     chunk_n = _spherical_chunk_n(n, d, k, chunk_size_N) if spherical else chunk_size_N
     # _resolve_approx_top_k (torch_fallback.py:598-606): top_k >= K is exact EM.
     if approx_top_k is not None and int(approx_top_k) <= 0:
@@ -633,7 +645,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
 
         lb = (total_ll / float(bsz * n)) if collect else torch.zeros((), dtype=torch.float32)
         history.append(float(lb))
-        means, covs, weights = means_new, covs_new, weights_new
+        means, covs, weights = (_bf16_values(means_new) if bf16_means else means_new), covs_new, weights_new
 
         # Convergence (:2322-2330 spherical; :2695-2698 others).
         if spherical:
@@ -659,13 +671,19 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
 
 
 def fit_one_iteration_stats(x, covariance_type, means, covs, weights, reg_covar=1e-6,
-                            min_weight=1e-8):
+                            min_weight=1e-8, bf16_means=False):
     """Convenience: one EM iteration from explicit parameters; returns the new
     parameters and that iteration's mean log-likelihood."""
     _, m, c, w, info = fit(x, means.shape[1], covariance_type, max_iters=1, tol=0.0,
                            init_means=means, init_covs=covs, init_weights=weights,
-                           reg_covar=reg_covar, min_weight=min_weight, compute_labels=False)
+                           reg_covar=reg_covar, min_weight=min_weight, compute_labels=False,
+                           bf16_means=bf16_means)
     return m, c, w, info["lower_bound"]
+
+
+def _bf16_values(t: torch.Tensor) -> torch.Tensor:
+    """fp32 tensor of the bf16 round-to-nearest-even values of t."""
+    return t.to(torch.bfloat16).to(torch.float32)
 
 
 # ---------------------------------------------------------------------------

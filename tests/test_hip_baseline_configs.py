@@ -4,7 +4,7 @@ the configs' initial parameters) against the CPU oracle.
 C1 runs at its full size (N = 100,000, D = 32, K = 64, 20 iterations); C2-C5 at
 reduced N with the recipe, K, D, B and iteration count of the config.  The same
 data and initial parameters go to both sides (bf16 x: the oracle computes in
-fp32 on the bf16 values).  Bars and the float64 arbiter: oracle/judge.py
+fp32 on the bf16 values and keeps the means in bf16, ``bf16_means``).  Bars and the float64 arbiter: oracle/judge.py
 (log-likelihood rtol 1e-5 fp32 / 2e-3 bf16; fp32 parameters element-wise rtol
 1e-4 with stated floors; a value outside the bar passes only if it is at least
 as close to the float64 result from the same inputs as the oracle's is,
@@ -61,7 +61,7 @@ def test_config_recipe_per_iteration(hip, name, n):
     means, covs, w = m0.cpu(), c0.cpu(), w0.cpu()
     worst = {}
     for it in range(iters):
-        e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(xc, cov, means, covs, w)
+        e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(xc, cov, means, covs, w, bf16_means=bf)
         m_d, c_d, w_d = (t.to(DEV).contiguous() for t in (means, covs, w))
         hip.em_step(cov, x, m_d, c_d, w_d, lb, gram_xx=gram, ws=ws)
         torch.cuda.synchronize()
@@ -97,7 +97,7 @@ def test_config_recipe_trajectory(hip, name, n):
     labels, m, c, w, info = em.fit(x, k, cov, max_iters=iters, tol=0.0, init_means=m0, init_covs=c0,
                                    init_weights=w0, record_all_lower_bounds=True)
     e_lab, e_m, e_c, e_w, e_info = torch_ref.fit(xc, k, cov, max_iters=iters, tol=0.0, init_means=m0.cpu(),
-                                                 init_covs=c0.cpu(), init_weights=w0.cpu())
+                                                 init_covs=c0.cpu(), init_weights=w0.cpu(), bf16_means=bf)
     assert info["n_iter"] == e_info["n_iter"] == iters
     truth = []
 

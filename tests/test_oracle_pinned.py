@@ -4,7 +4,9 @@
   scipy.stats (independent implementation), per covariance type;
 * one EM step: scikit-learn's GaussianMixture (independent textbook EM) with
   warm-started parameters; sklearn adds ``reg_covar`` where the reference
-  clamps to it, so a tiny ``reg_covar`` is used and the two agree;
+  clamps to it, so a tiny ``reg_covar`` is used and the two agree; with
+  ``bf16_means`` the means are sklearn's rounded to bf16 (half an ulp) and the
+  variances and weights sklearn's;
 * the Cholesky jitter ladder: a matrix whose first successful jitter is known
   in closed form, plus the batch-global retry;
 * finalize: hand-computed known answers restated from the reference's tests
@@ -115,6 +117,37 @@ def test_one_em_step_vs_sklearn(cov):
         warnings.simplefilter("ignore", ConvergenceWarning)
         gm.fit(x[0].double().numpy())
     np.testing.assert_allclose(m1[0].double().numpy(), gm.means_, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(w1[0].double().numpy(), gm.weights_, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(c1[0].double().numpy(), gm.covariances_, rtol=2e-4, atol=2e-5)
+    assert info["lower_bound_history"][0] == pytest.approx(gm.lower_bound_, rel=1e-5)
+
+
+def test_bf16_means_one_step_vs_sklearn():
+    """bf16 input's means (``bf16_means``): one spherical step from bf16-valued
+    means gives bf16 values within half a bf16 ulp of sklearn's float64 means,
+    and sklearn's variances (about the unrounded mean) and weights."""
+    from sklearn.exceptions import ConvergenceWarning
+    from sklearn.mixture import GaussianMixture
+
+    x, means, covs, w = _problem("spherical", b=1, n=400, d=3, k=3, seed=3)
+    means = means.to(torch.bfloat16).to(torch.float32)
+    reg = 1e-9
+    _, m1, c1, w1, info = torch_ref.fit(x, 3, "spherical", max_iters=1, tol=0.0, init_means=means,
+                                        init_covs=covs, init_weights=w, reg_covar=reg,
+                                        compute_labels=False, bf16_means=True)
+    gm = GaussianMixture(n_components=3, covariance_type="spherical", max_iter=1, tol=0.0, reg_covar=reg,
+                         means_init=means[0].double().numpy(),
+                         weights_init=(w[0].double() / w[0].double().sum()).numpy(),
+                         precisions_init=_precisions_init("spherical", covs))
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore", ConvergenceWarning)
+        gm.fit(x[0].double().numpy())
+    assert torch.equal(m1, m1.to(torch.bfloat16).to(torch.float32))
+    ref = torch.from_numpy(gm.means_)
+    _, e = torch.frexp(ref)
+    half_ulp = torch.ldexp(torch.ones_like(ref), e - 9)     # |v| in [2^(e-1), 2^e): ulp 2^(e-8)
+    assert bool(((m1[0].double() - ref).abs() <= half_ulp * 1.001 + 1e-6).all())
+    assert not torch.equal(m1[0].double(), ref)             # the rounding is visible at this size
     np.testing.assert_allclose(w1[0].double().numpy(), gm.weights_, rtol=1e-5, atol=1e-7)
     np.testing.assert_allclose(c1[0].double().numpy(), gm.covariances_, rtol=2e-4, atol=2e-5)
     assert info["lower_bound_history"][0] == pytest.approx(gm.lower_bound_, rel=1e-5)
