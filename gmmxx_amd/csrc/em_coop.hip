@@ -18,7 +18,7 @@
 //               the exact product of bf16 x and bf16 means on MFMA, scaled in
 //               fp32 (the two-pass kernels split -2·ca·μ into bf16 hi + lo
 //               instead: twice the MFMA work), the rest from the augmented chunk
-//               m_w = wave row max, e = 2^(l2 - m_w) (kept in LDS as bf16), s_w = Σ e
+//               m_w = wave row max, e = 2^(l2 - m_w) (kept in fp32 registers), s_w = Σ e
 //               workgroup partials (M, S) per row -> published to the group
 //   block i-2:  lse2 = merge of the group's partials (same order in every
 //               member, so all members use bit-identical log-normalisers)
@@ -167,13 +167,6 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
   __shared__ float red_m[2 * kNW * RR];
   __shared__ float red_s[2 * kNW * RR];
   __shared__ float lse_s[2 * kBN];
-  // e = 2^(l2 - m_w) of the two blocks in flight, per wave and block parity, in
-  // the accumulator layout (sixteen bf16 per lane: its components of row lr); kept in LDS,
-  // which leaves the registers to the W operands and the statistics.  e is
-  // rounded to bf16 here and r = e·2^(m_w - lse2) again before the M-GEMM (r is a
-  // bf16 MFMA operand in any case): half the LDS bytes of fp32 e, measured 3 %
-  // faster at K = 1024, with the sums and the log-normalisers still from fp32 e.
-  __shared__ uint4 es[kNW * 2 * 2 * 64];
 
   const int tid = threadIdx.x;
   const int wave = tid / 64, lane = tid % 64;
@@ -204,10 +197,15 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     const uint4 w = make_uint4(ch == 1 ? pack2((__bf16)1.f, (__bf16)0.f) : 0u, 0u, 0u, 0u);
     *reinterpret_cast<uint4*>(xs + row * XS + DP + 8 * ch) = w;
   }
-  for (int i = tid; i < kNW * 2 * 2 * 64; i += NTHR) es[i] = make_uint4(0u, 0u, 0u, 0u);
 
   bf16x8 wmu[XK], waug;
   float sc[16];            // log2(e)/σ² of the wave's output components (register v)
+  // e = 2^(l2 - m_w) of the two blocks in flight, per block parity, in the
+  // accumulator layout (register v: component 8(v/4) + 4hf + v%4 of row lr),
+  // kept in fp32 registers until its responsibilities are formed two blocks
+  // later (measured 6 % faster per C2 pass than a bf16 copy in LDS, which needs
+  // the pack, the read back and the unpack).
+  float er[2][16];
   f32x16 accx[XT], acca;
   float mw[2];             // wave row maxima of the two blocks in flight (row lr), per block parity
   unsigned seq = 0;        // blocks this group has exchanged before the current item
@@ -297,27 +295,19 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       }
     };
 
-    // Responsibilities of block i-2 (parity pb, first row rf): r = e · 2^(m_w - lse2)
-    // with e read back (bf16) from this wave's LDS slot, rounded to bf16 and staged
-    // row-major for the transposing reads of the M-GEMM.  Lane (lr, hf) holds
-    // components 8u + 4hf + (0..3), u = 0..3, of row lr.
+    // Responsibilities of block i-2 (parity pb, first row rf): r = e · 2^(m_w - lse2),
+    // rounded to bf16 and staged row-major for the transposing reads of the M-GEMM.
+    // Lane (lr, hf) holds components 8u + 4hf + (0..3), u = 0..3, of row lr.
     auto prep_r = [&](auto PB_, int rf, int nr) {
       constexpr int pb = decltype(PB_)::value;
       const float l2 = lse_s[pb * kBN + lr];     // read unconditionally: no branch around the LDS load
       const float f = (rf + lr < nr) ? fast_exp2(mw[pb] - l2) : 0.f;
-      const uint4* ew = es + ((wave * 2 + pb) * 2) * 64 + lane;
       __bf16* rrow = rs + wave * kBN * kRS + lr * kRS;
 #pragma unroll
-      for (int hq = 0; hq < 2; ++hq) {
-        const uint4 q = ew[hq * 64];
-        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int uu = 0; uu < 2; ++uu) {
-          const f32x2 e01 = __builtin_convertvector(__builtin_bit_cast(bf16x2, w4[2 * uu]), f32x2);
-          const f32x2 e23 = __builtin_convertvector(__builtin_bit_cast(bf16x2, w4[2 * uu + 1]), f32x2);
-          const uint2 pk = make_uint2(cvt2(e01[0] * f, e01[1] * f), cvt2(e23[0] * f, e23[1] * f));
-          *reinterpret_cast<uint2*>(rrow + rswz(lr, 8 * (2 * hq + uu) + 4 * hf)) = pk;
-        }
+      for (int u = 0; u < 4; ++u) {
+        const float* e4 = er[pb] + 4 * u;
+        const uint2 pk = make_uint2(cvt2(e4[0] * f, e4[1] * f), cvt2(e4[2] * f, e4[3] * f));
+        *reinterpret_cast<uint2*>(rrow + rswz(lr, 8 * u + 4 * hf)) = pk;
       }
     };
     // Transposing-read addresses of the 32x32x16 operands: lane i of 16-lane group
@@ -357,25 +347,22 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       for (int v = 0; v < 16; ++v) T[v] = fmaf(sc[v], T[v], A[v]);
       return T;
     };
-    // Wave row maxima m_w, e = 2^(l2 - m_w) (kept in this wave's LDS slot of the
-    // block parity) and the wave's row sums for the workgroup combine: a row's 32
-    // components sit in lanes lr and lr + 32.
+    // Wave row maxima m_w, e = 2^(l2 - m_w) (kept in er of the block parity) and
+    // the wave's row sums for the workgroup combine: a row's 32 components sit in
+    // lanes lr and lr + 32.
     auto lse_epilogue = [&](const f32x16& T, auto PB_) {
       constexpr int pb = decltype(PB_)::value;
       float m = T[0];
 #pragma unroll
       for (int v = 1; v < 16; ++v) m = fmaxf(m, T[v]);
       m = lanes_op<32, true>(m);
-      float e[16];
+      float* e = er[pb];
 #pragma unroll
       for (int v = 0; v < 16; ++v) e[v] = fast_exp2(T[v] - m);
       float ps[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) ps[u] = (e[4 * u] + e[4 * u + 1]) + (e[4 * u + 2] + e[4 * u + 3]);
       const float sum = lanes_op<32, false>((ps[0] + ps[1]) + (ps[2] + ps[3]));
-      uint4* ew = es + ((wave * 2 + pb) * 2) * 64 + lane;
-      ew[0] = make_uint4(cvt2(e[0], e[1]), cvt2(e[2], e[3]), cvt2(e[4], e[5]), cvt2(e[6], e[7]));
-      ew[64] = make_uint4(cvt2(e[8], e[9]), cvt2(e[10], e[11]), cvt2(e[12], e[13]), cvt2(e[14], e[15]));
       mw[pb] = m;
       // Both lanes of a row hold the same values: both store (no branch).
       red_m[(pb * kNW + wave) * RR + lr] = m;
