@@ -226,8 +226,10 @@ class Workspace:
 
 def take_status(ws: Workspace) -> torch.Tensor:
     """Device uint32 word: the asynchronous failures recorded on ``ws`` since the
-    last call (nonzero: a cooperative pass gave up waiting for a partner; its
-    iteration kept the parameters and wrote a NaN lower bound).  Clears it;
+    last call (nonzero: a single pass whose workgroups exchange row partials --
+    the cooperative spherical bf16 kernel or the fp32 exchange pass -- gave up
+    waiting for a partner; its iteration kept the parameters and wrote a NaN
+    lower bound).  Clears it;
     stream-ordered, no synchronisation."""
     out = torch.zeros((1,), dtype=torch.int32, device=ws.device)
     _check(_lib.gmmxx_hip_take_status(ctypes.byref(ws.prob), ws.ptr, ws.nbytes, _ptr(out), _stream(ws.device)),
@@ -239,9 +241,11 @@ def raise_on_status(status: torch.Tensor, what: str) -> None:
     """Raises HipRuntimeError when a take_status word is nonzero (synchronises)."""
     if int(status.item()) != 0:
         raise HipRuntimeError(
-            f"{what}: a cooperative single-pass launch timed out waiting for a partner workgroup "
-            "(are other kernels occupying the GPU?); the affected iterations left the parameters "
-            "unchanged and recorded a NaN lower bound")
+            f"{what}: a single-pass kernel whose workgroups exchange row partials (cooperative "
+            "spherical bf16 kernel or fp32 exchange pass) timed out waiting for a partner workgroup: "
+            "the members of a group were not all resident (another kernel or process holding part of "
+            "the GPU); the affected iterations left the parameters unchanged and recorded a NaN lower "
+            "bound (GMMXX_HIP_NO_COOP=1 / GMMXX_HIP_NO_XCH=1 select the two-pass kernels)")
 
 
 def device_info(device: int = 0) -> dict:

@@ -328,8 +328,8 @@ int run_coop(const Plan& pl, const void* x, void* ws, hipStream_t s) {
   c.spin_limit = 1 << 20;
   if (const char* sl = getenv("GMMXX_HIP_COOP_SPIN_LIMIT")) c.spin_limit = atoi(sl);
   const int rc = launch_sph_bf16_coop(pl.DP, c, s);
-  if (rc == -2) return fail(GMMXX_ERR_HIP, "cooperative launch of the single-pass kernel failed");
-  if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no cooperative kernel for this shape");
+  if (rc == -2) return fail(GMMXX_ERR_HIP, "launch of the single-pass cooperative kernel failed");
+  if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no single-pass cooperative kernel for this shape and device");
   return check_hip("cooperative single-pass kernel");
 }
 // Exchange single pass: partial statistics per row slice and partial log-likelihoods.
@@ -343,8 +343,8 @@ int run_xch(const Plan& pl, const void* x, void* ws, hipStream_t s, bool em = tr
   if (const char* sl = getenv("GMMXX_HIP_COOP_SPIN_LIMIT")) t.spin_limit = atoi(sl);
   const int64_t nwords = (int64_t)pl.B * pl.xslices * kRing * pl.ktiles * kBN;
   const int rc = launch_tile_xch(pl.cov, pl.DP, t, dim3(pl.xslices * pl.ktiles, pl.B), nwords, s);
-  if (rc == -2) return fail(GMMXX_ERR_HIP, "cooperative launch of the exchange pass failed");
-  if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no exchange tile kernel for this shape");
+  if (rc == -2) return fail(GMMXX_ERR_HIP, "launch of the exchange pass failed");
+  if (rc != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no exchange tile kernel for this shape and device");
   return check_hip("exchange single-pass kernel");
 }
 const unsigned* coop_status(const Plan& pl, void* ws) { return at<unsigned>(ws, pl.o_flags); }

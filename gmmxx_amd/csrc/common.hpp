@@ -71,6 +71,9 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// max(v, lo) that passes a NaN v through, as torch's clamp_min does (fmaxf
+// would return lo): the reference's clamps keep a non-finite input visible.
+__device__ __forceinline__ float clamp_lo(float v, float lo) { return v < lo ? lo : v; }
 
 __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(__bf16 v) { return (float)v; }

@@ -32,10 +32,11 @@
 // two roles sit on different waves (and SIMDs) because every wave waits at the
 // block's barrier for the slowest one: split, they cost the larger of the two
 // instead of their sum (measured 4.57 -> 4.15 ms per C2 pass).  Members of one
-// group must run at the same
-// time, so the kernel launches cooperatively (all workgroups co-resident); every
-// wait is bounded (spin limit), and a wait that times out sets *status and
-// stops waiting, so the kernel always drains.  Used for 2 <= G <= 4: with one
+// group must run at the same time, so the grid is at most the kernel's resident
+// capacity (all workgroups dispatched at once on an idle device; a plain launch,
+// not the cooperative-launch API); every wait is bounded (spin limit), and a
+// wait that times out sets *status and stops waiting, so the kernel always
+// drains.  Used for 2 <= G <= 4: with one
 // member the two-pass kernels are faster, and eight members wait on each other
 // too often (both measured).  Groups are placed on one XCD
 // (workgroup ids congruent mod 8) so the exchange stays in that XCD's L2.
@@ -44,12 +45,14 @@
 //
 // Exchange protocol (no fences): the pair of block j (j = blocks the group has
 // exchanged before) goes to slot j % kRing as one 64-bit relaxed agent-scope
-// atomic store of (M, ±S), the sign of S carrying the round parity
-// (j / kRing) & 1 (S > 0 always; the launcher zeroes the slots, and a zero S
-// matches neither sign).  A reader polls each partner's 64-bit word with
-// relaxed agent-scope atomic loads until the sign matches the expected round,
-// so every datum is checked on its own and no ordering between addresses is
-// needed.  A slot is rewritten only after every partner has read it: a member
+// atomic store of (M, S) with bit 31 of the S half replaced by the round parity
+// (j / kRing) & 1 (S >= 0, so the bit carries no data, and the tag is the same
+// for a NaN, infinite or zero S: a non-finite row propagates into the
+// parameters as in the reference instead of stalling the exchange).  The
+// launcher fills every slot with the odd tag, which no round-0 word carries.
+// A reader polls each partner's 64-bit word with relaxed agent-scope atomic
+// loads until the tag matches the expected round, so every datum is checked
+// on its own and no ordering between addresses is needed.  A slot is rewritten only after every partner has read it: a member
 // publishes block j after it has received every partner's block j - 1, which
 // they publish after finishing their reads of block j - 2, so a ring of two
 // slots would do; four are used.  A slot therefore holds block j or block
@@ -138,9 +141,11 @@ __device__ __forceinline__ bf16x8 cat(v4s lo, v4s hi) {
 // 4 rows x 4 chunks, touch distinct bank pairs.
 __device__ __forceinline__ int rswz(int row, int col) { return col ^ (((row >> 2) & 3) << 2); }
 
+// Exchange slots start with the odd round tag in the high (S) half of every
+// 64-bit word, so no slot reads as a round-0 word before it is written.
 __global__ void coop_zero_kernel(unsigned* p, int n, unsigned* status) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
+  if (i < n) p[i] = (i & 1) ? kTagOdd : 0u;
   if (i == n) *status = 0u;
 }
 
@@ -413,8 +418,8 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
           ownS = S;
           if (G > 1) {
             const unsigned j = seq + i - 1;
-            const float tagged = ((j / kRing) & 1) ? -S : S;
-            const uint64_t word = (uint64_t)__float_as_uint(M) | ((uint64_t)__float_as_uint(tagged) << 32);
+            const uint32_t tagged = (__float_as_uint(S) & ~kTagOdd) | (((j / kRing) & 1) ? kTagOdd : 0u);
+            const uint64_t word = (uint64_t)__float_as_uint(M) | ((uint64_t)tagged << 32);
             __hip_atomic_store(gxch + ((j % kRing) * G + mem) * kBN + lane, word, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
           }
@@ -475,17 +480,14 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
         float M = ownM, S = ownS;
         if (KG > 1 && G > 1) {
           const bool odd = (jx / kRing) & 1;
-          // A word is ready when its tag (the sum's sign) matches the round and its
-          // sum is neither zero (the slots start at zero) nor NaN: the same test as
-          // odd ? t < 0 : t > 0 on the float t.
-          const uint32_t want = odd ? 0x80000000u : 0u;
+          // A word is ready when its tag bit matches the round.
+          const uint32_t want = odd ? kTagOdd : 0u;
           auto ready = [&]() {
             uint32_t bad = 0u;
 #pragma unroll
             for (int p = 0; p < KG; ++p) {
               const uint32_t hi = (uint32_t)(words[p] >> 32);
-              const uint32_t b = ((hi ^ want) >> 31) | (((hi << 1) - 1u) >= 0xFF000000u ? 1u : 0u);
-              bad |= (p < G) ? b : 0u;
+              bad |= (p < G) ? ((hi ^ want) & kTagOdd) : 0u;
             }
             return lane >= kBN || bad == 0u;
           };
@@ -592,9 +594,14 @@ int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s) {
   coop_zero_kernel<<<(nwords + 1 + 255) / 256, 256, 0, s>>>(reinterpret_cast<unsigned*>(a.xch), nwords, a.status);
   const void* fn = a.G <= 2 ? reinterpret_cast<const void*>(sph_bf16_coop_kernel<128, 2>)
                             : reinterpret_cast<const void*>(sph_bf16_coop_kernel<128, 4>);
+  // A plain launch of at most the resident capacity: on an otherwise idle device
+  // every workgroup is dispatched at once.  Nothing else guarantees it, so the
+  // bounded waits are the guard: a member that never meets its partners gives
+  // up, sets the status word and drains.
+  if (grid > coop_capacity()) return -1;
   CoopArgs args = a;
   void* params[] = {&args};
-  const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(64 * kNW), params, 0, s);
+  const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(64 * kNW), params, 0, s);
   if (e != hipSuccess) {
     (void)hipGetLastError();
     return -2;

@@ -916,8 +916,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     // consecutive logical ids, so one XCD when the grid allows) each hold one
     // component tile; per block they swap this workgroup's per-row (max, sum)
     // through global memory, as the cooperative spherical kernel does
-    // (em_coop.hip: one 64-bit relaxed agent-scope word (max, ±sum) per row, the
-    // sign of the sum carrying the round parity (j / kRing) & 1, a ring of kRing
+    // (em_coop.hip: one 64-bit relaxed agent-scope word (max, sum) per row, bit
+    // 31 of the sum half carrying the round parity (j / kRing) & 1, a ring of kRing
     // slots, bounded waits that set *status and stop).  Lag one block: block i's
     // partials are published after its E-GEMM, and block i-1 -- whose logits wait
     // in registers and whose staged rows wait in the extra LDS buffer -- is
@@ -943,14 +943,17 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     };
     auto finish = [&](int64_t j, int bxp, int64_t n0p) {
       const bool odd = (j / kRing) & 1;
+      // A word is ready when its tag bit matches the round (whatever its data:
+      // a NaN or zero sum is passed on, not waited for).
+      const uint32_t want = odd ? kTagOdd : 0u;
       auto ready = [&]() {
-        bool ok = true;
+        uint32_t bad = 0u;
 #pragma unroll
         for (int p = 0; p < kMaxCoopGroup; ++p) {
-          const float t = __uint_as_float((uint32_t)(words[p] >> 32));
-          if (p < gm && p != ktile && lane < kBN) ok = ok && (odd ? t < 0.f : t > 0.f);
+          const uint32_t hi = (uint32_t)(words[p] >> 32);
+          bad |= (p < gm && p != ktile && lane < kBN) ? ((hi ^ want) & kTagOdd) : 0u;
         }
-        return ok;
+        return bad == 0u;
       };
       int spins = 0;
       while (!dead && (a.spin_limit < 0 || __ballot(!ready()) != 0)) {
@@ -1039,8 +1042,8 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         for (int w = 0; w < nw; ++w) S += red_s[lane * 8 + w] * fast_exp2(red_m[lane * 8 + w] - M);
       }
       if (wave == 0 && lane < kBN && gm > 1) {
-        const float tagged = ((ib / kRing) & 1) ? -S : S;
-        const uint64_t word = (uint64_t)__float_as_uint(M) | ((uint64_t)__float_as_uint(tagged) << 32);
+        const uint32_t tagged = (__float_as_uint(S) & ~kTagOdd) | (((ib / kRing) & 1) ? kTagOdd : 0u);
+        const uint64_t word = (uint64_t)__float_as_uint(M) | ((uint64_t)tagged << 32);
         __hip_atomic_store(gw + ((ib % kRing) * gm + ktile) * kBN + lane, word, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
       }
@@ -1150,11 +1153,12 @@ static int launch_tile_dp(int dp, int mode, const TileArgs& a, dim3 grid, int nw
   }
 }
 
-// ---- exchange pass (MODE_STATS_XCH): cooperative launch, all workgroups resident ----
+// ---- exchange pass (MODE_STATS_XCH): grid within the resident capacity, all workgroups co-resident ----
 
+// Every exchange slot starts with the odd round tag, which no round-0 word carries.
 __global__ void xch_zero_kernel(uint64_t* w, int64_t n, unsigned* status) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) w[i] = 0;
+  if (i < n) w[i] = (uint64_t)kTagOdd << 32;
   if (i == 0) *status = 0u;
 }
 
@@ -1202,9 +1206,12 @@ int launch_tile_xch(int cov, int dp, const TileArgs& a, dim3 grid, int64_t nword
   const void* fn = xch_kernel(cov, dp);
   if (!fn) return -1;
   xch_zero_kernel<<<(unsigned)((nwords + 255) / 256 + 1), 256, 0, s>>>(a.xch, nwords, a.status);
+  // At most the resident capacity, as a plain launch (em_coop.hip): the bounded
+  // waits guard against members that are not co-resident.
+  if ((int64_t)grid.x * grid.y * grid.z > tile_xch_capacity(cov, dp)) return -1;
   TileArgs args = a;
   void* params[] = {&args};
-  if (hipLaunchCooperativeKernel(fn, grid, dim3(64 * 8), params, 0, s) != hipSuccess) {
+  if (hipLaunchKernel(fn, grid, dim3(64 * 8), params, 0, s) != hipSuccess) {
     (void)hipGetLastError();
     return -2;
   }

@@ -31,7 +31,7 @@ struct TileArgs {
   const float* thr2;           // [B][N] STATS_TOPK: each row's k-th largest logit (log2)
   const int* thr_idx;          // [B][N] STATS_TOPK: its component index (ties: lower index first)
   int hard;                    // STATS_TOPK with k = 1: r = 1 for component thr_idx, else 0
-  uint64_t* xch;               // STATS_XCH: [B][slices][kRing][ktiles][32] (max, ±sum) words, zeroed by the launcher
+  uint64_t* xch;               // STATS_XCH: [B][slices][kRing][ktiles][32] (max, tagged sum) words, set by the launcher
   unsigned* status;            // STATS_XCH: nonzero after a timed-out wait (zeroed by the launcher)
   int spin_limit;              // STATS_XCH: polls per wait (negative: give up at once)
 };
@@ -47,9 +47,9 @@ int topk_select_blocks(int64_t N);
 int tile_cw(int cov, int dp, int bf);
 int launch_tile(int cov, int bf, int dp, int mode, const TileArgs& a, dim3 grid, int nw, hipStream_t s);
 // MODE_STATS_XCH (fp32 spherical / diag (DP <= 64) / tied, 8 waves): resident
-// workgroups per device (0 when the instance does not exist), and the
-// cooperative launch (zeroes the exchange words and status first); -2 when the
-// cooperative launch fails.
+// workgroups per device (0 when the instance does not exist), and the launch
+// (sets the exchange words and zeroes the status first; the grid must be within
+// the resident capacity, else -1); -2 when the launch fails.
 int tile_xch_capacity(int cov, int dp);
 int launch_tile_xch(int cov, int dp, const TileArgs& a, dim3 grid, int64_t nwords, hipStream_t s);
 // Spherical bf16 kernel (em_sph_bf16.hip): dp in {32, 64} with nw in {2, 4, 8};
@@ -68,6 +68,7 @@ int launch_sph_bf16_fused(int dp, int k, const TileArgs& a, int slices, hipStrea
 constexpr int kCoopComps = 256;      // components per workgroup
 constexpr int kMaxCoopGroup = 4;
 constexpr int kRing = 4;             // exchange slots per group
+constexpr uint32_t kTagOdd = 0x80000000u;  // round-parity tag bit of an exchanged word's sum half
 
 struct CoopArgs {
   const void* x;               // [B][N][D] bf16
@@ -83,7 +84,7 @@ struct CoopArgs {
   int64_t rows_per_item;       // multiple of 32
   float* part_stats;           // [spb][B][K][JP]
   double* ll_part;             // [B][spb] natural-log partial sums
-  uint64_t* xch;               // [NG][kRing][G][32] exchanged (max, ±sum) words, zeroed by the launcher
+  uint64_t* xch;               // [NG][kRing][G][32] exchanged (max, tagged sum) words, set by the launcher
   unsigned* status;            // nonzero after a timed-out wait (zeroed by the launcher)
   int spin_limit;
 };

@@ -35,7 +35,7 @@ __device__ T block_sum(T v, T* scratch) {
 // Σ_k max(w_k, floor) over one batch row, identical in every block.
 __device__ float weight_total(const float* w, int K, float floor_v, float* scratch) {
   float s = 0.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) s += fmaxf(w[k], floor_v);
+  for (int k = threadIdx.x; k < K; k += blockDim.x) s += clamp_lo(w[k], floor_v);
   return block_sum(s, scratch);
 }
 
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
   const float floor_v = a.prelude ? a.min_weight : -INFINITY;
   const float total = a.prelude ? weight_total(wrow, K, floor_v, scratch) : 1.f;
   const size_t bk = (size_t)b * K + k;
-  const float wk = a.prelude ? fmaxf(wrow[k], floor_v) / total : wrow[k];
+  const float wk = a.prelude ? clamp_lo(wrow[k], floor_v) / total : wrow[k];
   const float lw = logf(wk);
   const float* mu = a.means + bk * D;
   // bf16 x (spherical) computes with bf16 means, as the reference keeps them in
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
 
   if (a.cov == SPH) {
     float var = a.covs[bk];
-    if (a.prelude) var = fmaxf(var, a.reg_covar);
+    if (a.prelude) var = clamp_lo(var, a.reg_covar);
     if (lane == 0) a.covs_used[bk] = var;
     float msq = 0.f;
     for (int d = lane; d < D; d += 64) msq = fmaf(mus[d], mus[d], msq);
@@ -120,9 +120,9 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
     float logdet = 0.f, mpm = 0.f;
     for (int d = lane; d < D; d += 64) {
       float v = vr[d];
-      if (a.prelude) v = fmaxf(v, a.reg_covar);
+      if (a.prelude) v = clamp_lo(v, a.reg_covar);
       vu[d] = v;
-      const float vc = fmaxf(v, 1e-30f);
+      const float vc = clamp_lo(v, 1e-30f);
       const float p = 1.f / vc;
       const float wm = mus[d] * p;
       logdet += logf(vc);
@@ -781,7 +781,7 @@ __global__ __launch_bounds__(64 * kRedWaves) void reduce_slices_kernel(const flo
 __device__ float finalize_total(const FinalizeArgs& a, int b, float* scratch) {
   const float* st = a.stats + (size_t)b * a.K * a.JP + a.nk_col;
   float part = 0.f;
-  for (int k = threadIdx.x; k < a.K; k += blockDim.x) part += fmaxf(st[(size_t)k * a.JP] / (float)a.N, a.min_weight);
+  for (int k = threadIdx.x; k < a.K; k += blockDim.x) part += clamp_lo(st[(size_t)k * a.JP] / (float)a.N, a.min_weight);
   return block_sum(part, scratch);
 }
 
@@ -795,7 +795,7 @@ __device__ void finalize_comp(const FinalizeArgs& a, int b, int k, float total) 
   const float* sk = a.stats + bk * a.JP;
   const float nk = sk[a.nk_col];
   const bool active = nk > a.min_weight;
-  const float nk_safe = fmaxf(nk, a.min_weight);
+  const float nk_safe = clamp_lo(nk, a.min_weight);
   float* mu = a.means + bk * D;
   float msq = 0.f;
   for (int d = lane; d < D; d += 64) {
@@ -805,7 +805,7 @@ __device__ void finalize_comp(const FinalizeArgs& a, int b, int k, float total) 
     mu[d] = a.bf_means ? (float)(__bf16)m : m;
     msq = fmaf(m, m, msq);
     if (a.cov == DIAG) {
-      const float v = fmaxf(sk[a.DP + d] / nk_safe - m * m, a.reg_covar);
+      const float v = clamp_lo(sk[a.DP + d] / nk_safe - m * m, a.reg_covar);
       a.covs[bk * D + d] = active ? v : a.covs_used[bk * D + d];
     }
   }
@@ -813,11 +813,11 @@ __device__ void finalize_comp(const FinalizeArgs& a, int b, int k, float total) 
     for (int off = 32; off >= 1; off /= 2) msq += __shfl_xor(msq, off);
     float sq = 0.f;
     for (int i = 0; i < a.sq_n; ++i) sq += sk[a.sq_col + i];
-    float v = fmaxf(sq - nk * msq, 0.f) / (nk_safe * (float)D);
-    v = fmaxf(v, a.reg_covar);
+    float v = clamp_lo(sq - nk * msq, 0.f) / (nk_safe * (float)D);
+    v = clamp_lo(v, a.reg_covar);
     if (lane == 0) a.covs[bk] = active ? v : a.covs_used[bk];
   }
-  if (lane == 0) a.weights[bk] = fmaxf(nk / (float)a.N, a.min_weight) / total;
+  if (lane == 0) a.weights[bk] = clamp_lo(nk / (float)a.N, a.min_weight) / total;
 }
 
 // One wave per component, kFinWaves components per block.
@@ -876,7 +876,7 @@ __global__ void finalize_full_kernel(FinalizeArgs a) {
   const float* sk = a.stats + bk * JP;
   const float nk = sk[a.nk_col];
   const bool active = nk > a.min_weight;
-  const float nk_safe = fmaxf(nk, a.min_weight);
+  const float nk_safe = clamp_lo(nk, a.min_weight);
   const float* mu = a.means + bk * D;
   const float sxx = sk[DP + full_feature(d < e ? d : e, d < e ? e : d)];
   const float ade = (sxx - nk * (mu[d] * mu[e])) / nk_safe;
@@ -924,11 +924,11 @@ __global__ void pack_stats_kernel(PackArgs a) {
   for (int d = 0; d < D; ++d) sk[d] = a.sum_x[bk * D + d];
   if (a.cov == SPH) {
     sk[a.sq_col] = a.sum_q[bk];
-    a.covs_used[bk] = fmaxf(a.covs[bk], a.reg_covar);
+    a.covs_used[bk] = clamp_lo(a.covs[bk], a.reg_covar);
   } else if (a.cov == DIAG) {
     for (int d = 0; d < D; ++d) {
       sk[DP + d] = a.sum_q[bk * D + d];
-      a.covs_used[bk * D + d] = fmaxf(a.covs[bk * D + d], a.reg_covar);
+      a.covs_used[bk * D + d] = clamp_lo(a.covs[bk * D + d], a.reg_covar);
     }
   } else if (a.cov == FULL) {
     for (int d = 0; d < D; ++d)

@@ -95,6 +95,23 @@ def _init_weights(init_weights, bsz, k, device):
     return (w / w.sum(dim=-1, keepdim=True)).contiguous()
 
 
+def flash_kmeans_emulated() -> bool:
+    """Whether ``init_params="kmeans"`` runs the k-means initialisation.
+
+    The reference runs k-means only when the optional flash-kmeans package
+    imports (``_kmeans_initialize`` returns None without it,
+    torch_fallback.py:1571-1582); its default ``init_params="kmeans"`` then
+    silently becomes random rows plus the global variance with
+    ``init_source="random"`` (:1700-1727, and likewise :1747-1774, :1807-1834,
+    :1867-1894).  This engine runs the k-means initialisation on the device by
+    default, i.e. it behaves like a reference with flash-kmeans installed.
+    ``GMMXX_HIP_FLASH_KMEANS=0`` reproduces a reference without it: the random
+    branch, drawn from the same global RNG call (``torch.randint`` on x's
+    device) as the reference's ``_random_init_means`` (:1384-1387)."""
+    import os
+    return os.environ.get("GMMXX_HIP_FLASH_KMEANS", "1") != "0"
+
+
 def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init_means=None,
                init_covs=None, init_weights=None, reg_covar: float = 1e-6,
                init_params: str = "kmeans", generator: Optional[torch.Generator] = None,
@@ -105,7 +122,8 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
     (torch_fallback.py:1661-1682, :1731-1742, :1791-1802, :1851-1862).  Without
     ``init_means``, ``init_params="kmeans"`` runs k-means++ seeding, Lloyd
     refinement and the hard-label statistics on the device (``kmeans.py``; the
-    reference's branch at :1701-1716, :1747-1762, :1807-1822, :1867-1882), and
+    reference's branch at :1701-1716, :1747-1762, :1807-1822, :1867-1882) --
+    unless ``GMMXX_HIP_FLASH_KMEANS=0`` (see ``flash_kmeans_emulated``) -- and
     ``"random"`` takes random data rows plus the global variance (:1718-1727).
     """
     bsz, n, d = x.shape
@@ -120,7 +138,7 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
         if init_params not in {"kmeans", "random"}:
             raise ValueError("init_params must be 'kmeans' or 'random'")
         k = int(n_components)
-        if init_params == "kmeans":
+        if init_params == "kmeans" and flash_kmeans_emulated():
             from . import kmeans
             means, covs, weights = kmeans.kmeans_initialize(
                 x, covariance_type, k, max_iters=kmeans_init_iters, tol=kmeans_init_tol, reg_covar=reg_covar,
@@ -340,16 +358,41 @@ def _api(covariance_type):
             if key not in {"chunk_size_N", "chunk_size_K", "kmeans_use_triton", "gmm_use_triton",
                            "gmm_use_triton_estep", "gmm_use_triton_streaming_update"}:
                 raise TypeError(f"unexpected keyword argument {key!r}")
-        return fit(x, n_components, covariance_type, max_iters=max_iters, tol=tol, init_means=init_means,
-                   init_covs=init_variances, init_weights=init_weights, verbose=verbose,
-                   init_params=init_params, reg_covar=reg_covar, min_weight=min_weight,
-                   compute_labels=compute_labels, generator=generator, approx_top_k=approx_top_k,
-                   kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol,
-                   record_all_lower_bounds=record_all_lower_bounds)
+        x_dev, home = _to_engine_device(x)
+        labels, means, covs, weights, info = fit(
+            x_dev, n_components, covariance_type, max_iters=max_iters, tol=tol, init_means=init_means,
+            init_covs=init_variances, init_weights=init_weights, verbose=verbose,
+            init_params=init_params, reg_covar=reg_covar, min_weight=min_weight,
+            compute_labels=compute_labels, generator=generator, approx_top_k=approx_top_k,
+            kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol,
+            record_all_lower_bounds=record_all_lower_bounds)
+        return (*_to_home((labels, means, covs, weights), home), info)
     run.__name__ = f"batch_gmm_{ {'diag': 'Diagonal'}.get(covariance_type, covariance_type.capitalize()) }_hip"
     run.__doc__ = (f"{covariance_type} soft EM on the HIP engine; signature and return value of "
-                   f"the reference's batch_gmm_*_torch_native (chunk/Triton knobs are accepted and ignored).")
+                   f"the reference's batch_gmm_*_torch_native (chunk/Triton knobs are accepted and ignored). "
+                   f"Host (CPU) input is copied to the current GPU and the results come back to the "
+                   f"input's device, so a caller of the reference's CPU function gets CPU tensors.")
     return run
+
+
+def _to_engine_device(x):
+    """(x on a GPU, the device the caller's tensors live on).  The reference's
+    ``*_torch_native`` functions run wherever x is, CPU included; here the work
+    always runs on the GPU, so host input is copied to the current device once
+    and the results are copied back (the estimator does the same)."""
+    if not torch.is_tensor(x):
+        raise TypeError("x must be a torch.Tensor")
+    if x.is_cuda:
+        return x, None
+    if not torch.cuda.is_available():
+        raise _hip.HipBackendUnavailable("the hip backend needs a GPU; none is visible")
+    return x.to(torch.device("cuda", torch.cuda.current_device())), x.device
+
+
+def _to_home(tensors, home):
+    if home is None:
+        return tuple(tensors)
+    return tuple(None if t is None else t.to(home) for t in tensors)
 
 
 batch_gmm_Spherical_hip = _api("spherical")
@@ -368,18 +411,26 @@ batch_gmm_Full = batch_gmm_Full_torch_native = batch_gmm_full = batch_gmm_Full_h
 
 def _chunked(covariance_type, what):
     """<cov>_<assign|score_samples|predict_proba>_torch_native_chunked
-    (gmmxx/torch_fallback.py:780-1345) on the HIP kernels: (x, means, covariances,
-    weights) on the GPU; chunk sizes are accepted and ignored (the library tiles
-    rows and components itself).  bf16/fp16 x is computed in fp32, as the
-    reference's chunked functions do."""
+    (gmmxx/torch_fallback.py:780-1345) on the HIP kernels.  Host input is copied
+    to the current GPU and the result comes back to x's device; chunk sizes are
+    accepted and ignored (the library tiles rows and components itself).
+    Scores and responsibilities are returned in x's dtype and labels as int64,
+    as the reference returns them.  One deliberate difference: bf16/fp16 x is
+    computed in fp32 here (the reference's chunked functions compute in x's
+    dtype, :780-821), so the values are the fp32 algorithm's rounded to x's
+    dtype rather than the result of half-precision arithmetic."""
     def run(x, means, variances, weights, *, chunk_size_N=32768, chunk_size_K=1024):
-        xd = x if x.dtype == torch.float32 else x.to(torch.float32)
-        args = (covariance_type, xd, means, variances, weights)
+        xd, home = _to_engine_device(x)
+        dev = xd.device
+        xd = xd if xd.dtype == torch.float32 else xd.to(torch.float32)
+        args = (covariance_type, xd, *(t.to(dev) for t in (means, variances, weights)))
         if what == "assign":
-            return _hip.score(*args, want_scores=False, want_labels=True)[1]
-        if what == "score_samples":
-            return _hip.score(*args, want_scores=True, want_labels=False)[0]
-        return _hip.predict_proba(*args)
+            out = _hip.score(*args, want_scores=False, want_labels=True)[1]
+        elif what == "score_samples":
+            out = _hip.score(*args, want_scores=True, want_labels=False)[0].to(x.dtype)
+        else:
+            out = _hip.predict_proba(*args).to(x.dtype)
+        return out if home is None else out.to(home)
     prefix = {"diag": "diagonal"}.get(covariance_type, covariance_type)
     run.__name__ = f"{prefix}_{what}_torch_native_chunked"
     run.__doc__ = _chunked.__doc__

@@ -304,6 +304,7 @@ class GMMXX:
                 init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit,
                 approx_top_k=self.approx_top_k, kmeans_init_iters=self.init_kmeans_iters,
                 kmeans_init_tol=self.init_kmeans_tol)
+        self._scores_cache = None
         self.cluster_ids_b = labels_b
         self.means_b = means_b
         self.variances_b = covs_b
@@ -447,20 +448,28 @@ class GMMXX:
         (the same E-step gives both), for a score_samples call on the same,
         unmodified tensor under the same fitted parameters."""
         try:
-            self._scores_cache = (weakref.ref(data), data._version, self._param_versions(), scores)
+            params = self._fitted_params()
+            self._scores_cache = (weakref.ref(data), data._version, tuple(weakref.ref(t) for t in params),
+                                  tuple(t._version for t in params), scores)
         except TypeError:
             self._scores_cache = None
 
-    def _param_versions(self):
-        return tuple((id(t), t._version) for t in (self.means_b, self.variances_b, self.weights_b))
+    def _fitted_params(self):
+        return (self.means_b, self.variances_b, self.weights_b)
 
     def _cached_scores(self, data: torch.Tensor) -> Optional[torch.Tensor]:
+        """The cached scores when ``data`` and the fitted parameter tensors are
+        the very objects (identity through weak references, never ``id()``,
+        which a new tensor can reuse after a refit) at the same versions."""
         c = self._scores_cache
-        if (c is None or not torch.is_tensor(data) or c[0]() is not data or c[1] != data._version
-                or c[2] != self._param_versions()):
+        if c is None or not torch.is_tensor(data) or c[0]() is not data or c[1] != data._version:
+            return None
+        params = self._fitted_params()
+        if (any(r() is not t for r, t in zip(c[2], params))
+                or c[3] != tuple(t._version for t in params)):
             return None
         self._scores_cache = None
-        return c[3]
+        return c[4]
 
     def predict_proba(self, data: torch.Tensor) -> torch.Tensor:
         """Responsibilities (B, N, K) fp32 (gmmxx/interface.py:1973-2268).  The

@@ -100,11 +100,18 @@ int gmmxx_hip_em_step(const gmmxx_problem* p, const void* x, float* means, float
                       float* lower_bound, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Asynchronous failures of earlier calls on this workspace: the word is nonzero
- * when a single-pass cooperative launch (spherical bf16 at D = 128,
- * 256 < K <= 1024) gave up waiting for a partner workgroup.  Such an iteration
- * writes NaN to its lower bound (or ll_sum) and leaves the parameters
- * unchanged.  Copies the word into *status_out (device memory, 1 uint32) and
- * clears it, stream-ordered.  A newly allocated workspace holds arbitrary
+ * when a single pass whose workgroups exchange row partials gave up waiting for
+ * a partner workgroup (the members of a group were not all resident: another
+ * kernel or process held part of the GPU).  Two passes do this: the cooperative
+ * kernel (spherical bf16 at D = 128, 256 < K <= 1024; GMMXX_HIP_NO_COOP=1
+ * selects two passes instead) and the exchange pass (fp32 x: spherical at
+ * D <= 128, tied and diag at D <= 64, each with 256 < K <= 1024, i.e. two to
+ * four component tiles of 256; GMMXX_HIP_NO_XCH=1 selects two passes
+ * instead).  Such an iteration writes NaN to its lower bound (or ll_sum) and
+ * leaves the parameters unchanged.  A non-finite input row does not stall the
+ * exchange: it propagates into the lower bound and parameters as in the
+ * reference, and the word stays 0.  Copies the word into *status_out (device
+ * memory, 1 uint32) and clears it, stream-ordered.  A newly allocated workspace holds arbitrary
  * bytes: zero it, or call this once and discard the result, before the calls
  * whose status is wanted.  No reference counterpart: the reference's kernels
  * report errors synchronously through TORCH_CHECK (gmmxx/_cuda.py:41-54); this
@@ -119,6 +126,10 @@ int gmmxx_hip_take_status(const gmmxx_problem* p, void* workspace, int64_t works
  * 64 MiB are refused with GMMXX_ERR_WORKSPACE before any launch.  Every call
  * on one device shares that device's scratch: calls that overlap on one
  * device (two streams, two threads) race and must be ordered by the caller.
+ * The call clears the scratch's status words first and there is no workspace
+ * to pass to gmmxx_hip_take_status, so a single pass that timed out waiting
+ * for a partner workgroup (see gmmxx_hip_take_status) shows only as a NaN
+ * *lower_bound with the parameters left unchanged: check the lower bound.
  * Call with the stream's device current.  No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). */

@@ -334,6 +334,27 @@ def _init_weights(init_weights, x, k):
     return w / w.sum(dim=-1, keepdim=True)
 
 
+def random_initialize(x, covariance_type, n_components, indices, reg_covar):
+    """The random branch of the four initialisers, which is also what
+    ``init_params="kmeans"`` runs when flash-kmeans does not import
+    (torch_fallback.py:1571-1582 returns None): rows ``indices`` (B, K) of x as
+    the means (``_random_init_means`` :1384-1387 with its torch.randint draw
+    given), the global (co)variance (:1348-1381) and weights 1/K
+    (:1718-1727, :1766-1774, :1826-1834, :1886-1894)."""
+    bsz, _, d = x.shape
+    means = torch.gather(x, 1, indices[..., None].expand(-1, -1, d)).clone()
+    if covariance_type == "spherical":
+        covs = global_spherical_variance(x, n_components, reg_covar)
+    elif covariance_type == "diag":
+        covs = global_diag_variance(x, n_components, reg_covar)
+    elif covariance_type == "tied":
+        covs = global_tied_covariance(x, reg_covar)
+    else:
+        covs = global_tied_covariance(x, reg_covar).unsqueeze(1).expand(-1, n_components, -1, -1).clone()
+    weights = torch.full((bsz, n_components), 1.0 / float(n_components), dtype=x.dtype)
+    return means, covs, weights
+
+
 def init_user_parameters(x, covariance_type, init_means, init_covs, init_weights, reg_covar,
                          x_sq=None):
     """Explicit-init branch of the four initialisers

@@ -132,3 +132,36 @@ def test_lloyd_stop_rule_mid_run_vs_float64(hip):
     means, nk, sx, sq, it = kmeans.lloyd(xd, "spherical", seeds.to(DEV), 12, tol, kmeans._HardStats(xd, "spherical", 5))
     assert it == e_it
     torch.testing.assert_close(means.cpu().double(), torch.from_numpy(e_c), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("cov", ["spherical", "diag", "tied", "full"])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_without_flash_kmeans_default_init_is_the_reference_random_branch(hip, monkeypatch, cov, dt):
+    """GMMXX_HIP_FLASH_KMEANS=0: init_params="kmeans" falls back to random rows
+    plus the global (co)variance and weights 1/K with init_source "random", as
+    the reference does when flash-kmeans does not import
+    (torch_fallback.py:1571-1582, :1700-1727).  The rows come from the same
+    global-RNG torch.randint call on x's device, so the test draws the indices
+    the same way and hands them to the oracle's restatement."""
+    if dt == torch.bfloat16 and cov != "spherical":
+        pytest.skip("bf16 x keeps its own engine only for spherical")
+    monkeypatch.setenv("GMMXX_HIP_FLASH_KMEANS", "0")
+    b, n, d, k = 2, 3000, 12, 9
+    x, _, _, _ = make_problem(cov, b, n, d, k, seed=58, dtype=dt)
+    xd = to_dev(x, dt)
+    torch.manual_seed(123)
+    means, covs, weights, source = em.initialize(xd, cov, k, init_params="kmeans")
+    assert source == "random"
+    torch.manual_seed(123)
+    idx = torch.randint(0, n, (b, k), device=DEV).cpu()
+    e_m, e_c, e_w = torch_ref.random_initialize(x, cov, k, idx, 1e-6)
+    assert torch.equal(means.cpu(), e_m)          # rows of x (bf16 values for bf16 x): bit-exact
+    torch.testing.assert_close(covs.cpu(), e_c, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(weights.cpu(), e_w, rtol=1e-6, atol=0)
+    # the whole estimator reports the reference's init_source
+    est = GMMXX(n_components=k, covariance_type=cov, max_iter=2, tol=0.0, random_state=4, backend="hip")
+    est.fit(xd)
+    assert est.init_source_ == "random"
+    monkeypatch.setenv("GMMXX_HIP_FLASH_KMEANS", "1")
+    est.fit(xd)
+    assert est.init_source_ == "kmeans"

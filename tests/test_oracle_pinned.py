@@ -332,3 +332,33 @@ def test_topk_all_but_unreachable_equals_exact(cov):
     # top_k >= K resolves to exact EM (gmmxx/torch_fallback.py:598-606)
     assert torch_ref.fit(x, 4, cov, max_iters=1, init_means=means, init_covs=covs, init_weights=w,
                          approx_top_k=4)[4]["approximate_em_enabled"] is False
+
+
+@pytest.mark.parametrize("cov", COVS)
+def test_random_initialize_matches_numpy_float64(cov):
+    """The random-init branch (what init_params="kmeans" runs without
+    flash-kmeans): means are the drawn rows, the variances numpy's float64
+    population (co)variance of x (spherical: the mean of the per-feature
+    variances), weights 1/K; reg_covar added on the diagonal (tied, full) or
+    used as the floor (spherical, diag)."""
+    g = torch.Generator().manual_seed(8)
+    b, n, d, k = 2, 500, 5, 4
+    x = torch.randn((b, n, d), generator=g) * 3.0 + 1.0
+    idx = torch.randint(0, n, (b, k), generator=g)
+    m, c, w = torch_ref.random_initialize(x, cov, k, idx, 1e-6)
+    xn = x.double().numpy()
+    for bi in range(b):
+        np.testing.assert_array_equal(m[bi].numpy(), x[bi, idx[bi]].numpy())
+        var = xn[bi].var(axis=0)                    # population variance per feature
+        cov_np = np.cov(xn[bi].T, bias=True)
+        if cov == "spherical":
+            np.testing.assert_allclose(c[bi].double().numpy(), np.full(k, var.mean()), rtol=1e-5)
+        elif cov == "diag":
+            np.testing.assert_allclose(c[bi].double().numpy(), np.tile(var, (k, 1)), rtol=1e-5)
+        else:
+            exp = cov_np + 1e-6 * np.eye(d)
+            got = c[bi].double().numpy()
+            got = got if cov == "tied" else got.reshape(k, d, d)
+            np.testing.assert_allclose(got, exp if cov == "tied" else np.broadcast_to(exp, (k, d, d)),
+                                       rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(w.numpy(), np.full((b, k), 1.0 / k), rtol=1e-7)
