@@ -195,8 +195,11 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
   const int kbase = mem * (kNW * kCW) + __builtin_amdgcn_readfirstlane(wave) * kCW;
   uint64_t* const gxch = a.xch + (size_t)grp * kRing * G * kBN;
 
-  // Constant augmented columns 8..31 of every staged row: [1 0 0 ...]; the
-  // e slots start at zero, so no LDS word is read before it is written.
+  // Staged rows start at zero: the lead-in blocks multiply r = 0 by buffers no
+  // block has filled yet, which must not hold NaN bit patterns.
+  for (int i = tid; i < kNB * kBN * XS / 8; i += NTHR) *reinterpret_cast<uint4*>(xs + 8 * i) = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  // Constant augmented columns 8..31 of every staged row: [1 0 0 ...].
   for (int i = tid; i < kNB * kBN * 3; i += NTHR) {
     const int row = i / 3, ch = 1 + i % 3;
     const uint4 w = make_uint4(ch == 1 ? pack2((__bf16)1.f, (__bf16)0.f) : 0u, 0u, 0u, 0u);
@@ -306,7 +309,9 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     auto prep_r = [&](auto PB_, int rf, int nr) {
       constexpr int pb = decltype(PB_)::value;
       const float l2 = lse_s[pb * kBN + lr];     // read unconditionally: no branch around the LDS load
-      const float f = (rf + lr < nr) ? fast_exp2(mw[pb] - l2) : 0.f;
+      // rows outside the item (the pipeline's lead-in and drain blocks) get r = 0
+      const bool valid = rf + lr >= 0 && rf + lr < nr;
+      const float f = valid ? fast_exp2(mw[pb] - l2) : 0.f;
       __bf16* rrow = rs + wave * kBN * kRS + lr * kRS;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -345,19 +350,32 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
     // applied after the MFMA, and the augmented chunk carries the rest.
     auto egemm = [&](int bx) -> f32x16 {
       const __bf16* xr = xs + bx * kBN * XS + lr * XS + 8 * hf;
-      const f32x16 A = mfma32(waug, ld16<bf16x8>(xr + DP), f32x16{});
-      f32x16 T = f32x16{};
+      // Operand j of the XK + 1 MFMAs (0: augmented chunk, 1 + t: k-step t) in a
+      // rotating three-register-set pipeline, read two MFMAs ahead, so the chain
+      // waits for one LDS latency instead of one per MFMA.
+      auto opnd = [&](int j) { return ld16<bf16x8>(j == 0 ? xr + DP : xr + 16 * (j - 1)); };
+      bf16x8 ob[3];
+      ob[0] = opnd(0);
+      ob[1] = opnd(1);
+      ob[2] = opnd(2);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+      f32x16 A = f32x16{}, T = f32x16{};
 #pragma unroll
-      for (int t = 0; t < XK; ++t) T = mfma32(wmu[t], ld16<bf16x8>(xr + 16 * t), T);
+      for (int j = 0; j <= XK; ++j) {
+        if (j == 0) A = mfma32(waug, ob[0], f32x16{});
+        else T = mfma32(wmu[j - 1], ob[j % 3], T);
+        if (j + 3 <= XK) ob[j % 3] = opnd(j + 3);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (j + 3 <= XK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
 #pragma unroll
       for (int v = 0; v < 16; ++v) T[v] = fmaf(sc[v], T[v], A[v]);
       return T;
     };
     // E epilogue: wave row maxima m_w, e = 2^(l2 - m_w) (kept in er of the block
     // parity) and the wave's row sums for the workgroup combine; a row's 32
-    // components sit in lanes lr and lr + 32.  lse_epilogue does all three for
-    // the steps without an M-GEMM; the steady state puts the exponentials
-    // between the M-GEMM's MFMAs (see step).
+    // components sit in lanes lr and lr + 32.  The exponentials go between the
+    // M-GEMM's MFMAs (see step).
     auto row_max = [&](const f32x16& T) {
       float m = T[0];
 #pragma unroll
@@ -376,27 +394,28 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       red_m[(pb * kNW + wave) * RR + lr] = m;
       red_s[(pb * kNW + wave) * RR + lr] = sum;
     };
-    auto lse_epilogue = [&](const f32x16& T, auto PB_) {
-      constexpr int pb = decltype(PB_)::value;
-      const float m = row_max(T);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) er[pb][v] = fast_exp2(T[v] - m);
-      lse_sums(m, PB_);
-    };
     if (nblk > 0) { fetch(0); stash(0); }
     if (nblk > 1) { fetch(kBN); stash(1); }
+    if (nblk > 2) fetch(2 * kBN);
     __syncthreads();
 
-    // Iteration i of the block pipeline.  FIN: block i-2 is finished (i >= 2);
-    // EGM: block i is computed (i < nblk); PB = i & 1, the LDS/register slot
-    // parity of blocks i and i-2.  The flags are compile-time, so the steady
-    // state (both) is one basic block per half that the scheduler interleaves.
-    auto step = [&](auto FIN_, auto EGM_, auto PB_, int i) {
-      constexpr bool FIN = decltype(FIN_)::value, EGM = decltype(EGM_)::value;
+    // Iteration i of the block pipeline, i = 0 .. nblk + 1 (rounded up to even):
+    // the E-GEMM of block i and the M-GEMM of block i-2.  Every iteration runs
+    // the same code: the lead-in blocks -2, -1 and the drain blocks nblk,
+    // nblk + 1 compute on zeroed or stale staged rows (in bounds) and add
+    // nothing, since their rows get r = 0 and take part in no exchange and no
+    // log-likelihood.  PB = i & 1, the LDS/register slot parity of blocks i
+    // and i-2.
+#pragma unroll
+    for (int pb = 0; pb < 2; ++pb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) er[pb][v] = 0.f;
+      mw[pb] = 0.f;
+    }
+    auto step = [&](auto PB_, int i) {
       constexpr int PB = decltype(PB_)::value;
       const int r0 = i * kBN;                     // first row of block i in the item
-      const bool ahead = i + 2 < nblk;
-      if (ahead) fetch(r0 + 2 * kBN);
+      const bool ahead = i + 2 < nblk;            // block i+2 is in the prefetch registers
       const bool xchg = wave == 0 && i >= 1 && i <= nblk;   // wave 0 collects block i-1
       const bool pubw = wave == 1 && i >= 1 && i <= nblk;   // wave 1 publishes block i-1
 
@@ -407,13 +426,19 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       if (pubw) {
         if (lane < kBN) {
           constexpr int qb = PB ^ 1;              // parity of block i-1
-          float M = red_m[(qb * kNW) * RR + lane];
+          // all sixteen partials read before any is used: one LDS latency
+          float pm[kNW], ps[kNW];
 #pragma unroll
-          for (int w = 1; w < kNW; ++w) M = fmaxf(M, red_m[(qb * kNW + w) * RR + lane]);
+          for (int w = 0; w < kNW; ++w) {
+            pm[w] = red_m[(qb * kNW + w) * RR + lane];
+            ps[w] = red_s[(qb * kNW + w) * RR + lane];
+          }
+          float M = pm[0];
+#pragma unroll
+          for (int w = 1; w < kNW; ++w) M = fmaxf(M, pm[w]);
           float S = 0.f;
 #pragma unroll
-          for (int w = 0; w < kNW; ++w)
-            S += red_s[(qb * kNW + w) * RR + lane] * fast_exp2(red_m[(qb * kNW + w) * RR + lane] - M);
+          for (int w = 0; w < kNW; ++w) S += ps[w] * fast_exp2(pm[w] - M);
           ownM = M;
           ownS = S;
           if (G > 1) {
@@ -428,8 +453,8 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
 
       // ---- responsibilities of block i-2 with the E-GEMM of block i ----
       f32x16 T;
-      if constexpr (FIN) prep_r(PB_, r0 - 2 * kBN, nrows);
-      if constexpr (EGM) T = egemm(i % kNB);
+      prep_r(PB_, r0 - 2 * kBN, nrows);
+      T = egemm(i % kNB);
 
       // ---- wave 0: the group's words of block i-1 (published at the top of this
       // iteration; this workgroup's own included), loaded now and checked after
@@ -447,33 +472,26 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       if (KG > 1 && xchg && !dead) load_words();
 
       // ---- M-GEMM of block i-2 with the E epilogue of block i ----
-      if constexpr (FIN) {
-        // The staging writes of prep_r and the transposing reads below are LDS
-        // operations of this wave only, executed in order; keep the compiler
-        // from reordering them.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      }
-      if constexpr (FIN && EGM) {
+      // The staging writes of prep_r and the transposing reads below are LDS
+      // operations of this wave only, executed in order; keep the compiler
+      // from reordering them.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      {
         // The exponentials of block i go between the M-GEMM MFMAs of block i-2:
         // the transcendental unit then works while the matrix core does
         // (measured 2 % faster per C2 pass than after the M-GEMM).
         const float m = row_max(T);
-        mgemm((i - 2) % kNB, [&](int k) {
+        mgemm((i + kNB - 2) % kNB, [&](int k) {
           if (k < 8) {
             er[PB][2 * k] = fast_exp2(T[2 * k] - m);
             er[PB][2 * k + 1] = fast_exp2(T[2 * k + 1] - m);
           }
         });
         lse_sums(m, PB_);
-      } else {
-        if constexpr (FIN) mgemm((i - 2) % kNB, [](int) {});
-        if constexpr (EGM) lse_epilogue(T, PB_);
       }
-      if constexpr (FIN) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
       // ---- wave 0: the group's log-normalisers of block i-1 ----
       if (xchg) {
@@ -524,26 +542,18 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
       }
 
       if (ahead) stash((i + 2) % kNB);
+      // The next block's rows are fetched now, a whole iteration before they are
+      // staged: waits on the exchange's memory operations during that iteration
+      // (the vector memory counter is in order) find them arrived.
+      if (i + 3 < nblk) fetch(r0 + 3 * kBN);
       __syncthreads();
     };
-    using T_ = std::integral_constant<bool, true>;
-    using F_ = std::integral_constant<bool, false>;
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
-    step(F_{}, T_{}, P0{}, 0);                                  // nblk >= 1
-    if (nblk > 1) step(F_{}, T_{}, P1{}, 1);
-    else step(F_{}, F_{}, P1{}, 1);
-    int i = 2;
-    for (; i + 1 < nblk; i += 2) {
-      step(T_{}, T_{}, P0{}, i);
-      step(T_{}, T_{}, P1{}, i + 1);
+    for (int i = 0; i < nblk + 2; i += 2) {
+      step(P0{}, i);
+      step(P1{}, i + 1);
     }
-    if (i < nblk) { step(T_{}, T_{}, P0{}, i); ++i; }
-    // drain: the last two blocks are finished (i = nblk, nblk + 1); an item of
-    // one block has only block 0 left (i = 2), and block 1 was never staged.
-    if (nblk == 1) step(T_{}, F_{}, P0{}, 2);
-    else if (i & 1) { step(T_{}, F_{}, P1{}, i); step(T_{}, F_{}, P0{}, i + 1); }
-    else { step(T_{}, F_{}, P0{}, i); step(T_{}, F_{}, P1{}, i + 1); }
     seq += (unsigned)nblk;
 
     // ---- the item's partial statistics (lane (lr, hf), register v: component

@@ -595,6 +595,15 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
     for (int ct = 0; ct < CT; ++ct) { A.t[ct][0] = f32x4{0.f, 0.f, 0.f, 0.f}; A.t[ct][1] = A.t[ct][0]; }
     if constexpr (X3) {
       // Six products per k-step, the smallest first: W1φ3, W3φ1, W2φ2, W1φ2, W2φ1, W1φ1.
+      // Full covariance sums the five correction products in an accumulator of
+      // their own: its logits are differences of terms ~10^2 times larger, and
+      // adding each small product to the large running sum would round it at
+      // that sum's magnitude (five roundings per k-step instead of one).
+      constexpr bool SPLIT = COV == FULL;
+      Acc Bs;
+      if constexpr (SPLIT)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) { Bs.t[ct][0] = A.t[ct][0]; Bs.t[ct][1] = A.t[ct][0]; }
 #pragma unroll
       for (int ec = 0; ec < X3K; ++ec) {
         bf16x8 xv[3][2];
@@ -613,14 +622,18 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
               return LSE ? mfma_bf16(w, x, c) : mfma_bf16(x, w, c);
             };
             const bf16x8 wp3 = W3L ? w3s[((wave * CT + ct) * X3K + ec) * 64 + lane] : w3[W3L ? 0 : 2][ct][ec];
-            A.t[ct][h] = mm(w3[0][ct][ec], xv[2][h], A.t[ct][h]);
-            A.t[ct][h] = mm(wp3, xv[0][h], A.t[ct][h]);
-            A.t[ct][h] = mm(w3[1][ct][ec], xv[1][h], A.t[ct][h]);
-            A.t[ct][h] = mm(w3[0][ct][ec], xv[1][h], A.t[ct][h]);
-            A.t[ct][h] = mm(w3[1][ct][ec], xv[0][h], A.t[ct][h]);
+            f32x4& sm = SPLIT ? Bs.t[ct][h] : A.t[ct][h];
+            sm = mm(w3[0][ct][ec], xv[2][h], sm);
+            sm = mm(wp3, xv[0][h], sm);
+            sm = mm(w3[1][ct][ec], xv[1][h], sm);
+            sm = mm(w3[0][ct][ec], xv[1][h], sm);
+            sm = mm(w3[1][ct][ec], xv[0][h], sm);
             A.t[ct][h] = mm(w3[0][ct][ec], xv[0][h], A.t[ct][h]);
           }
       }
+      if constexpr (SPLIT)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) { A.t[ct][0] += Bs.t[ct][0]; A.t[ct][1] += Bs.t[ct][1]; }
       return A;
     } else {
 #pragma unroll

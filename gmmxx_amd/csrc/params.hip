@@ -165,23 +165,33 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
       }
     }
   } else {
-    // FULL: W_k = [packed P_k with doubled off-diagonal | -2 P_k μ_k]  (torch_fallback.py:418-432)
+    // FULL: W_k = [packed P_k with doubled off-diagonal | -2 P_k μ_k]  (torch_fallback.py:418-432).
+    // The entries, P_k μ_k and μ_kᵀP_kμ_k are formed in float64 from the precision
+    // and its residual (P + P_lo, the float64 inverse) and rounded once: the
+    // logit's terms reach ~10^2 times the logit, so each fp32 rounding on the
+    // way (the off-diagonal sum, the Pμ and μᵀPμ chains, the constant) would
+    // add an error of that order.
     const float* P = a.prec + bk * D * D;
+    const float* Pl = a.prec_lo ? a.prec_lo + bk * D * D : nullptr;
+    auto pd = [&](int d, int e) { return (double)P[d * D + e] + (Pl ? (double)Pl[d * D + e] : 0.0); };
     const int S = DP * (DP + 1) / 2;
     for (int e = lane; e < EP; e += 64) put_f32(e, 0.f);
     __syncthreads();   // the zero fill lands before the packed entries below
-    float mpm = 0.f;
+    double mpm = 0.0;
     for (int d = lane; d < D; d += 64) {
-      float pm = 0.f;
-      for (int e = 0; e < D; ++e) pm = fmaf(P[d * D + e], mus[e], pm);
-      mpm = fmaf(mus[d], pm, mpm);
-      put_f32(S + d, -2.f * pm);
-      for (int e = d; e < D; ++e)
-        put_f32(full_feature(d, e), d == e ? P[d * D + d] : P[d * D + e] + P[e * D + d]);
+      double pm = 0.0;
+      for (int e = 0; e < D; ++e) pm = fma(pd(d, e), (double)mus[e], pm);
+      mpm = fma((double)mus[d], pm, mpm);
+      put_f32(S + d, (float)(-2.0 * pm));
+      for (int e = d; e < D; ++e) put_f32(full_feature(d, e), (float)(d == e ? pd(d, d) : pd(d, e) + pd(e, d)));
     }
-    colq = wave_sum(mpm);
-    ca = -0.5f * kLog2e;
-    cb = (lw - 0.5f * (log2pi_d + a.logdet[bk])) * kLog2e;
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) mpm += __shfl_xor(mpm, off);
+    // (ca, ca·μᵀPμ + cb) with the constant rounded once from float64
+    constexpr double kLog2eD = 1.4426950408889634;
+    const double cbd = ((double)lw - 0.5 * ((double)log2pi_d + (double)a.logdet[bk])) * kLog2eD;
+    if (lane == 0) a.cconst[bk] = make_float4(-0.5f * kLog2e, (float)(-0.5 * kLog2eD * mpm + cbd), 0.f, 0.f);
+    return;
   }
   // l2 = ca * (rowq - 2S + colq) + cb (spherical, tied: S is the cross term x·μ / x·Pμ) or
   // ca * (S + colq) + cb (diag, full: W already carries the -2), stored as (ca, ca*colq + cb).
@@ -523,6 +533,94 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const f
     chol_blocked<DP>(a, sh[w]);
   }
   chol_inverse<DP>(D, sh[w], prec + (size_t)w * D * D, logdet + w);
+}
+
+// Full covariance (D <= 16): the precision matrix and log-determinant again in
+// float64.  The jitter ladder above decides exactly as the reference's fp32
+// factorisation does (torch_fallback.py:316-334); this pass then factorises the
+// same fp32 matrix sym(C) + jitter·I (formed entry by entry as chol_row forms
+// it) in float64, inverts it and writes P = L^-T L^-1 rounded to fp32, its
+// residual P - fp32(P) (the parameter packing forms the E-step operand and
+// constants from the pair in float64), and 2 Σ log L_ii rounded to fp32.  The E-step's quadratic forms expand x P x - 2 x P μ + μ P μ with
+// terms up to ~10^3 times the result at conditioned-but-narrow components, so
+// the fp32 inverse's error (κ·eps relative) dominated every logit; from the
+// float64 inverse the logits are ~7x closer to float64 than the reference's
+// fp32 ones (median |error| of the quadratic form 3e-5 vs 2e-4, measured on
+// the full-covariance benchmark recipe).  A matrix that factorises at no
+// level keeps the fp32 result, as the reference keeps its last attempt.
+// One wave per matrix, the matrix in LDS; lanes over entries.
+constexpr int kRefineWaves = 4;
+
+__global__ __launch_bounds__(64 * kRefineWaves) void chol_refine64_kernel(const float* cov, int D, int M,
+                                                                          const int* first_ok, const int* level,
+                                                                          float* prec, float* prec_lo,
+                                                                          float* logdet) {
+  __shared__ double A[kRefineWaves][16][17];
+  __shared__ double X[kRefineWaves][16][17];
+  const int w = threadIdx.x / 64, lane = threadIdx.x & 63;
+  const int m = blockIdx.x * kRefineWaves + w;
+  if (m >= M || D > 16) return;   // whole wave
+  const int lv = (M > kCholLevelInline) ? *level : wave_level(first_ok, M);
+  if (first_ok[m] > lv) {
+    // no factor at the batch level: the fp32 result stays, with no residual
+    for (int e = lane; e < D * D; e += 64) prec_lo[(size_t)m * D * D + e] = 0.f;
+    return;
+  }
+  const float jitter = jitter_of(lv);
+  const float* C = cov + (size_t)m * D * D;
+  double (*L)[17] = A[w];
+  double (*Xw)[17] = X[w];
+  for (int e = lane; e < D * D; e += 64) {
+    const int r = e / D, c = e % D;
+    const float v = (r == c) ? C[r * D + c] + jitter : 0.5f * (C[r * D + c] + C[c * D + r]);
+    L[r][c] = (double)v;
+  }
+  wave_lds_sync();
+  // right-looking Cholesky in place (lower triangle)
+  for (int k = 0; k < D; ++k) {
+    const double lkk = sqrt(L[k][k]);
+    wave_lds_sync();
+    if (lane == k) L[k][k] = lkk;
+    if (lane > k && lane < D) L[lane][k] = L[lane][k] / lkk;
+    wave_lds_sync();
+    for (int e = lane; e < D * D; e += 64) {
+      const int r = e / D, c = e % D;
+      if (c > k && r >= c) L[r][c] = fma(-L[r][k], L[c][k], L[r][c]);
+    }
+    wave_lds_sync();
+  }
+  // X = L^-1, lane c owns column c (forward substitution)
+  if (lane < D) {
+    const int c = lane;
+    for (int r = 0; r < D; ++r) {
+      double x = 0.0;
+      if (r == c) {
+        x = 1.0 / L[c][c];
+      } else if (r > c) {
+        double t = 0.0;
+        for (int k = c; k < r; ++k) t = fma(L[r][k], Xw[k][c], t);
+        x = -t / L[r][r];
+      }
+      Xw[r][c] = x;
+    }
+  }
+  wave_lds_sync();
+  // P = Xᵀ X; (i, j) and (j, i) use the same products in the same order: symmetric
+  float* P = prec + (size_t)m * D * D;
+  float* Plo = prec_lo + (size_t)m * D * D;
+  for (int e = lane; e < D * D; e += 64) {
+    const int i = e / D, j = e % D;
+    double t = 0.0;
+    for (int k = (i > j ? i : j); k < D; ++k) t = fma(Xw[k][i], Xw[k][j], t);
+    const float hi = (float)t;
+    P[e] = hi;
+    Plo[e] = (float)(t - (double)hi);
+  }
+  if (lane == 0) {
+    double ld = 0.0;
+    for (int k = 0; k < D; ++k) ld += log(L[k][k]);
+    logdet[m] = (float)(2.0 * ld);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1033,12 +1131,15 @@ static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* l
 }
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
-                 float* logdet, hipStream_t s) {
+                 float* prec_lo, float* logdet, hipStream_t s) {
   switch (chol_dp(D)) {
     case 16: launch_chol_dp<16>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
     case 32: launch_chol_dp<32>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
     default: launch_chol_dp<64>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
   }
+  if (prec_lo && D <= 16 && M > 0)
+    chol_refine64_kernel<<<(M + kRefineWaves - 1) / kRefineWaves, 64 * kRefineWaves, 0, s>>>(
+        cov, D, M, first_ok, level, prec, prec_lo, logdet);
 }
 
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s) {

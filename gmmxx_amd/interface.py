@@ -20,6 +20,14 @@ engine (bf16 means as the reference keeps them, products of exact bf16 values
 with fp32 accumulation, responsibilities rounded to bf16 before the M-step
 product): more accurate than the reference's bf16 arithmetic, held to the bf16
 bar (2e-3 on the log-likelihood), not to the fp32 one.
+
+Attribution: the estimator contract -- the constructor signature and sklearn
+aliases, the parameter validation and its messages, the ``set_params``
+branches and ``_n_parameters`` / ``bic`` / ``aic`` -- follows the reference's
+``gmmxx/interface.py`` (:77-121, :125-230, :1318-1360, :1605-1607,
+:2537-2558), GMMXX, MIT License, Copyright (c) 2026 GMMXX contributors; a
+drop-in must accept the same calls.  Everything that computes is this
+package's own.
 """
 
 from __future__ import annotations

@@ -16,16 +16,45 @@ the bar; the oracle itself then differs from float64 by as much.  A tensor
 outside the bar is therefore accepted when the HIP result is at least as
 accurate as the oracle's, judged against the float64 result from the same
 inputs (``f64_em``): its largest error relative to the bar, measured from
-the float64 value, is at most 4 times the oracle's largest (or within the
-bar).  The HIP result is then as accurate as the reference's own arithmetic
+the float64 value, is at most FACTOR (2) times the oracle's largest (or
+within two bars).  The HIP result is then as accurate as the reference's own arithmetic
 and the difference is the problem's conditioning, not an error.  (Per
 element the comparison would hinge on where the oracle happens to round
 luckily; over the tensor it compares the two implementations' accuracy.)
+
+Precisely: a tensor outside the bar passes when its largest error against
+float64, in bars, is at most FACTOR times the larger of the oracle's largest
+error and one bar -- within twice the oracle's own fp32 error, or within two
+bars of the float64 value (``arbiter_ok``).
+
+Where a problem is ill-conditioned enough that single elements of both fp32
+results land several bars from float64 (the full-covariance benchmark
+recipe: condition numbers up to ~1400), the largest error is a noisy
+statistic of a few elements; there the distribution rule applies
+(``arbiter_distribution_ok``): the bulk -- the 99th percentile of the
+error against float64 -- within FACTOR times the oracle's (or 0.05 bar),
+and the tail -- the largest error -- within TAIL_FACTOR times the oracle's
+largest (or one bar).  A systematic error (a wrong term) moves the bulk, a
+gross error of single elements (a wrong index) the tail.
 """
 
 import torch
 
-FACTOR = 4.0
+FACTOR = 2.0
+TAIL_FACTOR = 5.0
+
+
+def arbiter_ok(hip_vs_f64, oracle_vs_f64):
+    """The float64 arbiter's rule on the largest errors (see the module docstring)."""
+    return hip_vs_f64 <= FACTOR * max(oracle_vs_f64, 1.0)
+
+
+def arbiter_distribution_ok(hip_dist, oracle_dist):
+    """The distribution rule on two ``error_distribution`` results against
+    float64 (see the module docstring)."""
+    bulk = hip_dist["p99"] <= FACTOR * max(oracle_dist["p99"], 0.05)
+    tail = hip_dist["max"] <= TAIL_FACTOR * max(oracle_dist["max"], 1.0)
+    return bulk and tail
 
 
 def bf16_ulp(v):
@@ -73,9 +102,25 @@ def judge_params(got, exp, kind, x, bf16=False, truth_fn=None):
     band_t = rtol * t.abs() + floor + (bf16_ulp(t) if bf16 and kind == "means" else 0.0)
     res["hip_vs_float64"] = float(((got - t).abs() / band_t).max())
     res["oracle_vs_float64"] = float(((exp - t).abs() / band_t).max())
-    if res["hip_vs_float64"] > max(FACTOR * res["oracle_vs_float64"], 1.0):
+    if not arbiter_ok(res["hip_vs_float64"], res["oracle_vs_float64"]):
         res["unexplained"] = res["outside_bar"]
     return res
+
+
+def error_distribution(got, ref, kind, x, bf16=False):
+    """Median, 99th percentile and largest |got - ref| in units of the bar,
+    and the count outside it (for reports)."""
+    got = got.detach().cpu().double().flatten()
+    ref = ref.detach().cpu().double().flatten()
+    rtol, floor = param_band(kind, x, bf16)
+    if floor is None:
+        floor = rtol * float(ref.abs().max())
+        rtol = 0.0
+    r = (got - ref).abs() / (rtol * ref.abs() + floor)
+    sample = r if r.numel() <= (1 << 24) else r[:1 << 24]
+    q = torch.quantile(sample.float(), torch.tensor([0.5, 0.99])).tolist()
+    return {"median": q[0], "p99": q[1], "max": float(r.max()), "outside": int((r > 1).sum()),
+            "elements": int(r.numel())}
 
 
 def judge_ll(got, exp, tol, truth_fn=None):
@@ -86,8 +131,8 @@ def judge_ll(got, exp, tol, truth_fn=None):
            "worst_rel": max(abs(g - e) / abs(e) for g, e in zip(got, exp)), "unexplained": 0}
     if bad and truth_fn is not None:
         t = truth_fn()
-        res["unexplained"] = sum(1 for i in bad if abs(got[i] - t[i]) > max(FACTOR * abs(exp[i] - t[i]),
-                                                                             tol * abs(t[i])))
+        res["unexplained"] = sum(1 for i in bad if abs(got[i] - t[i]) > FACTOR * max(abs(exp[i] - t[i]),
+                                                                                     tol * abs(t[i])))
         res["float64"] = [t[i] for i in bad]
         res["hip"] = [got[i] for i in bad]
         res["oracle"] = [exp[i] for i in bad]

@@ -53,3 +53,38 @@ def test_judge_flags_a_planted_error():
     assert judge.judge_params(m64.float(), e_m, "means", x, False, lambda: m64)["unexplained"] == 0
     res = judge.judge_ll([e_lb * (1 + 1e-3)], [e_lb], 1e-5, lambda: [lb64])
     assert res["unexplained"] == 1
+
+
+def test_distribution_arbiter_flags_planted_errors():
+    """The distribution rule: a systematic error moves the 99th percentile, a
+    gross single-element error the largest error; both are flagged, while an
+    fp32 result as accurate as the oracle's passes."""
+    from oracle import judge
+    x, means, covs, w = _problem("diag", 1, 3000, 4, 3, seed=74)
+    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "diag", means, covs, w)
+    m64, c64, w64, lb64 = f64_em.em_step(x, "diag", means, covs, w)
+    o = judge.error_distribution(e_c, c64, "covs", x)
+    assert judge.arbiter_distribution_ok(judge.error_distribution(e_c.clone(), c64, "covs", x), o)
+    systematic = e_c * (1 + 3e-4)                       # every element 3 bars off
+    assert not judge.arbiter_distribution_ok(judge.error_distribution(systematic, c64, "covs", x), o)
+    gross = e_c.clone()
+    gross[0, 1, 2] += 0.5                               # one element far off
+    assert not judge.arbiter_distribution_ok(judge.error_distribution(gross, c64, "covs", x), o)
+
+
+@pytest.mark.parametrize("cov", ["spherical", "full"])
+def test_label_arbiter_flags_planted_errors(cov):
+    """The label check: the oracle's own labels pass; one row moved to its
+    float64 runner-up component (a misordering far beyond the near-tie bar) is
+    flagged, though the count rule alone would allow one such row."""
+    from tests.test_hip_parity import assert_labels
+    x, means, covs, w = _problem(cov, 1, 2000, 8, 6, seed=75)
+    exp = torch_ref.assign(x, means, covs, w, cov)
+    assert_labels(exp.clone(), x, means, covs, w, cov)
+    l64 = f64_em._logits(x.double(), cov, means.double(), covs.double(), w.double())[0]
+    top2 = l64.topk(2, dim=-1)
+    row = int((top2.values[:, 0] - top2.values[:, 1]).argmin())
+    planted = exp.clone()
+    planted[0, row] = int(top2.indices[row, 1])          # the runner-up, closest of all rows to a tie
+    with pytest.raises(AssertionError):
+        assert_labels(planted, x, means, covs, w, cov)

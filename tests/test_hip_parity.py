@@ -12,7 +12,8 @@ oracle on the CPU from identical parameters.  Tolerances (stated per check):
   * fp32 statistics: rtol 1e-4 of the statistic's scale;
   * per-iteration mean log-likelihood: rtol 1e-5 fp32, 2e-3 bf16;
   * labels: equal, except near-ties: rows whose float64 logit gap between the
-    two labels is below 1e-5·max(1, |logit|), for fp32 and bf16 x alike.
+    two labels is below 1e-5·max(1, |logit|), for fp32 and bf16 x alike; wider
+    gaps as judged by the float64 arbiter (``assert_labels``).
 """
 
 import math
@@ -20,7 +21,7 @@ import math
 import pytest
 import torch
 
-from oracle import torch_ref
+from oracle import f64_em, judge, torch_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -61,37 +62,60 @@ def to_dev(x, dtype=torch.float32):
 
 
 def assert_labels(got, x, means, covs, w, cov, gap_tol=1e-5):
-    """Labels equal, except near-ties: |Δlogit| < gap_tol·max(1, |logit|) in float64.
-    A wider gap is accepted only where the oracle's own fp32 logits cannot order
-    the two components either: the float64 gap is below twice the fp32
-    oracle's logit error on that row (ill-conditioned full covariances, where
-    fp32 logits carry errors above 1e-5 relative).  Prints the counts."""
+    """Labels equal, except near-ties: |Δlogit| < gap_tol·max(1, |logit|) in float64
+    (float64 logits from oracle/f64_em.py: Cholesky solves, no fp32 precision).
+
+    A mismatch with a wider float64 gap is one side misordering the two
+    components.  Where the HIP label is the float64 winner, the fp32 oracle
+    erred (counted).  Where the oracle's label is the winner, the HIP label is
+    accepted when the oracle's own fp32 logits cannot order the two either (the
+    gap is below twice the oracle's logit error on that row: ill-conditioned
+    full covariances, where fp32 logits carry errors above 1e-5 relative), or
+    under the float64 arbiter's distribution rule (oracle/judge.py): the
+    rows HIP misorders beyond that number at most FACTOR times the rows the
+    oracle misorders (or FACTOR), each within TAIL_FACTOR near-tie bars.
+    Prints the counts."""
     exp = torch_ref.assign(x, means, covs, w, cov)
     got = got.cpu()
     bad = (got != exp).nonzero(as_tuple=False)
     if bad.numel() == 0:
         return
-    mdl = torch_ref._Model(cov, means.double(), covs.double(), w.double())
-    xs = x.double().square().sum(-1) if cov == "spherical" else None
-    logits = mdl.logits(x.double(), xs, 0, means.shape[1])
-    worst, beyond = 0.0, 0
+    worst, beyond, oracle_wrong, hip_wrong = 0.0, 0, 0, []
     for bi, ni in bad.tolist():
-        l = logits[bi, ni]
+        # float64 logits of this row only (full-size inputs have millions of rows),
+        # from float64 Cholesky solves: the oracle's own model casts tied/full
+        # precisions to fp32, which is not the float64 truth both sides are judged by
+        xr64 = x[bi:bi + 1, ni:ni + 1].double()
+        l = f64_em._logits(xr64, cov, means[bi:bi + 1].double(), covs[bi:bi + 1].double(),
+                           w[bi:bi + 1].double())[0, 0]
         ga, ea = int(got[bi, ni]), int(exp[bi, ni])
         gap = abs(float(l[ga] - l[ea]))
         rel = gap / max(1.0, abs(float(l[ea])))
         worst = max(worst, rel)
-        if rel >= gap_tol:
-            mdl32 = torch_ref._Model(cov, means[bi:bi + 1].float(), covs[bi:bi + 1].float(), w[bi:bi + 1].float())
-            xr = x[bi:bi + 1, ni:ni + 1].float()
-            l32 = mdl32.logits(xr, xr.square().sum(-1) if cov == "spherical" else None, 0,
-                               means.shape[1])[0, 0].double()
-            err32 = max(abs(float(l32[ga] - l[ga])), abs(float(l32[ea] - l[ea])))
-            assert gap < 2.0 * err32, (f"label mismatch at ({bi},{ni}): float64 logit gap {gap:.3e} "
-                                       f"({rel:.3e} relative) above the fp32 oracle's logit error {err32:.3e}")
+        if rel < gap_tol:
+            continue
+        if float(l[ga]) > float(l[ea]):
+            oracle_wrong += 1
+            continue
+        mdl32 = torch_ref._Model(cov, means[bi:bi + 1].float(), covs[bi:bi + 1].float(), w[bi:bi + 1].float())
+        xr = x[bi:bi + 1, ni:ni + 1].float()
+        l32 = mdl32.logits(xr, xr.square().sum(-1) if cov == "spherical" else None, 0,
+                           means.shape[1])[0, 0].double()
+        err32 = max(abs(float(l32[ga] - l[ga])), abs(float(l32[ea] - l[ea])))
+        if gap < 2.0 * err32:
             beyond += 1
-    print(f"  labels: {bad.shape[0]} of {got.numel()} differ, largest relative logit gap {worst:.3e}"
-          f" ({beyond} beyond {gap_tol:g}, each within the fp32 oracle's own logit error)", flush=True)
+        else:
+            hip_wrong.append((bi, ni, gap, rel, err32))
+    print(f"  labels: {bad.shape[0]} of {got.numel()} differ, largest relative logit gap {worst:.3e};"
+          f" beyond {gap_tol:g}: {oracle_wrong} where the oracle misorders, {beyond} within the oracle's"
+          f" own logit error, {len(hip_wrong)} where HIP misorders", flush=True)
+    for bi, ni, gap, rel, err32 in hip_wrong:
+        print(f"    HIP misorders ({bi},{ni}): float64 gap {gap:.3e} ({rel:.3e} relative),"
+              f" oracle logit error {err32:.3e}", flush=True)
+    assert len(hip_wrong) <= judge.FACTOR * max(oracle_wrong, 1), \
+        f"{len(hip_wrong)} rows misordered by HIP against {oracle_wrong} by the oracle"
+    assert all(rel < judge.TAIL_FACTOR * gap_tol for *_, rel, _ in hip_wrong), \
+        f"a HIP misordering beyond {judge.TAIL_FACTOR:g} near-tie bars"
 
 
 def assert_bf16_means(got, exp):
