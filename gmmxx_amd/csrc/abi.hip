@@ -63,7 +63,7 @@ struct Plan {
   int chol_m = 0;
   size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_wmu = 0, o_wsc = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
   size_t o_xch = 0, o_flags = 0;
-  size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_lbuf = 0, o_prec = 0, o_prec_lo = 0, o_logdet = 0,
+  size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_lbuf = 0, o_prec = 0, o_logdet = 0,
          o_gram = 0, total = 0;
 };
 
@@ -232,7 +232,6 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_first = take((size_t)q.chol_m * 4 + 4);   // per-matrix first levels, then the global level
   q.o_lbuf = take(q.chol_m ? (size_t)q.chol_m * chol_dp(q.D) * chol_dp(q.D) * 4 : 0);
   q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
-  q.o_prec_lo = take(q.cov == FULL && q.D <= 16 ? (size_t)q.chol_m * q.D * q.D * 4 : 0);
   q.o_logdet = take((size_t)q.chol_m * 4);
   q.o_gram = take(q.cov == TIED ? (size_t)q.gram_slices * q.B * q.D * q.D * 4 : 0);
   q.total = off;
@@ -391,14 +390,12 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
             double reg, double minw, int prelude, void* ws, hipStream_t s, bool rowquad = true,
             const float* gram = nullptr, double* shift = nullptr) {
   float* prec = nullptr;
-  float* prec_lo = nullptr;
   float* logdet = nullptr;
   if (pl.cov == TIED || pl.cov == FULL) {
     prec = at<float>(ws, pl.o_prec);
-    prec_lo = (pl.cov == FULL && pl.D <= 16) ? at<float>(ws, pl.o_prec_lo) : nullptr;
     logdet = at<float>(ws, pl.o_logdet);
     launch_chol(covs, pl.D, pl.chol_m, at<int>(ws, pl.o_first), at<int>(ws, pl.o_first) + pl.chol_m,
-                at<float>(ws, pl.o_lbuf), prec, prec_lo, logdet, s);
+                at<float>(ws, pl.o_lbuf), prec, logdet, s);
   }
   PrepArgs a{};
   a.cov = pl.cov;
@@ -415,7 +412,8 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   a.covs = covs;
   a.weights = weights;
   a.prec = prec;
-  a.prec_lo = prec_lo;
+  a.first_ok = (pl.cov == FULL) ? at<int>(ws, pl.o_first) : nullptr;
+  a.chol_level = (pl.cov == FULL) ? at<int>(ws, pl.o_first) + pl.chol_m : nullptr;
   a.logdet = logdet;
   a.covs_used = (pl.cov == SPH || pl.cov == DIAG) ? at<float>(ws, pl.o_covs_used) : nullptr;
   a.w_hi = at<void>(ws, pl.o_whi);

@@ -50,9 +50,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+__device__ float jitter_of(int level);
+
 __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
   __shared__ float scratch[32];
   __shared__ float mus[kMaxPrepD];
+  __shared__ double fa[16][17], fp[16][17], ff[16][17];   // full covariance (D <= 16) refinement
   const int b = blockIdx.y, k = blockIdx.x, lane = threadIdx.x;
   const int K = a.K, D = a.D, DP = a.DP, EP = a.EP;
   const float* wrow = a.weights + (size_t)b * K;
@@ -166,14 +169,52 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
     }
   } else {
     // FULL: W_k = [packed P_k with doubled off-diagonal | -2 P_k μ_k]  (torch_fallback.py:418-432).
-    // The entries, P_k μ_k and μ_kᵀP_kμ_k are formed in float64 from the precision
-    // and its residual (P + P_lo, the float64 inverse) and rounded once: the
-    // logit's terms reach ~10^2 times the logit, so each fp32 rounding on the
-    // way (the off-diagonal sum, the Pμ and μᵀPμ chains, the constant) would
-    // add an error of that order.
+    // The logit's terms reach ~10^2 times the logit, so every fp32 rounding on the
+    // way to W (the inverse itself, the off-diagonal sum, the Pμ and μᵀPμ chains,
+    // the constant) adds an error of that order.  The fp32 precision of the
+    // Cholesky kernels (the reference's jitter ladder, torch_fallback.py:316-334)
+    // is refined here by two Newton steps P <- P + P(I - A·P) in float64 against
+    // A = sym(Σ) + jitter·I (formed entry by entry as the factorisation formed it),
+    // which square the residual each (fp32 inverse: ~κ·1e-7), and W and the
+    // constant are formed in float64 and rounded once.  A matrix the ladder left
+    // unfactorised, or whose fp32 inverse is too far off (residual > 1/2),
+    // keeps its fp32 precision.
     const float* P = a.prec + bk * D * D;
-    const float* Pl = a.prec_lo ? a.prec_lo + bk * D * D : nullptr;
-    auto pd = [&](int d, int e) { return (double)P[d * D + e] + (Pl ? (double)Pl[d * D + e] : 0.0); };
+    const float* Cv = a.covs + bk * D * D;
+    const int lv = *a.chol_level;
+    const float jit = jitter_of(lv);
+    for (int e = lane; e < D * D; e += 64) {
+      const int r = e / D, c = e % D;
+      fa[r][c] = (double)((r == c) ? Cv[r * D + c] + jit : 0.5f * (Cv[r * D + c] + Cv[c * D + r]));
+      fp[r][c] = (double)P[e];
+    }
+    const bool refine = a.first_ok[bk] <= lv;   // D <= 16: the plan's limit for full covariance
+    for (int it = 0; it < 2 && refine; ++it) {
+      __syncthreads();
+      double worst = 0.0;
+      for (int e = lane; e < D * D; e += 64) {
+        const int r = e / D, c = e % D;
+        double t = (r == c) ? 1.0 : 0.0;
+        for (int k = 0; k < D; ++k) t = fma(-fa[r][k], fp[k][c], t);
+        ff[r][c] = t;
+        worst = fmax(worst, fabs(t));
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off /= 2) worst = fmax(worst, __shfl_xor(worst, off));
+      if (!(worst <= 0.5)) break;            // whole block (one wave): keep the current P
+      __syncthreads();
+      double nv[4];
+      for (int e = lane, u = 0; e < D * D; e += 64, ++u) {
+        const int r = e / D, c = e % D;
+        double t = fp[r][c];
+        for (int k = 0; k < D; ++k) t = fma(fp[r][k], ff[k][c], t);
+        nv[u] = t;
+      }
+      __syncthreads();
+      for (int e = lane, u = 0; e < D * D; e += 64, ++u) fp[e / D][e % D] = nv[u];
+    }
+    __syncthreads();
+    auto pd = [&](int d, int e) { return 0.5 * (fp[d][e] + fp[e][d]); };
     const int S = DP * (DP + 1) / 2;
     for (int e = lane; e < EP; e += 64) put_f32(e, 0.f);
     __syncthreads();   // the zero fill lands before the packed entries below
@@ -474,18 +515,20 @@ __device__ int wave_level(const int* first_ok, int M) {
   return min(v, 6);
 }
 
-// level == nullptr: the batch level is computed from first_ok here (M <= kCholLevelInline).
+// inline_level: the batch level is computed from first_ok here (M <= kCholLevelInline)
+// and written to *level; otherwise read from *level.
 template <int DP>
 __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_finish_kernel(const float* cov, int D, int M,
-                                                                            const int* first_ok, const int* level,
-                                                                            const float* lbuf, float* prec,
-                                                                            float* logdet) {
+                                                                            const int* first_ok, int* level,
+                                                                            bool inline_level, const float* lbuf,
+                                                                            float* prec, float* logdet) {
   constexpr int RS = chol_rs<DP>();
   __shared__ __align__(16) CholLds<DP> sh[chol_waves<DP>()];
   const int w = threadIdx.x / 64, i = threadIdx.x & 63;
   const int m = blockIdx.x * chol_waves<DP>() + w;
   if (m >= M) return;   // whole wave
-  const int lv = level ? *level : wave_level(first_ok, M);
+  const int lv = inline_level ? wave_level(first_ok, M) : *level;
+  if (inline_level && m == 0 && i == 0) *level = lv;   // for readers after the launch
   if (first_ok[m] == lv) {
     if (i < DP) {
       const float* Lg = lbuf + ((size_t)m * DP + i) * DP;
@@ -533,94 +576,6 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const f
     chol_blocked<DP>(a, sh[w]);
   }
   chol_inverse<DP>(D, sh[w], prec + (size_t)w * D * D, logdet + w);
-}
-
-// Full covariance (D <= 16): the precision matrix and log-determinant again in
-// float64.  The jitter ladder above decides exactly as the reference's fp32
-// factorisation does (torch_fallback.py:316-334); this pass then factorises the
-// same fp32 matrix sym(C) + jitter·I (formed entry by entry as chol_row forms
-// it) in float64, inverts it and writes P = L^-T L^-1 rounded to fp32, its
-// residual P - fp32(P) (the parameter packing forms the E-step operand and
-// constants from the pair in float64), and 2 Σ log L_ii rounded to fp32.  The E-step's quadratic forms expand x P x - 2 x P μ + μ P μ with
-// terms up to ~10^3 times the result at conditioned-but-narrow components, so
-// the fp32 inverse's error (κ·eps relative) dominated every logit; from the
-// float64 inverse the logits are ~7x closer to float64 than the reference's
-// fp32 ones (median |error| of the quadratic form 3e-5 vs 2e-4, measured on
-// the full-covariance benchmark recipe).  A matrix that factorises at no
-// level keeps the fp32 result, as the reference keeps its last attempt.
-// One wave per matrix, the matrix in LDS; lanes over entries.
-constexpr int kRefineWaves = 4;
-
-__global__ __launch_bounds__(64 * kRefineWaves) void chol_refine64_kernel(const float* cov, int D, int M,
-                                                                          const int* first_ok, const int* level,
-                                                                          float* prec, float* prec_lo,
-                                                                          float* logdet) {
-  __shared__ double A[kRefineWaves][16][17];
-  __shared__ double X[kRefineWaves][16][17];
-  const int w = threadIdx.x / 64, lane = threadIdx.x & 63;
-  const int m = blockIdx.x * kRefineWaves + w;
-  if (m >= M || D > 16) return;   // whole wave
-  const int lv = (M > kCholLevelInline) ? *level : wave_level(first_ok, M);
-  if (first_ok[m] > lv) {
-    // no factor at the batch level: the fp32 result stays, with no residual
-    for (int e = lane; e < D * D; e += 64) prec_lo[(size_t)m * D * D + e] = 0.f;
-    return;
-  }
-  const float jitter = jitter_of(lv);
-  const float* C = cov + (size_t)m * D * D;
-  double (*L)[17] = A[w];
-  double (*Xw)[17] = X[w];
-  for (int e = lane; e < D * D; e += 64) {
-    const int r = e / D, c = e % D;
-    const float v = (r == c) ? C[r * D + c] + jitter : 0.5f * (C[r * D + c] + C[c * D + r]);
-    L[r][c] = (double)v;
-  }
-  wave_lds_sync();
-  // right-looking Cholesky in place (lower triangle)
-  for (int k = 0; k < D; ++k) {
-    const double lkk = sqrt(L[k][k]);
-    wave_lds_sync();
-    if (lane == k) L[k][k] = lkk;
-    if (lane > k && lane < D) L[lane][k] = L[lane][k] / lkk;
-    wave_lds_sync();
-    for (int e = lane; e < D * D; e += 64) {
-      const int r = e / D, c = e % D;
-      if (c > k && r >= c) L[r][c] = fma(-L[r][k], L[c][k], L[r][c]);
-    }
-    wave_lds_sync();
-  }
-  // X = L^-1, lane c owns column c (forward substitution)
-  if (lane < D) {
-    const int c = lane;
-    for (int r = 0; r < D; ++r) {
-      double x = 0.0;
-      if (r == c) {
-        x = 1.0 / L[c][c];
-      } else if (r > c) {
-        double t = 0.0;
-        for (int k = c; k < r; ++k) t = fma(L[r][k], Xw[k][c], t);
-        x = -t / L[r][r];
-      }
-      Xw[r][c] = x;
-    }
-  }
-  wave_lds_sync();
-  // P = Xᵀ X; (i, j) and (j, i) use the same products in the same order: symmetric
-  float* P = prec + (size_t)m * D * D;
-  float* Plo = prec_lo + (size_t)m * D * D;
-  for (int e = lane; e < D * D; e += 64) {
-    const int i = e / D, j = e % D;
-    double t = 0.0;
-    for (int k = (i > j ? i : j); k < D; ++k) t = fma(Xw[k][i], Xw[k][j], t);
-    const float hi = (float)t;
-    P[e] = hi;
-    Plo[e] = (float)(t - (double)hi);
-  }
-  if (lane == 0) {
-    double ld = 0.0;
-    for (int k = 0; k < D; ++k) ld += log(L[k][k]);
-    logdet[m] = (float)(2.0 * ld);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1126,20 +1081,17 @@ static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* l
   chol_try_kernel<DP><<<blocks, 64 * NW, 0, s>>>(cov, D, M, first_ok, lbuf);
   const bool inline_level = M <= kCholLevelInline;
   if (!inline_level) chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
-  chol_finish_kernel<DP><<<blocks, 64 * NW, 0, s>>>(cov, D, M, first_ok, inline_level ? nullptr : level,
-                                                    lbuf, prec, logdet);
+  chol_finish_kernel<DP><<<blocks, 64 * NW, 0, s>>>(cov, D, M, first_ok, level, inline_level, lbuf, prec,
+                                                    logdet);
 }
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
-                 float* prec_lo, float* logdet, hipStream_t s) {
+                 float* logdet, hipStream_t s) {
   switch (chol_dp(D)) {
     case 16: launch_chol_dp<16>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
     case 32: launch_chol_dp<32>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
     default: launch_chol_dp<64>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
   }
-  if (prec_lo && D <= 16 && M > 0)
-    chol_refine64_kernel<<<(M + kRefineWaves - 1) / kRefineWaves, 64 * kRefineWaves, 0, s>>>(
-        cov, D, M, first_ok, level, prec, prec_lo, logdet);
 }
 
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s) {

@@ -14,7 +14,8 @@ struct PrepArgs {
   const float* covs;       // spherical [B][K], diag [B][K][D]
   const float* weights;    // [B][K]
   const float* prec;       // tied [B][D][D], full [B][K][D][D]
-  const float* prec_lo;    // full: residual of the float64 precision, P64 - prec (or null)
+  const int* first_ok;     // full: per-matrix first jitter level of the Cholesky ladder
+  const int* chol_level;   // full: the batch's jitter level (written by launch_chol's kernels)
   const float* logdet;     // tied [B], full [B][K]
   float* covs_used;        // spherical/diag: the (clamped) variances this iteration used
   void* w_hi;              // [B][K][EP]
@@ -82,11 +83,9 @@ struct PackArgs {
 void launch_prep(const PrepArgs& a, hipStream_t s);
 // Padded order of the per-matrix factor buffer (lbuf: M x chol_dp(D)^2 floats).
 int chol_dp(int D);
-// prec_lo non-null (full covariance, D <= 16): precision and log-determinant
-// formed again in float64 from the matrix the fp32 jitter ladder factorised;
-// prec holds the precision rounded to fp32 and prec_lo (M x D x D) its residual.
+// first_ok: M per-matrix first levels, then the batch level (written by every path).
 void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
-                 float* prec_lo, float* logdet, hipStream_t s);
+                 float* logdet, hipStream_t s);
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s);
 int launch_combine(const CombineArgs& a, hipStream_t s);  // returns the per-batch block count
 int combine_blocks(int64_t N);
