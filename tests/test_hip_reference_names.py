@@ -6,6 +6,8 @@ equal on well-separated blobs, log-likelihoods rtol 1e-5 with a floor of 1e-5 of
 the mean magnitude, responsibilities within 2e-5 absolute, fit lower bounds
 rtol 1e-5)."""
 
+import math
+
 import pytest
 import torch
 
@@ -51,11 +53,38 @@ def test_chunked_inference_functions(cov):
     assert torch.equal(lab.cpu(), e_lab)
     torch.testing.assert_close(sc.cpu(), e_sc, rtol=1e-5, atol=1e-5 * float(e_sc.abs().mean()))
     torch.testing.assert_close(pr.cpu(), e_pr, rtol=0, atol=2e-5)
-    # hip_ops: the same kernels under the cuda_ops names
-    ops = {"diag": "diag"}.get(cov, cov)
-    assert torch.equal(getattr(hip_ops, f"{ops}_assign")(xd, md, cd, wd).cpu(), e_lab)
-    torch.testing.assert_close(getattr(hip_ops, f"{ops}_logsumexp")(xd, md, cd, wd).cpu(), sc.cpu(), rtol=0, atol=0)
-    torch.testing.assert_close(getattr(hip_ops, f"{ops}_resp")(xd, md, cd, wd).cpu(), pr.cpu(), rtol=0, atol=0)
+    # hip_ops: the cuda_ops names with the reference ops' arguments (log-weights;
+    # the Cholesky factor for tied and full), int32 labels
+    lw = wd.log()
+    par = torch.linalg.cholesky(cd) if cov in ("tied", "full") else cd
+    lab_o = getattr(hip_ops, f"{cov}_assign")(xd, md, par, lw)
+    assert lab_o.dtype == torch.int32 and torch.equal(lab_o.cpu().long(), e_lab)
+    lse_o = getattr(hip_ops, f"{cov}_logsumexp")(xd, md, par, lw)
+    torch.testing.assert_close(lse_o.cpu(), e_sc, rtol=1e-5, atol=1e-5 * float(e_sc.abs().mean()))
+    r_o = getattr(hip_ops, f"{cov}_resp")(xd, md, par, lw, lse_o)
+    torch.testing.assert_close(r_o.cpu(), e_pr, rtol=0, atol=2e-5)
+    # a log_norm shifted by c scales every responsibility by e^-c
+    r_s = getattr(hip_ops, f"{cov}_resp")(xd, md, par, lw, lse_o + 0.5)
+    torch.testing.assert_close(r_s.cpu(), e_pr * math.exp(-0.5), rtol=1e-5, atol=2e-5)
+
+
+def test_hip_ops_fused_spherical_is_one_em_iteration():
+    """fused_spherical / soft_update_spherical (_cuda.py:1056-1088, :415-682):
+    the oracle's iteration from the same parameters, and the E-step's
+    per-sample log-likelihood and labels under the input parameters."""
+    x, m, c, w = _problem("spherical")
+    print("[reference-names fused_spherical]", flush=True)
+    xd, md, cd, wd = (t.to(DEV) for t in (x, m, c, w))
+    mh, vh, wh, lse, lab = hip_ops.fused_spherical(xd, md, cd, wd.log(), 1e-6)
+    e_m, e_c, e_w, _ = torch_ref.fit_one_iteration_stats(x, "spherical", m, c, w)
+    torch.testing.assert_close(mh.cpu(), e_m, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(vh.cpu(), e_c, rtol=1e-4, atol=1e-6)
+    torch.testing.assert_close(wh.cpu(), e_w, rtol=1e-4, atol=1e-7)
+    e_sc = torch_ref.score_samples(x, m, c, w, "spherical")
+    torch.testing.assert_close(lse.cpu(), e_sc, rtol=1e-5, atol=1e-5 * float(e_sc.abs().mean()))
+    assert lab.dtype == torch.int32 and torch.equal(lab.cpu().long(), torch_ref.assign(x, m, c, w, "spherical"))
+    out = hip_ops.soft_update_spherical(xd, md, cd, wd.log(), 1e-6, compute_ids=False)
+    assert out[4] is None and torch.equal(out[0], mh) and torch.equal(out[3], lse)
 
 
 @pytest.mark.parametrize("cov", ["spherical", "diag", "tied", "full"])

@@ -363,9 +363,15 @@ REFERENCE_NAMES = [
 ]
 REFERENCE_OPS = [
     "canary_add_offset", "spherical_assign", "spherical_logsumexp", "spherical_resp", "soft_update_spherical",
-    "finalize_spherical", "fused_spherical", "approx_topk_update_spherical", "diag_assign", "diag_logsumexp",
-    "diag_resp", "finalize_diag", "tied_assign", "tied_logsumexp", "tied_resp", "full_assign",
-    "full_logsumexp", "full_resp",
+    "fused_spherical", "diag_assign", "diag_logsumexp", "diag_resp", "tied_assign", "tied_logsumexp",
+    "tied_resp", "full_assign", "full_logsumexp", "full_resp",
+]
+# cuda_ops names of the reference's hard-EM and torch-only ops, which hip_ops
+# does not provide: each must fail with an AttributeError naming the replacement.
+REFERENCE_OPS_NOT_PROVIDED = [
+    "blocked_update_spherical", "blocked_update_spherical_sorted", "finalize_spherical", "blocked_update_diag",
+    "blocked_update_diag_sorted", "finalize_diag", "tied_project", "tied_log_det", "tied_finalize",
+    "full_blocked_update", "full_finalize", "approx_topk_update_spherical",
 ]
 
 
@@ -380,11 +386,22 @@ def test_reference_function_names_exported():
 
 
 def test_hip_ops_mirrors_cuda_ops_names():
+    import inspect
     from gmmxx_amd import hip_ops
     missing = [n for n in REFERENCE_OPS if not callable(getattr(hip_ops, n, None))]
     assert not missing
     assert set(REFERENCE_OPS) <= set(hip_ops.__all__)
     assert hip_ops.HipRuntimeFallback.__mro__[1].__name__ == "HipRuntimeError"
+    # the reference ops' leading parameters (_cuda.py:328-412, :897-959, :1126-1201, :1274-1314, :1056)
+    params = lambda f: list(inspect.signature(f).parameters)
+    assert params(hip_ops.spherical_resp)[:6] == ["x", "means", "var", "log_w", "log_norm", "out"]
+    assert params(hip_ops.diag_assign) == ["x", "means", "var", "log_w", "out"]
+    assert params(hip_ops.tied_resp) == ["x", "means", "L", "log_w", "log_norm"]
+    assert params(hip_ops.full_logsumexp) == ["x", "means", "L", "log_w"]
+    assert params(hip_ops.fused_spherical) == ["x", "means", "var", "log_w", "reg_covar"]
+    for name in REFERENCE_OPS_NOT_PROVIDED:
+        with pytest.raises(AttributeError, match="not provided"):
+            getattr(hip_ops, name)
 
 
 def test_reference_named_wrappers_reject_unknown_keywords():
