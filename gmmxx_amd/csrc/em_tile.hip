@@ -435,7 +435,10 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
         } else if constexpr (COV == FULL) {
           // φ = [xxᵀ products in full_feature order | x]: the row's four chunks sit
           // in a quad of lanes; this lane (chunk c = cc / 4) writes its diagonal
-          // block, its chunk times chunks c+1 and (c < 2) c+2, and its x values.
+          // block, its chunk times chunk c+1, half of the pair {c, c+2} (rows
+          // 2h, 2h+1 of the owner's 4x4 block, h = c / 2, owner c % 2) and its x
+          // values: 38 features per lane, so no lane of the wave idles while
+          // others form the pair blocks.
           static_assert(DP == 16 && VEC == 4 && CPR == 4, "full covariance runs at DP = 16");
           const int c = cc / VEC, q0 = lane & ~3;
           float w1[VEC], w2[VEC];
@@ -456,12 +459,20 @@ __global__ __launch_bounds__(512) void em_tile_kernel(TileArgs a) {
 #pragma unroll
             for (int j = 0; j < VEC; ++j) o[4 * i + j] = v[i] * w1[j];
           put3n(40 + 16 * c, o);
-          if (c < 2) {
+          {
+            // owner chunk a = c % 2 (rows i of the block), partner a + 2 (columns j);
+            // lanes c < 2 hold a in v, lanes c >= 2 hold it in w2
+            const int h = c >> 1;
+            float p8[8];
 #pragma unroll
-            for (int i = 0; i < VEC; ++i)
+            for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-              for (int j = 0; j < VEC; ++j) o[4 * i + j] = v[i] * w2[j];
-            put3n(104 + 16 * c, o);
+              for (int j = 0; j < VEC; ++j) {
+                const float own = h ? w2[2 + ii] : v[ii];   // row 2h + ii of chunk a
+                const float par = h ? v[j] : w2[j];
+                p8[4 * ii + j] = own * par;
+              }
+            put3n(104 + 16 * (c & 1) + 8 * h, p8);
           }
           put3(S + cc, v);
         } else {
