@@ -599,7 +599,7 @@ int coop_capacity() {
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s) {
   if (dp != 128 || a.G < 2 || a.G > kMaxCoopGroup) return -1;
   const int grid = a.NG * a.G;
-  // The exchange slots (64-bit words) and the status word start at zero.
+  // The exchange slots (64-bit words) start with the odd round tag, the status word at zero.
   const int nwords = a.NG * kRing * a.G * kBN * 2;
   coop_zero_kernel<<<(nwords + 1 + 255) / 256, 256, 0, s>>>(reinterpret_cast<unsigned*>(a.xch), nwords, a.status);
   const void* fn = a.G <= 2 ? reinterpret_cast<const void*>(sph_bf16_coop_kernel<128, 2>)
