@@ -96,7 +96,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.D = (int)p->D;
   q.K = (int)p->K;
   if (q.bf && q.cov != SPH) return fail(GMMXX_ERR_UNSUPPORTED, "bf16 input is supported for spherical only");
-  const int dmax = (q.cov == FULL) ? 16 : (q.cov == TIED ? 64 : 128);
+  const int dmax = (q.cov == FULL) ? 16 : 128;
   if (p->D > dmax) return fail(GMMXX_ERR_UNSUPPORTED, "D exceeds the supported maximum for this covariance type");
   q.DP = dp_for(q.D);
   const bool sph_bf = q.bf && q.cov == SPH;          // dedicated kernel, DP >= 32

@@ -579,6 +579,122 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const f
 }
 
 // ---------------------------------------------------------------------------
+// 64 < D <= 128 (tied): one workgroup of kChol128Threads per matrix, the matrix
+// in LDS.  Unblocked right-looking factorisation (column scale, then the
+// trailing update, two barriers per column), the same ladder as above:
+// chol128_try finds each matrix's first factorising level, chol128_finish
+// factorises at the batch level and writes X = L^-1 (one thread per column,
+// forward substitution), P = XᵀX and 2 Σ log L_jj.  A wave per matrix cannot
+// hold a 128-row panel, and these sizes are rare (tied covariance has one
+// matrix per problem), so simplicity wins over the blocked MFMA path.
+// ---------------------------------------------------------------------------
+
+constexpr int kChol128Threads = 256;
+constexpr int kChol128RS = 129;   // row stride (floats)
+
+// A = sym(C) + jitter·I (lower triangle) into LDS, then factorised in place;
+// returns false when a pivot is not positive (or not finite).
+__device__ bool chol128_factor(const float* C, int D, float jitter, float* A) {
+  const int t = threadIdx.x;
+  for (int e = t; e < D * D; e += kChol128Threads) {
+    const int r = e / D, c = e % D;
+    if (c <= r) A[r * kChol128RS + c] = (r == c) ? C[r * D + c] + jitter : 0.5f * (C[r * D + c] + C[c * D + r]);
+  }
+  __syncthreads();
+  for (int k = 0; k < D; ++k) {
+    const float p = A[k * kChol128RS + k];
+    const bool ok = p > 0.f && p < INFINITY;   // every thread reads the same pivot
+    if (!ok) return false;                     // uniform over the workgroup
+    const float lkk = sqrtf(p);
+    const float inv = 1.f / lkk;
+    __syncthreads();                           // every thread has read the pivot
+    if (t == 0) A[k * kChol128RS + k] = lkk;
+    for (int i = k + 1 + t; i < D; i += kChol128Threads) A[i * kChol128RS + k] *= inv;
+    __syncthreads();
+    // trailing update A[i][j] -= L[i][k] L[j][k], k < j <= i: row k + 1 + t/2, columns of parity t & 1
+    for (int i = k + 1 + (t >> 1); i < D; i += kChol128Threads / 2) {
+      const float lik = A[i * kChol128RS + k];
+      for (int j = k + 1 + (t & 1); j <= i; j += 2) A[i * kChol128RS + j] = fmaf(-lik, A[j * kChol128RS + k], A[i * kChol128RS + j]);
+    }
+    __syncthreads();
+  }
+  return true;
+}
+
+__global__ __launch_bounds__(kChol128Threads) void chol128_try_kernel(const float* cov, int D, int M, int* first_ok) {
+  __shared__ float A[128 * kChol128RS];
+  const int m = blockIdx.x;
+  if (m >= M) return;
+  const float* C = cov + (size_t)m * D * D;
+  int first = 7;
+  for (int lv = 0; lv <= 6; ++lv) {
+    if (chol128_factor(C, D, jitter_of(lv), A)) {
+      first = lv;
+      break;
+    }
+    __syncthreads();   // the failed attempt's readers are done before the next fill
+  }
+  if (threadIdx.x == 0) first_ok[m] = first;
+}
+
+// inline_level: the batch level is the maximum of first_ok over the batch
+// (M <= kCholLevelInline), written to *level by block 0; else read from *level.
+__global__ __launch_bounds__(kChol128Threads) void chol128_finish_kernel(const float* cov, int D, int M,
+                                                                         const int* first_ok, int* level,
+                                                                         bool inline_level, float* prec,
+                                                                         float* logdet) {
+  __shared__ float A[128 * kChol128RS];
+  __shared__ float X[128 * kChol128RS];
+  __shared__ int lvs;
+  const int m = blockIdx.x, t = threadIdx.x;
+  if (m >= M) return;
+  if (t == 0) {
+    int v = 0;
+    if (inline_level) {
+      for (int i = 0; i < M; ++i) v = max(v, first_ok[i]);
+      v = min(v, 6);
+      if (m == 0) *level = v;
+    } else {
+      v = *level;
+    }
+    lvs = v;
+  }
+  __syncthreads();
+  const int lv = lvs;
+  // a matrix that factorises at no level keeps the partial factor, as the reference does
+  (void)chol128_factor(cov + (size_t)m * D * D, D, jitter_of(lv), A);
+  __syncthreads();
+  // X = L^-1, thread c owns column c
+  if (t < D) {
+    const int c = t;
+    for (int r = 0; r < c; ++r) X[r * kChol128RS + c] = 0.f;
+    for (int r = c; r < D; ++r) {
+      float acc = 0.f;
+      for (int k = c; k < r; ++k) acc = fmaf(A[r * kChol128RS + k], X[k * kChol128RS + c], acc);
+      X[r * kChol128RS + c] = ((r == c) ? 1.f : -acc) / A[r * kChol128RS + r];
+    }
+  }
+  __syncthreads();
+  // P = XᵀX, entries (i >= j) mirrored: the same products in the same order on both sides
+  float* P = prec + (size_t)m * D * D;
+  for (int e = t; e < D * D; e += kChol128Threads) {
+    const int i = e / D, j = e % D;
+    if (i < j) continue;
+    float acc = 0.f;
+    for (int k = i; k < D; ++k) acc = fmaf(X[k * kChol128RS + i], X[k * kChol128RS + j], acc);
+    P[(size_t)i * D + j] = acc;
+    P[(size_t)j * D + i] = acc;
+  }
+  if (t < 64) {
+    float ld = 0.f;
+    for (int k = t; k < D; k += 64) ld += logf(A[k * kChol128RS + k]);
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) ld += __shfl_xor(ld, off);
+    if (t == 0) logdet[m] = 2.f * ld;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Tied: per-row quadratic form xᵀ P x (torch_fallback.py:451)
 // ---------------------------------------------------------------------------
 
@@ -892,7 +1008,8 @@ constexpr int kTiedWaves = 4;   // waves per covariance row, splitting the compo
 
 __global__ __launch_bounds__(64 * kTiedWaves) void finalize_tied_kernel(FinalizeArgs a) {
   __shared__ float red[kTiedWaves][64];
-  const int b = blockIdx.y, d = blockIdx.x, w = threadIdx.x / 64, e = threadIdx.x & 63;
+  // column e of row d; blockIdx.z picks the half of the columns (D > 64)
+  const int b = blockIdx.y, d = blockIdx.x, w = threadIdx.x / 64, e = (threadIdx.x & 63) + 64 * blockIdx.z;
   if (a.skip && *a.skip != 0u) return;   // uniform over the grid
   const int K = a.K, D = a.D, JP = a.JP;
   const int ec = min(e, D - 1);
@@ -908,10 +1025,11 @@ __global__ __launch_bounds__(64 * kTiedWaves) void finalize_tied_kernel(Finalize
     s3 = fmaf(st[(size_t)(k + 12) * JP], mu[(k + 12) * D + d] * mu[(k + 12) * D + ec], s3);
   }
   for (; k < K; k += kTiedWaves) s0 = fmaf(st[(size_t)k * JP], mu[k * D + d] * mu[k * D + ec], s0);
-  red[w][e] = (s0 + s1) + (s2 + s3);
+  const int el = threadIdx.x & 63;
+  red[w][el] = (s0 + s1) + (s2 + s3);
   __syncthreads();
   if (w != 0 || e >= D) return;
-  const float sde = (red[0][e] + red[1][e]) + (red[2][e] + red[3][e]);
+  const float sde = (red[0][el] + red[1][el]) + (red[2][el] + red[3][el]);
   const float* G = a.gram + (size_t)b * D * D;
   const float ade = (G[d * D + e] - sde) / (float)a.N;
   const float aed = (G[e * D + d] - sde) / (float)a.N;
@@ -1001,12 +1119,15 @@ __global__ void pack_stats_kernel(PackArgs a) {
 // The waves' sums meet in LDS and the workgroup writes one partial.
 constexpr int kGramWaves = 4;
 
+// D > 64: blockIdx.z = 2·qi + qj picks the 64 x 64 quadrant (rows 64qi.., columns
+// 64qj..) of G that the workgroup sums, with T = 4.
 template <int T>
 __global__ __launch_bounds__(64 * kGramWaves) void gram_mfma_kernel(const float* x, int64_t N, int D,
                                                                     int64_t rows_per_slice, float* part) {
   constexpr int DPG = 16 * T;
   __shared__ float red[kGramWaves][DPG * DPG];
   const int b = blockIdx.y, slice = blockIdx.x;
+  const int orow = DPG * (blockIdx.z >> 1), ocol = DPG * (blockIdx.z & 1);
   const int w = threadIdx.x / 64, lane = threadIdx.x & 63, li = lane & 15, g = lane >> 4;
   const int64_t r0 = (int64_t)slice * rows_per_slice;
   const int64_t r1 = (r0 + rows_per_slice < N) ? r0 + rows_per_slice : N;
@@ -1021,16 +1142,17 @@ __global__ __launch_bounds__(64 * kGramWaves) void gram_mfma_kernel(const float*
     for (int tj = 0; tj < T; ++tj) acc[ti][tj] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int64_t n = w0; n < w1; n += 4) {
     const int64_t row = n + g;
-    float f[T];
+    float f[T], fc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const int c = 16 * t + li;
+      const int c = orow + 16 * t + li, cc = ocol + 16 * t + li;
       f[t] = (row < w1 && c < D) ? xb[(size_t)row * D + c] : 0.f;
+      fc[t] = (row < w1 && cc < D) ? xb[(size_t)row * D + cc] : 0.f;
     }
 #pragma unroll
     for (int ti = 0; ti < T; ++ti)
 #pragma unroll
-      for (int tj = 0; tj < T; ++tj) acc[ti][tj] = mfma_f32(f[ti], f[tj], acc[ti][tj]);
+      for (int tj = 0; tj < T; ++tj) acc[ti][tj] = mfma_f32(f[ti], fc[tj], acc[ti][tj]);
   }
 #pragma unroll
   for (int ti = 0; ti < T; ++ti)
@@ -1040,12 +1162,13 @@ __global__ __launch_bounds__(64 * kGramWaves) void gram_mfma_kernel(const float*
       for (int v = 0; v < 4; ++v) red[w][(16 * ti + 4 * g + v) * DPG + 16 * tj + li] = acc[ti][tj][v];
   __syncthreads();
   float* out = part + ((size_t)slice * gridDim.y + b) * D * D;
-  for (int o = threadIdx.x; o < D * D; o += blockDim.x) {
-    const int d = o / D, e = o % D;
+  for (int o = threadIdx.x; o < DPG * DPG; o += blockDim.x) {
+    const int dl = o / DPG, el = o % DPG, d = orow + dl, e = ocol + el;
+    if (d >= D || e >= D) continue;
     float sum = 0.f;
 #pragma unroll
-    for (int u = 0; u < kGramWaves; ++u) sum += red[u][d * DPG + e];
-    out[o] = sum;
+    for (int u = 0; u < kGramWaves; ++u) sum += red[u][dl * DPG + el];
+    out[(size_t)d * D + e] = sum;
   }
 }
 
@@ -1067,7 +1190,7 @@ void launch_prep(const PrepArgs& a, hipStream_t s) {
 }
 
 
-int chol_dp(int D) { return D <= 16 ? 16 : (D <= 32 ? 32 : 64); }
+int chol_dp(int D) { return D <= 16 ? 16 : (D <= 32 ? 32 : (D <= 64 ? 64 : 128)); }
 
 template <int DP>
 static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
@@ -1087,6 +1210,14 @@ static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* l
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
                  float* logdet, hipStream_t s) {
+  if (D > 64) {
+    if (M <= 0) return;
+    chol128_try_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok);
+    const bool inline_level = M <= kCholLevelInline;
+    if (!inline_level) chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
+    chol128_finish_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok, level, inline_level, prec, logdet);
+    return;
+  }
   switch (chol_dp(D)) {
     case 16: launch_chol_dp<16>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
     case 32: launch_chol_dp<32>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
@@ -1100,8 +1231,10 @@ void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, 
     rowquad_kernel<16><<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
   else if (D <= 32)
     rowquad_kernel<32><<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
-  else
+  else if (D <= 64)
     rowquad_kernel<64><<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
+  else
+    rowquad_kernel<128><<<grid, 256, 0, s>>>(x, N, D, prec, rowq);
 }
 
 int combine_blocks(int64_t N) { return (int)((N + 255) / 256); }
@@ -1160,7 +1293,7 @@ void launch_take_status(unsigned* sticky, uint32_t* out, hipStream_t s) {
 
 void launch_finalize(const FinalizeArgs& a, hipStream_t s) {
   finalize_kernel<<<dim3((a.K + kFinWaves - 1) / kFinWaves, a.B), 64 * kFinWaves, 0, s>>>(a);
-  if (a.cov == TIED) finalize_tied_kernel<<<dim3(a.D, a.B), 64 * kTiedWaves, 0, s>>>(a);
+  if (a.cov == TIED) finalize_tied_kernel<<<dim3(a.D, a.B, (a.D + 63) / 64), 64 * kTiedWaves, 0, s>>>(a);
   if (a.cov == FULL) finalize_full_kernel<<<dim3(a.K, a.B), 256, 0, s>>>(a);
 }
 
@@ -1174,7 +1307,7 @@ void launch_pack(const PackArgs& a, int B, hipStream_t s) {
 
 void launch_gram(const float* x, int B, int64_t N, int D, int slices, int64_t rows_per_slice, float* part,
                  hipStream_t s) {
-  const dim3 grid(slices, B), block(64 * kGramWaves);
+  const dim3 grid(slices, B, D > 64 ? 4 : 1), block(64 * kGramWaves);
   if (D <= 16) gram_mfma_kernel<1><<<grid, block, 0, s>>>(x, N, D, rows_per_slice, part);
   else if (D <= 32) gram_mfma_kernel<2><<<grid, block, 0, s>>>(x, N, D, rows_per_slice, part);
   else gram_mfma_kernel<4><<<grid, block, 0, s>>>(x, N, D, rows_per_slice, part);

@@ -24,6 +24,7 @@ FAMILIES = [
     ("one-tile", "spherical", 1, 9000, 32, 64, torch.float32),         # fp32 single tile pass
     ("two-pass-fp32", "diag", 1, 9000, 64, 512, torch.float32),        # fp32 LSE + STATS
     ("cholesky-tied", "tied", 1, 9000, 64, 128, torch.float32),        # jitter ladder + tied M-step
+    ("cholesky-tied-d100", "tied", 1, 6000, 100, 40, torch.float32),   # one-workgroup factorisation, D > 64
     ("cholesky-full", "full", 4, 6000, 16, 32, torch.float32),         # per-component Cholesky
 ]
 

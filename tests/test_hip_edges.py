@@ -152,3 +152,35 @@ def test_estimator_approx_top_k_large_k(hip):
                backend="hip", approx_top_k=6, device=DEV, compute_labels_on_fit=False)
     m2.fit(torch.randn(192, 8, device=DEV))
     assert m2.approximate_em_enabled_ is False and m2.approx_top_k_ is None
+
+
+@pytest.mark.parametrize("d", [40, 100])
+def test_tied_jitter_ladder_indefinite_covariance(hip, d):
+    """An indefinite tied covariance (eigenvalues in [1e-3, 3e-3] and one of
+    -5e-4): the factorisation fails at levels 0-3 and succeeds at jitter 1e-3
+    (level 4) in both implementations, with a factor of 2 to spare either way
+    (torch_fallback.py:316-334); the jittered matrix is well conditioned
+    (κ ≈ 8), so the fp32 precisions agree closely.  Data on the same scale.  The
+    per-sample log-likelihoods and the EM step from it match the oracle's.
+    D = 100 runs the one-workgroup factorisation of 64 < D <= 128."""
+    print(f"[edges] tied jitter ladder D={d}", flush=True)
+    x, means, _, w = make_problem("tied", 1, 6000, d, 12, seed=66)
+    x, means = 0.03 * x, 0.03 * means
+    g = torch.Generator().manual_seed(67)
+    q, _ = torch.linalg.qr(torch.randn(d, d, generator=g, dtype=torch.float64))
+    lam = 1e-3 * (1.0 + 2.0 * torch.rand(d, generator=g, dtype=torch.float64))
+    lam[0] = -5e-4
+    covs = ((q * lam) @ q.T)[None].float()
+    covs = 0.5 * (covs + covs.transpose(-1, -2))
+    scores, _ = hip.score("tied", to_dev(x), to_dev(means), to_dev(covs), to_dev(w))
+    e_sc = torch_ref.score_samples(x, means, covs, w, "tied")
+    torch.testing.assert_close(scores.cpu(), e_sc, rtol=1e-5, atol=1e-5 * float(e_sc.abs().mean()))
+    xd = to_dev(x)
+    m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
+    lb = torch.zeros(1, device=DEV)
+    hip.em_step("tied", xd, m_d, c_d, w_d, lb, gram_xx=hip.gram(xd))
+    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "tied", means, covs, w)
+    assert float(lb) == pytest.approx(e_lb, rel=1e-5)
+    _close(m_d, e_m)
+    _close(c_d, e_c)
+    _close(w_d, e_w)

@@ -170,6 +170,8 @@ CASES = [
     ("diag", 1, 2000, 100, 17, torch.float32),
     ("tied", 1, 20000, 64, 256, torch.float32),
     ("tied", 2, 1000, 7, 9, torch.float32),
+    ("tied", 1, 12000, 100, 40, torch.float32),          # D > 64: one-workgroup Cholesky, 128-wide tiles
+    ("tied", 1, 20000, 128, 300, torch.float32),         # D = 128, two component tiles (two passes)
     ("full", 4, 20000, 16, 32, torch.float32),
     ("full", 2, 1000, 3, 5, torch.float32),
 ]

@@ -65,7 +65,9 @@ def _prob(cov, dtype, b, n, d, k):
     ("diag", torch.float32, 128, True),
     ("diag", torch.bfloat16, 64, False),
     ("tied", torch.float32, 64, True),
-    ("tied", torch.float32, 65, False),
+    ("tied", torch.float32, 65, True),
+    ("tied", torch.float32, 128, True),
+    ("tied", torch.float32, 129, False),
     ("full", torch.float32, 16, True),
     ("full", torch.float32, 17, False),
 ])
