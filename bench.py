@@ -71,9 +71,10 @@ CONFIGS = {
     "c1l": dict(cov="spherical", B=1, N=1 << 24, D=32, K=64, dtype="bf16", iters=20, seed=0, bound="hbm",
                 desc="spherical bf16 N=16777216 D=32 K=64 (C1 recipe, large N), 20 iterations"),
 }
-# CPU-baseline samples: rows per batch and oracle iterations (about 2-8 s each on 16 cores).
-CPU_SAMPLE = {"c1": (100_000, 20), "c2": (131_072, 2), "c3": (131_072, 2), "c4": (262_144, 2),
-              "c5": (16_384, 2), "c1l": (1_048_576, 2)}
+# CPU-baseline samples: rows per batch and oracle iterations, about 10 s of CPU
+# work for the headline (C2) and 1-4 s for the others on the GPU box's 16 cores.
+CPU_SAMPLE = {"c1": (100_000, 20), "c2": (524_288, 2), "c3": (524_288, 2), "c4": (524_288, 2),
+              "c5": (65_536, 2), "c1l": (4_194_304, 2)}
 
 
 def flops(cfg):
@@ -447,7 +448,7 @@ def parity(name, data, sample):
     1e-5·mean(x²) (covariances), 1e-7 (weights); values outside the bar count
     as explained when HIP is at least as close to a float64 fit from the same
     start as the oracle is (judge.arbiter_params_ok: largest error within 2x
-    the oracle's; where the oracle itself is 2 bars or more off, the
+    the oracle's; where the oracle itself misses the bar against float64, the
     distribution rule).  For bf16 x the bar is the log-likelihood (the means,
     bf16 on both sides, are reported against one bf16 ulp)."""
     from gmmxx_amd import em

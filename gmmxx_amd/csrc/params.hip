@@ -83,17 +83,33 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
     reinterpret_cast<__bf16*>(a.w_lo)[bk * EP + e] = (__bf16)(v - (float)hi);
   };
 
+  // fp32 x: the constant C = ca·colq + cb, which the logit adds to ca·(terms ~10²
+  // times the logit), is formed in float64 (colq and cb too) and rounded once.
+  double cy64 = 0.0;
+  bool have64 = false;
+  constexpr double kLog2eD = 1.4426950408889634;
   if (a.cov == SPH) {
     float var = a.covs[bk];
     if (a.prelude) var = clamp_lo(var, a.reg_covar);
     if (lane == 0) a.covs_used[bk] = var;
     float msq = 0.f;
-    for (int d = lane; d < D; d += 64) msq = fmaf(mus[d], mus[d], msq);
+    double msq64 = 0.0;
+    for (int d = lane; d < D; d += 64) {
+      msq = fmaf(mus[d], mus[d], msq);
+      msq64 = fma((double)mus[d], (double)mus[d], msq64);
+    }
     msq = wave_sum(msq);
     const float lognorm = (float)D * ((float)kLog2Pi + logf(var));
     colq = msq;
     ca = -0.5f * kLog2e / var;
     cb = (lw - 0.5f * lognorm) * kLog2e;
+    if (!a.bf) {
+#pragma unroll
+      for (int off = 32; off >= 1; off /= 2) msq64 += __shfl_xor(msq64, off);
+      const double cb64 = ((double)lw - 0.5 * (double)D * (kLog2Pi + log((double)var))) * kLog2eD;
+      cy64 = (double)ca * msq64 + cb64;
+      have64 = true;
+    }
     if (a.bf) {
       // bf16 kernel: W' = -2·ca·μ (hi/lo) and the augmented constants
       // [A_h A_h A_h A_m A_m A_l C_h C_m | C_l 0 ...] with A = ca, C = ca·‖μ‖² + cb.
@@ -120,39 +136,51 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
     // torch_fallback.py:2491-2494
     const float* vr = a.covs + bk * D;
     float* vu = a.covs_used + bk * D;
-    float logdet = 0.f, mpm = 0.f;
+    // P = 1/v (correctly rounded either way), -2μP and Σ μ²P in float64, each
+    // rounded once (fp32 chains here carried the largest share of the logit error)
+    double logdet = 0.0, mpm = 0.0;
     for (int d = lane; d < D; d += 64) {
       float v = vr[d];
       if (a.prelude) v = clamp_lo(v, a.reg_covar);
       vu[d] = v;
       const float vc = clamp_lo(v, 1e-30f);
-      const float p = 1.f / vc;
-      const float wm = mus[d] * p;
-      logdet += logf(vc);
-      mpm = fmaf(mus[d], wm, mpm);
-      put_f32(d, p);
-      put_f32(DP + d, -2.f * wm);
+      const double p = 1.0 / (double)vc;
+      const double wm = (double)mus[d] * p;
+      logdet += log((double)vc);
+      mpm = fma((double)mus[d], wm, mpm);
+      put_f32(d, (float)p);
+      put_f32(DP + d, (float)(-2.0 * wm));
     }
     for (int d = D + lane; d < DP; d += 64) { put_f32(d, 0.f); put_f32(DP + d, 0.f); }
     for (int e = 2 * DP + lane; e < EP; e += 64) put_f32(e, 0.f);
-    logdet = wave_sum(logdet);
-    colq = wave_sum(mpm);
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) {
+      logdet += __shfl_xor(logdet, off);
+      mpm += __shfl_xor(mpm, off);
+    }
+    colq = (float)mpm;
     ca = -0.5f * kLog2e;
-    cb = (lw - 0.5f * (log2pi_d + logdet)) * kLog2e;
+    cb = (float)(((double)lw - 0.5 * ((double)log2pi_d + logdet)) * kLog2eD);
+    cy64 = -0.5 * kLog2eD * mpm + ((double)lw - 0.5 * ((double)log2pi_d + logdet)) * kLog2eD;
+    have64 = true;
   } else if (a.cov == TIED) {
     // Pμ_k (torch_fallback.py:2873), μᵀPμ (:2874)
     const float* P = a.prec + (size_t)b * D * D;
-    float mpm = 0.f;
+    double mpm = 0.0;
     for (int d = lane; d < D; d += 64) {
-      float pm = 0.f;
-      for (int e = 0; e < D; ++e) pm = fmaf(mus[e], P[d * D + e], pm);
-      mpm = fmaf(mus[d], pm, mpm);
-      put_f32(d, pm);
+      double pm = 0.0;
+      for (int e = 0; e < D; ++e) pm = fma((double)mus[e], (double)P[d * D + e], pm);
+      mpm = fma((double)mus[d], pm, mpm);
+      put_f32(d, (float)pm);
     }
     for (int e = D + lane; e < EP; e += 64) put_f32(e, 0.f);
-    colq = wave_sum(mpm);
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) mpm += __shfl_xor(mpm, off);
+    colq = (float)mpm;
     ca = -0.5f * kLog2e;
     cb = (lw - 0.5f * (log2pi_d + a.logdet[b])) * kLog2e;
+    cy64 = (double)ca * mpm + ((double)lw - 0.5 * ((double)log2pi_d + (double)a.logdet[b])) * kLog2eD;
+    have64 = true;
     if (a.shift) {
       // The tied EM logits leave out each row's xᵀPx, so the row log-normalisers
       // are each ½ xᵀPx too large; their sum, -½ Σ_n x_nᵀ P x_n = -½ Σ_rj P_rj
@@ -229,14 +257,13 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
 #pragma unroll
     for (int off = 32; off >= 1; off /= 2) mpm += __shfl_xor(mpm, off);
     // (ca, ca·μᵀPμ + cb) with the constant rounded once from float64
-    constexpr double kLog2eD = 1.4426950408889634;
     const double cbd = ((double)lw - 0.5 * ((double)log2pi_d + (double)a.logdet[bk])) * kLog2eD;
     if (lane == 0) a.cconst[bk] = make_float4(-0.5f * kLog2e, (float)(-0.5 * kLog2eD * mpm + cbd), 0.f, 0.f);
     return;
   }
   // l2 = ca * (rowq - 2S + colq) + cb (spherical, tied: S is the cross term x·μ / x·Pμ) or
   // ca * (S + colq) + cb (diag, full: W already carries the -2), stored as (ca, ca*colq + cb).
-  if (lane == 0) a.cconst[bk] = make_float4(ca, fmaf(ca, colq, cb), 0.f, 0.f);
+  if (lane == 0) a.cconst[bk] = make_float4(ca, have64 ? (float)cy64 : fmaf(ca, colq, cb), 0.f, 0.f);
 }
 
 // ---------------------------------------------------------------------------

@@ -4,7 +4,8 @@ Test infrastructure, like the rest of ``oracle/``: only ``tests/``, the smoke
 check and the checker legs of ``bench.py`` use it; the product never does.
 
 Direct float64 arithmetic (spherical/diag logits from the expanded quadratic
-form, tied/full from triangular solves of (x - μ), natural-log units), with
+form, full from triangular solves of (x - μ), tied from the solves of x and μ
+expanded, natural-log units), with
 the reference's iteration prelude and
 finalize semantics (variance clamp to reg_covar, weight floor and
 renormalisation, active masks, tied/full symmetrisation plus reg·I;
@@ -47,7 +48,13 @@ def _logits(x, cov, means, covs, w):
         return -0.5 * (maha.clamp_min(0.0) + d * LOG_2PI + torch.log(var).sum(-1)[:, None, :]) + logw
     Ls = _chol(covs)
     if cov == "tied":
-        Ls = Ls[:, None].expand(-1, means.shape[1], -1, -1)
+        # one solve for the rows and one for the means: ‖L⁻¹(x - μ)‖² expanded,
+        # harmless in float64
+        z = torch.linalg.solve_triangular(Ls, x.transpose(1, 2), upper=False).transpose(1, 2)
+        nu = torch.linalg.solve_triangular(Ls, means.transpose(1, 2), upper=False).transpose(1, 2)
+        maha = z.square().sum(-1)[:, :, None] - 2.0 * torch.bmm(z, nu.transpose(1, 2)) + nu.square().sum(-1)[:, None, :]
+        logdet = 2.0 * torch.log(torch.diagonal(Ls, dim1=-2, dim2=-1)).sum(-1)
+        return -0.5 * (maha.clamp_min(0.0) + d * LOG_2PI + logdet[:, None, None]) + logw
     out = torch.empty((b, n, means.shape[1]), dtype=torch.float64)
     for kk in range(means.shape[1]):
         L = Ls[:, kk]

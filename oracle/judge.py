@@ -31,8 +31,8 @@ Where a problem is ill-conditioned enough that single elements of both fp32
 results land several bars from float64 (the full-covariance benchmark
 recipe: condition numbers up to ~1400; the diagonal recipe on a row sample),
 the largest error is a noisy statistic of a few elements; there -- the
-oracle's own largest error at least ILL_CONDITIONED = 2 bars -- the
-distribution rule applies (``arbiter_distribution_ok``, and
+oracle's own largest error at least ILL_CONDITIONED = 1 bar, i.e. the fp32
+reference itself misses the bar -- the distribution rule applies (``arbiter_distribution_ok``, and
 ``arbiter_params_ok`` for the selection ``judge_params`` makes): the bulk -- the 99th percentile of the
 error against float64 -- within FACTOR times the oracle's (or 0.05 bar),
 and the tail -- the largest error -- within TAIL_FACTOR times the oracle's
@@ -60,8 +60,9 @@ def arbiter_distribution_ok(hip_dist, oracle_dist):
 
 
 # The oracle's own largest error against float64, in bars, from which a problem
-# counts as ill-conditioned (single elements of an fp32 result several bars off).
-ILL_CONDITIONED = 2.0
+# counts as ill-conditioned: the reference's fp32 arithmetic itself misses the
+# bar there, so single elements are a noisy statistic at the bar's scale.
+ILL_CONDITIONED = 1.0
 
 
 def arbiter_params_ok(hip_dist, oracle_dist):
