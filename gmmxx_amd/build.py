@@ -19,8 +19,8 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libgmmxx_hip.so")
-SOURCES = ("em_tile.hip", "em_sph_bf16.hip", "em_fused.hip", "em_coop.hip", "params.hip", "kmeans.hip",
-           "abi.hip")
+SOURCES = ("em_tile.hip", "em_sph_bf16.hip", "em_fused.hip", "em_coop.hip", "em_full_wide.hip", "params.hip",
+           "kmeans.hip", "abi.hip")
 ARCH = os.environ.get("GMMXX_HIP_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.

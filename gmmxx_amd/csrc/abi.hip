@@ -63,6 +63,11 @@ struct Plan {
   int chol_m = 0;
   size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_wmu = 0, o_wsc = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
   size_t o_xch = 0, o_flags = 0;
+  // full covariance at D > 16 (whitening E-step, weighted-Gram statistics)
+  bool fw = false;
+  int fw_eblk = 0, fw_slices = 0;
+  int64_t fw_rows = 0;
+  size_t o_lpack = 0, o_lpaug = 0, o_l2w = 0, o_linv = 0;
   size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_lbuf = 0, o_prec = 0, o_logdet = 0,
          o_gram = 0, total = 0;
 };
@@ -96,15 +101,18 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.D = (int)p->D;
   q.K = (int)p->K;
   if (q.bf && q.cov != SPH) return fail(GMMXX_ERR_UNSUPPORTED, "bf16 input is supported for spherical only");
-  const int dmax = (q.cov == FULL) ? 16 : 128;
+  const int dmax = 128;
   if (p->D > dmax) return fail(GMMXX_ERR_UNSUPPORTED, "D exceeds the supported maximum for this covariance type");
   q.DP = dp_for(q.D);
+  // Full covariance beyond D = 16: the whitening kernels of em_full_wide.hip
+  // (the tile kernel's augmented features are built for D = 16).
+  q.fw = q.cov == FULL && q.DP > 16;
   const bool sph_bf = q.bf && q.cov == SPH;          // dedicated kernel, DP >= 32
   if (sph_bf) q.DP = std::max(q.DP, 32);
   const int S = q.DP * (q.DP + 1) / 2;
   const int E = (q.cov == SPH || q.cov == TIED) ? q.DP : (q.cov == DIAG ? 2 * q.DP : S + q.DP);
   const int J = (q.cov == SPH) ? q.DP + 3 : (q.cov == DIAG ? 2 * q.DP + 1 : (q.cov == TIED ? q.DP + 1 : q.DP + S + 1));
-  q.EP = round_up(E, 32);
+  q.EP = q.fw ? 0 : round_up(E, 32);
   q.JP = round_up(J, 16);
   q.nk_col = (q.cov == SPH) ? q.DP : (q.cov == DIAG ? 2 * q.DP : (q.cov == TIED ? q.DP : q.DP + S));
   q.sq_col = q.DP + 1;
@@ -176,7 +184,8 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   // statistics kernel is at the register limit).  GMMXX_HIP_NO_SINGLE=1 selects
   // the two passes.
   const char* no_single = getenv("GMMXX_HIP_NO_SINGLE");
-  q.single = !sph_bf && q.ktiles == 1 && !(q.cov == DIAG && q.DP >= 128) && !(no_single && no_single[0] == '1');
+  q.single = !sph_bf && !q.fw && q.ktiles == 1 && !(q.cov == DIAG && q.DP >= 128) &&
+             !(no_single && no_single[0] == '1');
   // Exchange single pass (fp32 spherical, tied, diag at D <= 64; 2..4 component
   // tiles of 8 waves): the workgroups of a row slice swap per-row (max, sum)
   // partials, so x is read once per iteration.  They must be co-resident: the
@@ -200,6 +209,16 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.gram_rows = ((q.N + gs - 1) / gs + 15) / 16 * 16;
   q.gram_slices = (int)((q.N + q.gram_rows - 1) / q.gram_rows);
   q.chol_m = (q.cov == TIED) ? q.B : (q.cov == FULL ? q.B * q.K : 0);
+  if (q.fw) {
+    // E-step: one wave per 32-row block.  Statistics: one wave per component,
+    // about 2048 workgroups of four components over row slices.
+    q.fw_eblk = fw_eblocks(q.N);
+    const int64_t groups = (int64_t)((q.K + 3) / 4) * q.B;
+    int64_t fs = std::max<int64_t>(1, (2048 + groups - 1) / groups);
+    fs = std::min(fs, std::max<int64_t>(1, row_blocks / kMinBlocksPerSlice));
+    q.fw_rows = ((q.N + fs - 1) / fs + kBN - 1) / kBN * kBN;
+    q.fw_slices = (int)((q.N + q.fw_rows - 1) / q.fw_rows);
+  }
 
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -220,10 +239,11 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_rowaux = take(sph_bf && q.DP >= 128 ? BN * 16 : 0);
   q.o_pms = take((size_t)std::max(q.ktiles, q.lktiles) * BN * 8);
   q.o_pidx = take((size_t)q.ktiles * BN * 4);
-  q.o_pstats = take((size_t)std::max({q.slices, q.fslices, q.cspb, q.xslices}) * BK * q.JP * 4);
+  // (the full-covariance kernels at D > 16 use their own slices only)
+  q.o_pstats = take((size_t)(q.fw ? q.fw_slices : std::max({q.slices, q.fslices, q.cspb, q.xslices})) * BK * q.JP * 4);
   q.o_stats = take(BK * q.JP * 4);
   // (+B: the tied EM iteration's per-batch log-likelihood shift, after the row partials)
-  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices, q.xslices}) + q.D + 1) * 8);
+  q.o_ll = take((size_t)q.B * (std::max({q.cblocks, q.fslices, q.cspb, q.slices, q.xslices, q.fw_eblk}) + q.D + 1) * 8);
   q.o_xch = take(q.coop ? (size_t)q.cNG * kRing * q.cG * kBN * 8
                         : (q.xch ? (size_t)q.B * q.xslices * kRing * q.ktiles * kBN * 8 : 0));
   // [0] status of the last cooperative pass (zeroed by its launcher), [1] sticky
@@ -234,6 +254,10 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
   q.o_logdet = take((size_t)q.chol_m * 4);
   q.o_gram = take(q.cov == TIED ? (size_t)q.gram_slices * q.B * q.D * q.D * 4 : 0);
+  q.o_lpack = take(q.fw ? (size_t)fw_lpack_floats(q.B, q.K, q.DP) * 4 : 0);
+  q.o_lpaug = take(q.fw ? BK * (q.DP / 32) * 64 * 4 : 0);
+  q.o_l2w = take(q.fw ? BK * (size_t)q.N * 4 : 0);
+  q.o_linv = take(q.fw ? BK * q.D * q.D * 4 : 0);
   q.total = off;
   return GMMXX_OK;
 }
@@ -366,14 +390,44 @@ LlFold ll_fold(const Plan& pl, void* ws, int parts, double inv_total, float* out
   return ll;
 }
 int stat_slices(const Plan& pl) {
-  return pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.xch ? pl.xslices : pl.slices));
+  return pl.fw ? pl.fw_slices : (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.xch ? pl.xslices : pl.slices)));
 }
 // The tile-partial buffer is free once the statistics are being reduced: it is
 // the scratch of the grouped slice reduction.
 float* red_tmp(const Plan& pl, void* ws) { return at<float>(ws, pl.o_pms); }
 int64_t red_tmp_floats(const Plan& pl) { return (int64_t)std::max(pl.ktiles, pl.lktiles) * pl.B * pl.N * 2; }
 int ll_parts(const Plan& pl) {
-  return pl.B * (pl.fused ? pl.fparts : (pl.coop ? pl.cspb : (pl.xch ? pl.xslices : (pl.single ? pl.slices : pl.cblocks))));
+  return pl.B * (pl.fw ? pl.fw_eblk
+                       : (pl.fused ? pl.fparts
+                                   : (pl.coop ? pl.cspb : (pl.xch ? pl.xslices : (pl.single ? pl.slices : pl.cblocks)))));
+}
+// The log-likelihood partials come out of the pass itself (no combine phase).
+bool ll_in_pass(const Plan& pl) { return single_pass(pl) || pl.fw; }
+
+// Full covariance at D > 16: the E-step / statistics kernels' arguments.
+FwArgs fw_args(const Plan& pl, const void* x, void* ws) {
+  FwArgs a{};
+  a.x = reinterpret_cast<const float*>(x);
+  a.vec_ok = (pl.D == pl.DP) && ((uintptr_t)x % 16 == 0);
+  a.N = pl.N;
+  a.D = pl.D;
+  a.K = pl.K;
+  a.B = pl.B;
+  a.lpack = at<float>(ws, pl.o_lpack);
+  a.lpaug = at<float>(ws, pl.o_lpaug);
+  a.cconst = at<float4>(ws, pl.o_cconst);
+  a.l2 = at<float>(ws, pl.o_l2w);
+  a.lse2 = at<float>(ws, pl.o_lse2);
+  a.ll_part = at<double>(ws, pl.o_ll);
+  a.part_stats = at<float>(ws, pl.o_pstats);
+  a.JP = pl.JP;
+  a.nk_col = pl.nk_col;
+  a.rows_per_slice = pl.fw_rows;
+  return a;
+}
+int run_fw(const Plan& pl, int phase, const FwArgs& a, hipStream_t s) {
+  if (launch_fw(pl.DP, phase, a, pl.fw_slices, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no full-covariance kernel for this D");
+  return check_hip(phase == 0 ? "full-covariance E-step" : "full-covariance statistics");
 }
 // Where an EM iteration's tied -½ tr(P XᵀX) terms go: after the log-likelihood
 // partials of its log-normaliser pass (the single-pass or the combine kernel's),
@@ -395,7 +449,25 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
     prec = at<float>(ws, pl.o_prec);
     logdet = at<float>(ws, pl.o_logdet);
     launch_chol(covs, pl.D, pl.chol_m, at<int>(ws, pl.o_first), at<int>(ws, pl.o_first) + pl.chol_m,
-                at<float>(ws, pl.o_lbuf), prec, logdet, s);
+                at<float>(ws, pl.o_lbuf), prec, logdet, s, pl.fw ? at<float>(ws, pl.o_linv) : nullptr);
+  }
+  if (pl.fw) {
+    FwPackArgs f{};
+    f.B = pl.B;
+    f.K = pl.K;
+    f.D = pl.D;
+    f.DP = pl.DP;
+    f.prelude = prelude;
+    f.min_weight = (float)minw;
+    f.means = means;
+    f.weights = weights;
+    f.linv = at<float>(ws, pl.o_linv);
+    f.logdet = logdet;
+    f.lpack = at<float>(ws, pl.o_lpack);
+    f.lpaug = at<float>(ws, pl.o_lpaug);
+    f.cconst = at<float4>(ws, pl.o_cconst);
+    launch_fw_pack(f, s);
+    return check_hip("parameter preparation");
   }
   PrepArgs a{};
   a.cov = pl.cov;
@@ -626,6 +698,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s, /*rowquad=*/false, gram,
                      tied_shift(pl, ws));
     case GMMXX_PHASE_LSE_TILE: {
+      if (pl.fw) return run_fw(pl, 0, fw_args(pl, x, ws), s);
       if (pl.coop) return run_coop(pl, x, ws, s);
       if (pl.xch) return run_xch(pl, x, ws, s, /*em=*/true);
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
@@ -640,7 +713,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     case GMMXX_PHASE_COMBINE: {
       // A single pass already produced per-slice log-likelihoods: they are summed
       // by the reduce phase's launch (one launch fewer per iteration).
-      if (single_pass(pl)) return GMMXX_OK;
+      if (ll_in_pass(pl)) return GMMXX_OK;
       CombineArgs c{};
       c.B = pl.B;
       c.ktiles = pl.lktiles;
@@ -656,6 +729,7 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
       return check_hip("combine");
     }
     case GMMXX_PHASE_STATS_TILE: {
+      if (pl.fw) return run_fw(pl, 1, fw_args(pl, x, ws), s);
       if (single_pass(pl)) return GMMXX_OK;  // statistics came out of the single pass
       const TileArgs t = tile_args(pl, x, ws, /*em=*/true);
       if (run_tile(pl, MODE_STATS, t, s) != 0)
@@ -664,14 +738,14 @@ int gmmxx_hip_em_phase(const gmmxx_problem* p, int phase, const void* x, float* 
     }
     case GMMXX_PHASE_REDUCE: {
       LlFold ll{};
-      if (single_pass(pl)) {
+      if (ll_in_pass(pl)) {
         int parts = ll_parts(pl);
         if (tied_shift(pl, ws)) parts += pl.B * pl.D;   // -½ tr(P XᵀX) rows, from the prepare phase
         ll = ll_fold(pl, ws, parts, 1.0 / ((double)pl.B * (double)pl.N), lower_bound);
       }
       launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                            at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl),
-                           single_pass(pl) ? &ll : nullptr);
+                           ll_in_pass(pl) ? &ll : nullptr);
       return check_hip("statistics reduction");
     }
     case GMMXX_PHASE_FINALIZE:
@@ -727,7 +801,14 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, reg_covar, min_weight, 1, ws, s))) return rc;
-  if (pl.fused || pl.coop || pl.single || pl.xch) {
+  if (pl.fw) {
+    const FwArgs a = fw_args(pl, x, ws);
+    if ((rc = run_fw(pl, 0, a, s)) || (rc = run_fw(pl, 1, a, s))) return rc;
+    const LlFold ll = ll_fold(pl, ws, ll_parts(pl), 1.0, ll_sum);
+    launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
+                         at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl), &ll);
+    if ((rc = check_hip("full-covariance statistics reduction"))) return rc;
+  } else if (pl.fused || pl.coop || pl.single || pl.xch) {
     if (pl.coop) {
       if ((rc = run_coop(pl, x, ws, s))) return rc;
     } else if (pl.xch) {
@@ -790,6 +871,7 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   if (top_k < 1 || top_k >= pl.K)
     return fail(GMMXX_ERR_INVALID_ARGUMENT, "top_k must be in [1, K-1] (top_k >= K is exact EM)");
+  if (pl.fw) return fail(GMMXX_ERR_UNSUPPORTED, "approximate top-k EM is not available for full covariance at D > 16");
   const hipStream_t s = (hipStream_t)stream;
   // Parameters with the iteration prelude; tied rows get xᵀPx, so the logits
   // (and the log-normalisers) are complete.
@@ -906,6 +988,14 @@ int gmmxx_hip_score(const gmmxx_problem* p, const void* x, const float* means, c
   if (!means || !covs || !weights) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL parameter buffer");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
+  if (pl.fw) {
+    FwArgs a = fw_args(pl, x, ws);
+    a.l2 = nullptr;
+    a.ll_part = nullptr;
+    a.scores = scores;
+    a.labels = labels;
+    return run_fw(pl, 0, a, s);
+  }
   return lse_pass(pl, x, ws, scores, labels, false, s);
 }
 
@@ -919,6 +1009,15 @@ int gmmxx_hip_predict_proba_score(const gmmxx_problem* p, const void* x, const f
   if (!proba && !scores) return fail(GMMXX_ERR_INVALID_ARGUMENT, "proba and scores are both NULL");
   const hipStream_t s = (hipStream_t)stream;
   if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
+  if (pl.fw) {
+    FwArgs a = fw_args(pl, x, ws);
+    if (!proba) a.l2 = nullptr;
+    a.ll_part = nullptr;
+    a.scores = scores;
+    if ((rc = run_fw(pl, 0, a, s))) return rc;
+    if (proba) launch_fw_proba(a.l2, a.lse2, proba, pl.B, pl.N, pl.K, s);
+    return check_hip("predict_proba");
+  }
   if (!proba) return lse_pass(pl, x, ws, scores, nullptr, false, s);
   // One tile pass when the workgroup holds every component (the pass forms the
   // row log-normalisers, which are the scores); otherwise the log-normaliser

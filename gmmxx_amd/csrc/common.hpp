@@ -63,6 +63,14 @@ __host__ __device__ constexpr int full_feature(int d, int e) {
   return 104 + 16 * cd + 4 * i + j;   // ce == cd + 2
 }
 
+// Position of Σ r x_d x_e (d <= e < DP) in the statistics rows of the full
+// covariance at DP >= 32: the upper triangle row by row.
+__host__ __device__ constexpr int fw_tri(int DP, int d, int e) { return d * DP - d * (d - 1) / 2 + (e - d); }
+
+// Column of Σ r x_d x_e (d <= e) after the DP columns of Σ r x in a full-covariance
+// statistics row: the tile kernel's feature order at DP = 16, fw_tri above it.
+__host__ __device__ constexpr int full_sxx(int DP, int d, int e) { return DP == 16 ? full_feature(d, e) : fw_tri(DP, d, e); }
+
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

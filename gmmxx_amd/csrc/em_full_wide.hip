@@ -1,0 +1,363 @@
+// Full covariance at 16 < D <= 128: whitening E-step and weighted-Gram M-step
+// on the fp32 MFMA (v_mfma_f32_32x32x2_f32).
+//
+// The augmented formulation of em_tile.hip (features = the D(D+1)/2 products
+// x_d x_e, split into bf16 parts) is built for D = 16; at larger D its feature
+// rows outgrow the LDS.  Here the per-component quadratic form is formed as a
+// squared norm instead, (x - μ)ᵀ Σ⁻¹ (x - μ) = ‖L⁻¹x - L⁻¹μ‖² with Σ = L Lᵀ
+// (torch_fallback.py:400-432 computes the same value expanded, xᵀPx - 2xᵀPμ +
+// μᵀPμ, clamped at zero; the norm is never negative and has no cancellation
+// between the expanded terms), and the M-step statistics are the uncentered
+// sums N_k = Σ r, Σ r·x and Σ r·x xᵀ the reference's matrix M-step reads
+// (:3143-3167).
+//
+//   fw_pack_kernel   per component: the iteration prelude's weight, b = L⁻¹μ and
+//                    the log2 constant in float64, and L⁻¹ laid out as the MFMA's
+//                    A operand (one 16-deep chunk = 64 lanes x 16 floats);
+//   fw_estep_kernel  one wave per 32-row block, every component in turn: the
+//                    32 x 32 output tiles of y = L⁻¹x (rows i of L⁻¹ against the
+//                    block's rows, k over x's columns; L⁻¹ is lower triangular, so
+//                    tile t needs only chunks c <= t), one more rank-1 MFMA adds
+//                    -b, and each lane sums the squares of its 16 entries; the
+//                    partner lane (l ^ 32) holds the other 16.  The row's
+//                    log-normaliser is accumulated online over the components;
+//                    the log2 logits go to a (B, K, N) buffer;
+//   fw_stats_kernel  one wave per component and row slice: Σ_n r_n x_n x_nᵀ as
+//                    the lower tiles of (r ⊙ X)ᵀ X over 2-row k-steps, Σ r x and
+//                    Σ r beside it on the VALU, r = 2^(l2 - lse2) from the
+//                    E-step's buffers;
+//   fw_proba_kernel  predict_proba: r = 2^(l2 - lse2) transposed to (B, N, K).
+//
+// 32x32x2 fp32 MFMA operand layout: lane l supplies A[i = l % 32][k = l / 32]
+// and B[k = l / 32][j = l % 32]; accumulator register v of lane l holds
+// C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+
+#include <math.h>
+
+#include "common.hpp"
+#include "engine.hpp"
+
+namespace gx {
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32f(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// v of lane l % 32 plus v of lane l % 32 + 32, the same bits in both lanes
+// (the swap yields the low half's value in one word and the high half's in the
+// other, in every lane).
+__device__ __forceinline__ float half_sum(float v) {
+  const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+
+constexpr int kFwWaves = 4;
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Operand packing (prelude, L⁻¹ chunks, -L⁻¹μ, constants)
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void fw_pack_kernel(FwPackArgs a) {
+  __shared__ double red[4];
+  __shared__ double bsh[128];
+  const int k = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int K = a.K, D = a.D, DP = a.DP, NT = DP / 32, NCH = NT * (NT + 1) / 2;
+  const size_t bk = (size_t)b * K + k;
+  // Iteration prelude (torch_fallback.py:2061-2066): w <- max(w, min_weight) / Σ;
+  // inference uses the weights as given.
+  const float* wrow = a.weights + (size_t)b * K;
+  float wk = wrow[k];
+  if (a.prelude) {
+    float sw = 0.f;
+    for (int j = t; j < K; j += 256) sw += clamp_lo(wrow[j], a.min_weight);
+    for (int off = 32; off >= 1; off /= 2) sw += __shfl_xor(sw, off);
+    if ((t & 63) == 0) red[t >> 6] = (double)sw;
+    __syncthreads();
+    const float total = (float)red[0] + (float)red[1] + (float)red[2] + (float)red[3];
+    wk = clamp_lo(wk, a.min_weight) / total;
+  }
+  const float* X = a.linv + bk * D * D;
+  const float* mu = a.means + bk * D;
+  // b = L⁻¹μ in float64 (row i of L⁻¹ has entries j <= i)
+  if (t < D) {
+    double acc = 0.0;
+    for (int j = 0; j <= t; ++j) acc = fma((double)X[t * D + j], (double)mu[j], acc);
+    bsh[t] = acc;
+  }
+  __syncthreads();
+  if (t < 64) {
+    float* aug = a.lpaug + bk * NT * 64;
+    for (int tt = 0; tt < NT; ++tt) {
+      const int i = 32 * tt + (t & 31);
+      aug[tt * 64 + t] = (t < 32 && i < D) ? (float)(-bsh[i]) : 0.f;
+    }
+  }
+  if (t == 0) {
+    constexpr double kLog2eD = 1.4426950408889634;
+    const double c2 = (log((double)wk) - 0.5 * ((double)D * kLog2Pi + (double)a.logdet[bk])) * kLog2eD;
+    a.cconst[bk] = make_float4((float)c2, 0.f, 0.f, 0.f);
+  }
+  // chunk j = (tile tt, column chunk c), j = tt (tt + 1) / 2 + c; lane l, slot u:
+  // L⁻¹[32 tt + l % 32][32 c + 16 (l / 32) + u]
+  float* lp = a.lpack + bk * NCH * 1024;
+  for (int e = t; e < NCH * 1024; e += 256) {
+    const int j = e >> 10, lane = (e >> 4) & 63, u = e & 15;
+    int tt = 0;
+    while ((tt + 1) * (tt + 2) / 2 <= j) ++tt;
+    const int c = j - tt * (tt + 1) / 2;
+    const int i = 32 * tt + (lane & 31), col = 32 * c + 16 * (lane >> 5) + u;
+    lp[e] = (i < D && col < D) ? X[i * D + col] : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// E-step: log2 logits, row log-normalisers, labels, log-likelihood partials
+// ---------------------------------------------------------------------------
+
+template <int DP>
+__global__ __launch_bounds__(64 * kFwWaves) void fw_estep_kernel(FwArgs a) {
+  constexpr int NT = DP / 32, NCH = NT * (NT + 1) / 2;
+  __shared__ double llw[kFwWaves];
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane & 31, h = lane >> 5;
+  const int b = blockIdx.y;
+  const int64_t N = a.N;
+  const int D = a.D, K = a.K;
+  const int64_t n0 = ((int64_t)blockIdx.x * kFwWaves + wave) * 32;
+  const int64_t n = n0 + lr;
+  const bool valid = n < N;
+
+  // x block as the B operand: lane l holds row n, columns 32 c + 16 h + u.
+  float xr[NT][16];
+  {
+    const float* xrow = a.x + ((size_t)b * N + (valid ? n : 0)) * D;
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      const int col0 = 32 * c + 16 * h;
+      if (a.vec_ok) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = valid ? *reinterpret_cast<const f32x4*>(xrow + col0 + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xr[c][4 * q + r] = v[r];
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) xr[c][u] = (valid && col0 + u < D) ? xrow[col0 + u] : 0.f;
+      }
+    }
+  }
+  const float one = h == 0 ? 1.f : 0.f;
+
+  // L⁻¹ chunks stream through a one-chunk prefetch; the buffer holds one spare
+  // chunk after the last component, so the final prefetch stays in bounds.
+  const float* lp = a.lpack + (size_t)b * K * NCH * 1024 + lane * 16;
+  f32x4 nx[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) nx[q] = *reinterpret_cast<const f32x4*>(lp + 4 * q);
+
+  float m = -INFINITY, s = 0.f, best = -INFINITY;
+  int bidx = 0;
+  for (int k = 0; k < K; ++k) {
+    const size_t bk = (size_t)b * K + k;
+    float augv[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) augv[tt] = a.lpaug[(bk * NT + tt) * 64 + lane];
+    float q = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      f32x16 acc = f32x16{};
+#pragma unroll
+      for (int c = 0; c <= tt; ++c) {
+        f32x4 cur[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cur[r] = nx[r];
+        lp += 1024;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) nx[r] = *reinterpret_cast<const f32x4*>(lp + 4 * r);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc = mfma32f(cur[u / 4][u % 4], xr[c][u], acc);
+      }
+      acc = mfma32f(augv[tt], one, acc);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) q = fmaf(acc[v], acc[v], q);
+    }
+    q = half_sum(q);
+    const float l2 = a.cconst[bk].x - 0.5f * kLog2e * q;
+    if (l2 > m) {
+      s = s * fast_exp2(m - l2) + 1.f;   // m = -inf: s is 0
+      m = l2;
+    } else if (l2 != -INFINITY) {
+      s += fast_exp2(l2 - m);            // NaN passes through
+    }
+    if (l2 > best) {
+      best = l2;
+      bidx = k;
+    }
+    if (a.l2 && h == 0 && valid) a.l2[bk * N + n] = l2;
+  }
+  const float lse = m + __log2f(s);
+  double ll = 0.0;
+  if (h == 0 && valid) {
+    a.lse2[(size_t)b * N + n] = lse;
+    if (a.scores) a.scores[(size_t)b * N + n] = lse * kLn2;
+    if (a.labels) a.labels[(size_t)b * N + n] = bidx;
+    ll = (double)lse * (double)kLn2;
+  }
+  if (a.ll_part) {
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) ll += __shfl_xor(ll, off);
+    if (lane == 0) llw[wave] = ll;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double sum = 0.0;
+      for (int w = 0; w < kFwWaves; ++w) sum += llw[w];
+      a.ll_part[(size_t)b * gridDim.x + blockIdx.x] = sum;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// M-step statistics: N_k, Σ r x, Σ r x xᵀ per component and row slice
+// ---------------------------------------------------------------------------
+
+template <int DP>
+__global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
+  constexpr int NT = DP / 32, NTT = NT * (NT + 1) / 2;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane & 31, h = lane >> 5;
+  const int b = blockIdx.z;
+  const int k = blockIdx.y * kFwWaves + wave;
+  if (k >= a.K) return;   // whole wave; the kernel has no barrier
+  const int64_t N = a.N;
+  const int D = a.D;
+  const size_t bk = (size_t)b * a.K + k;
+  const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_slice;
+  const int64_t r1 = (r0 + a.rows_per_slice < N) ? r0 + a.rows_per_slice : N;
+  const float* xb = a.x + (size_t)b * N * D;
+  const float* l2 = a.l2 + bk * N;
+  const float* lse2 = a.lse2 + (size_t)b * N;
+
+  f32x16 acc[NTT];
+#pragma unroll
+  for (int i = 0; i < NTT; ++i) acc[i] = f32x16{};
+  float sx[NT];
+#pragma unroll
+  for (int c = 0; c < NT; ++c) sx[c] = 0.f;
+  float sr = 0.f;
+
+  for (int64_t n0 = r0; n0 < r1; n0 += 32) {
+    const int64_t nr = n0 + lr;
+    const float rv = nr < r1 ? fast_exp2(l2[nr] - lse2[nr]) : 0.f;
+#pragma unroll 4
+    for (int st = 0; st < 16; ++st) {
+      const int src = 2 * st + h;   // row of this k-step for this lane's half
+      const float r = __shfl(rv, src);
+      const int64_t n = n0 + src;
+      const bool rowok = n < r1;
+      float xv[NT], z[NT];
+#pragma unroll
+      for (int c = 0; c < NT; ++c) {
+        const int col = 32 * c + lr;
+        xv[c] = (rowok && col < D) ? xb[(size_t)n * D + col] : 0.f;
+        z[c] = r * xv[c];
+        sx[c] += z[c];
+      }
+      sr += r;
+      int ti = 0;
+#pragma unroll
+      for (int I = 0; I < NT; ++I)
+#pragma unroll
+        for (int J = 0; J <= I; ++J, ++ti) acc[ti] = mfma32f(z[I], xv[J], acc[ti]);
+    }
+  }
+
+  // Statistics row: [Σ r x (DP) | Σ r x xᵀ packed (d <= e < DP, row by row) | N_k | 0 ...]
+  float* out = a.part_stats + (((size_t)blockIdx.x * a.B + b) * a.K + k) * a.JP;
+#pragma unroll
+  for (int c = 0; c < NT; ++c) {
+    const float tot = half_sum(sx[c]);
+    if (h == 0) out[32 * c + lr] = tot;
+  }
+  int ti = 0;
+#pragma unroll
+  for (int I = 0; I < NT; ++I)
+#pragma unroll
+    for (int J = 0; J <= I; ++J, ++ti)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gi = 32 * I + 8 * (v / 4) + 4 * h + (v % 4), gj = 32 * J + lr;
+        if (gi >= gj) out[DP + fw_tri(DP, gj, gi)] = acc[ti][v];
+      }
+  const float nk = half_sum(sr);
+  if (lane == 0) out[a.nk_col] = nk;
+  if (lane >= 1 && a.nk_col + lane < a.JP) out[a.nk_col + lane] = 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// predict_proba: r[b][n][k] = 2^(l2[b][k][n] - lse2[b][n]), through a 32 x 32 LDS tile
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void fw_proba_kernel(const float* l2, const float* lse2, float* proba,
+                                                       int64_t N, int K) {
+  __shared__ float tile[32][33];
+  const int b = blockIdx.z;
+  const int64_t n0 = (int64_t)blockIdx.x * 32;
+  const int k0 = blockIdx.y * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int kk = ty; kk < 32; kk += 8) {
+    const int64_t n = n0 + tx;
+    const int k = k0 + kk;
+    float v = 0.f;
+    if (n < N && k < K) v = fast_exp2(l2[((size_t)b * K + k) * N + n] - lse2[(size_t)b * N + n]);
+    tile[kk][tx] = v;
+  }
+  __syncthreads();
+  for (int nn = ty; nn < 32; nn += 8) {
+    const int64_t n = n0 + nn;
+    const int k = k0 + tx;
+    if (n < N && k < K) proba[((size_t)b * N + n) * K + k] = tile[tx][nn];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+
+int64_t fw_lpack_floats(int B, int K, int DP) {
+  const int NT = DP / 32;
+  return ((int64_t)B * K * (NT * (NT + 1) / 2) + 1) * 1024;
+}
+
+int fw_eblocks(int64_t N) { return (int)((N + 32 * kFwWaves - 1) / (32 * kFwWaves)); }
+
+void launch_fw_pack(const FwPackArgs& a, hipStream_t s) {
+  fw_pack_kernel<<<dim3(a.K, a.B), 256, 0, s>>>(a);
+}
+
+template <int DP>
+static void launch_fw_dp(int phase, const FwArgs& a, int slices, hipStream_t s) {
+  if (phase == 0)
+    fw_estep_kernel<DP><<<dim3(fw_eblocks(a.N), a.B), 64 * kFwWaves, 0, s>>>(a);
+  else
+    fw_stats_kernel<DP><<<dim3(slices, (a.K + kFwWaves - 1) / kFwWaves, a.B), 64 * kFwWaves, 0, s>>>(a);
+}
+
+int launch_fw(int dp, int phase, const FwArgs& a, int slices, hipStream_t s) {
+  switch (dp) {
+    case 32: launch_fw_dp<32>(phase, a, slices, s); return 0;
+    case 64: launch_fw_dp<64>(phase, a, slices, s); return 0;
+    case 128: launch_fw_dp<128>(phase, a, slices, s); return 0;
+    default: return -1;
+  }
+}
+
+void launch_fw_proba(const float* l2, const float* lse2, float* proba, int B, int64_t N, int K, hipStream_t s) {
+  fw_proba_kernel<<<dim3((unsigned)((N + 31) / 32), (K + 31) / 32, B), 256, 0, s>>>(l2, lse2, proba, N, K);
+}
+
+}  // namespace gx

@@ -92,6 +92,44 @@ struct CoopArgs {
 int coop_capacity();
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s);
 
+// Full covariance at 16 < D <= 128 (em_full_wide.hip): whitening E-step and
+// weighted-Gram statistics on the fp32 MFMA, DP in {32, 64, 128}.
+struct FwPackArgs {
+  int B, K, D, DP, prelude;
+  float min_weight;
+  const float* means;          // [B][K][D]
+  const float* weights;        // [B][K]
+  const float* linv;           // [B][K][D][D] L^-1 (lower triangular)
+  const float* logdet;         // [B][K]
+  float* lpack;                // fw_lpack_floats(B, K, DP): L^-1 as MFMA A-operand chunks
+  float* lpaug;                // [B][K][DP/32][64] -L^-1 μ (lanes 0..31 of each tile)
+  float4* cconst;              // [B][K] (log2 w - ½ log2(e) (D log 2π + log det), 0, 0, 0)
+};
+struct FwArgs {
+  const float* x;              // [B][N][D] fp32
+  int vec_ok;                  // D == DP and x 16-byte aligned
+  int64_t N;
+  int D, K, B;
+  const float* lpack;
+  const float* lpaug;
+  const float4* cconst;
+  float* l2;                   // [B][K][N] log2 logits (E-step output, statistics input), or null
+  float* lse2;                 // [B][N] log2 row log-normalisers
+  float* scores;               // [B][N] natural-log scores, or null
+  int64_t* labels;             // [B][N] first argmax, or null
+  double* ll_part;             // [B][fw_eblocks(N)] natural-log partial sums, or null
+  float* part_stats;           // [slices][B][K][JP]
+  int JP, nk_col;
+  int64_t rows_per_slice;      // statistics kernel: rows per slice
+};
+int64_t fw_lpack_floats(int B, int K, int DP);
+int fw_eblocks(int64_t N);
+void launch_fw_pack(const FwPackArgs& a, hipStream_t s);
+// phase 0: the E-step over fw_eblocks(N) x B workgroups; 1: the statistics over
+// slices x ceil(K / 4) x B.  Returns -1 for an unsupported dp.
+int launch_fw(int dp, int phase, const FwArgs& a, int slices, hipStream_t s);
+void launch_fw_proba(const float* l2, const float* lse2, float* proba, int B, int64_t N, int K, hipStream_t s);
+
 // Greedy k-means++ seeding (kmeans.hip).  Row sample [B][S][D] fp32; the first
 // centre's row index per batch and T uniform draws per later centre are inputs.
 constexpr int kKppMaxTrials = 16;

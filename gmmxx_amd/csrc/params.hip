@@ -433,7 +433,7 @@ __device__ __forceinline__ int chol_first(const float* C, int D, float (&a)[DP],
 //   P_IJ = Σ_{K>=I} X_KIᵀ X_KJ for I >= J (X is block lower triangular), each
 //     entry i >= j written to both (i, j) and (j, i), so P is exactly symmetric.
 template <int DP>
-__device__ __forceinline__ void chol_inverse(int D, CholLds<DP>& sh, float* Pm, float* logdet) {
+__device__ __forceinline__ void chol_inverse(int D, CholLds<DP>& sh, float* Pm, float* logdet, float* Xm) {
   constexpr int RS = chol_rs<DP>(), NB = DP / 16;
   const int i = threadIdx.x & 63, g = i / 16, li = i % 16;
   float ld = (i < D) ? logf(sh.L[i * RS + i]) : 0.f;
@@ -479,6 +479,10 @@ __device__ __forceinline__ void chol_inverse(int D, CholLds<DP>& sh, float* Pm, 
       for (int v = 0; v < 4; ++v) sh.X[(I0 + 4 * g + v) * RS + J0 + li] = -acc2[v];
       wave_lds_sync();
     }
+  // X itself (D x D; the blocks above the diagonal are never formed in sh.X, so
+  // zeros are written there) for the whitening E-step of the full covariance at D > 16
+  if (Xm)
+    for (int e = i; e < D * D; e += 64) Xm[e] = (e % D <= e / D) ? sh.X[(e / D) * RS + e % D] : 0.f;
 #pragma unroll
   for (int I = 0; I < NB; ++I)
 #pragma unroll
@@ -548,7 +552,7 @@ template <int DP>
 __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_finish_kernel(const float* cov, int D, int M,
                                                                             const int* first_ok, int* level,
                                                                             bool inline_level, const float* lbuf,
-                                                                            float* prec, float* logdet) {
+                                                                            float* prec, float* logdet, float* linv) {
   constexpr int RS = chol_rs<DP>();
   __shared__ __align__(16) CholLds<DP> sh[chol_waves<DP>()];
   const int w = threadIdx.x / 64, i = threadIdx.x & 63;
@@ -569,7 +573,7 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_finish_kernel(cons
     chol_row<DP>(cov + (size_t)m * D * D, D, jitter_of(lv), a);
     chol_blocked<DP>(a, sh[w]);
   }
-  chol_inverse<DP>(D, sh[w], prec + (size_t)m * D * D, logdet + m);
+  chol_inverse<DP>(D, sh[w], prec + (size_t)m * D * D, logdet + m, linv ? linv + (size_t)m * D * D : nullptr);
 }
 
 // Whole batch in one workgroup (M <= chol_waves): factor, batch level through
@@ -577,7 +581,7 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_finish_kernel(cons
 template <int DP>
 __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const float* cov, int D, int M,
                                                                          int* first_ok, int* level, float* prec,
-                                                                         float* logdet) {
+                                                                         float* logdet, float* linv) {
   constexpr int NW = chol_waves<DP>();
   __shared__ __align__(16) CholLds<DP> sh[NW];
   __shared__ int lev[NW];
@@ -602,7 +606,7 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const f
     chol_row<DP>(C, D, jitter_of(lv), a);
     chol_blocked<DP>(a, sh[w]);
   }
-  chol_inverse<DP>(D, sh[w], prec + (size_t)w * D * D, logdet + w);
+  chol_inverse<DP>(D, sh[w], prec + (size_t)w * D * D, logdet + w, linv ? linv + (size_t)w * D * D : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -669,7 +673,7 @@ __global__ __launch_bounds__(kChol128Threads) void chol128_try_kernel(const floa
 __global__ __launch_bounds__(kChol128Threads) void chol128_finish_kernel(const float* cov, int D, int M,
                                                                          const int* first_ok, int* level,
                                                                          bool inline_level, float* prec,
-                                                                         float* logdet) {
+                                                                         float* logdet, float* linv) {
   __shared__ float A[128 * kChol128RS];
   __shared__ float X[128 * kChol128RS];
   __shared__ int lvs;
@@ -702,6 +706,8 @@ __global__ __launch_bounds__(kChol128Threads) void chol128_finish_kernel(const f
     }
   }
   __syncthreads();
+  if (linv)
+    for (int e = t; e < D * D; e += kChol128Threads) linv[(size_t)m * D * D + e] = X[(e / D) * kChol128RS + e % D];
   // P = XᵀX, entries (i >= j) mirrored: the same products in the same order on both sides
   float* P = prec + (size_t)m * D * D;
   for (int e = t; e < D * D; e += kChol128Threads) {
@@ -1067,21 +1073,22 @@ __global__ __launch_bounds__(64 * kTiedWaves) void finalize_tied_kernel(Finalize
 __global__ void finalize_full_kernel(FinalizeArgs a) {
   const int b = blockIdx.y, k = blockIdx.x;
   const int K = a.K, D = a.D, JP = a.JP, DP = a.DP;
-  const int t = threadIdx.x;
-  if (t >= D * D || (a.skip && *a.skip != 0u)) return;
-  const int d = t / D, e = t % D;
+  if (a.skip && *a.skip != 0u) return;
   const size_t bk = (size_t)b * K + k;
   const float* sk = a.stats + bk * JP;
   const float nk = sk[a.nk_col];
   const bool active = nk > a.min_weight;
   const float nk_safe = clamp_lo(nk, a.min_weight);
   const float* mu = a.means + bk * D;
-  const float sxx = sk[DP + full_feature(d < e ? d : e, d < e ? e : d)];
-  const float ade = (sxx - nk * (mu[d] * mu[e])) / nk_safe;
-  const float aed = (sxx - nk * (mu[e] * mu[d])) / nk_safe;
   float* C = a.covs + bk * D * D;
-  const float v = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
-  if (active) C[t] = v;  // inactive components keep their previous covariance
+  for (int t = threadIdx.x; t < D * D; t += blockDim.x) {
+    const int d = t / D, e = t % D;
+    const float sxx = sk[DP + full_sxx(DP, d < e ? d : e, d < e ? e : d)];
+    const float ade = (sxx - nk * (mu[d] * mu[e])) / nk_safe;
+    const float aed = (sxx - nk * (mu[e] * mu[d])) / nk_safe;
+    const float v = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
+    if (active) C[t] = v;  // inactive components keep their previous covariance
+  }
 }
 
 // Unpacks the statistics rows into (N_k, Σ r x, Σ r q(x)) for callers and tests.
@@ -1104,7 +1111,7 @@ __global__ void unpack_stats_kernel(UnpackArgs a) {
   } else if (a.cov == FULL) {
     for (int d = 0; d < D; ++d)
       for (int e = 0; e < D; ++e)
-        a.sum_q[(bk * D + d) * D + e] = sk[DP + full_feature(d < e ? d : e, d < e ? e : d)];
+        a.sum_q[(bk * D + d) * D + e] = sk[DP + full_sxx(DP, d < e ? d : e, d < e ? e : d)];
   }
 }
 
@@ -1130,7 +1137,7 @@ __global__ void pack_stats_kernel(PackArgs a) {
     }
   } else if (a.cov == FULL) {
     for (int d = 0; d < D; ++d)
-      for (int e = d; e < D; ++e) sk[DP + full_feature(d, e)] = a.sum_q[(bk * D + d) * D + e];
+      for (int e = d; e < D; ++e) sk[DP + full_sxx(DP, d, e)] = a.sum_q[(bk * D + d) * D + e];
   }
 }
 
@@ -1221,10 +1228,10 @@ int chol_dp(int D) { return D <= 16 ? 16 : (D <= 32 ? 32 : (D <= 64 ? 64 : 128))
 
 template <int DP>
 static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
-                           float* logdet, hipStream_t s) {
+                           float* logdet, float* linv, hipStream_t s) {
   constexpr int NW = chol_waves<DP>();
   if (M <= NW) {
-    chol_one_kernel<DP><<<1, 64 * NW, 0, s>>>(cov, D, M, first_ok, level, prec, logdet);
+    chol_one_kernel<DP><<<1, 64 * NW, 0, s>>>(cov, D, M, first_ok, level, prec, logdet, linv);
     return;
   }
   const int blocks = (M + NW - 1) / NW;
@@ -1232,23 +1239,24 @@ static void launch_chol_dp(const float* cov, int D, int M, int* first_ok, int* l
   const bool inline_level = M <= kCholLevelInline;
   if (!inline_level) chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
   chol_finish_kernel<DP><<<blocks, 64 * NW, 0, s>>>(cov, D, M, first_ok, level, inline_level, lbuf, prec,
-                                                    logdet);
+                                                    logdet, linv);
 }
 
 void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
-                 float* logdet, hipStream_t s) {
+                 float* logdet, hipStream_t s, float* linv) {
   if (D > 64) {
     if (M <= 0) return;
     chol128_try_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok);
     const bool inline_level = M <= kCholLevelInline;
     if (!inline_level) chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
-    chol128_finish_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok, level, inline_level, prec, logdet);
+    chol128_finish_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok, level, inline_level, prec, logdet,
+                                                        linv);
     return;
   }
   switch (chol_dp(D)) {
-    case 16: launch_chol_dp<16>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
-    case 32: launch_chol_dp<32>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
-    default: launch_chol_dp<64>(cov, D, M, first_ok, level, lbuf, prec, logdet, s); break;
+    case 16: launch_chol_dp<16>(cov, D, M, first_ok, level, lbuf, prec, logdet, linv, s); break;
+    case 32: launch_chol_dp<32>(cov, D, M, first_ok, level, lbuf, prec, logdet, linv, s); break;
+    default: launch_chol_dp<64>(cov, D, M, first_ok, level, lbuf, prec, logdet, linv, s); break;
   }
 }
 

@@ -26,6 +26,8 @@ FAMILIES = [
     ("cholesky-tied", "tied", 1, 9000, 64, 128, torch.float32),        # jitter ladder + tied M-step
     ("cholesky-tied-d100", "tied", 1, 6000, 100, 40, torch.float32),   # one-workgroup factorisation, D > 64
     ("cholesky-full", "full", 4, 6000, 16, 32, torch.float32),         # per-component Cholesky
+    ("whitening-full-d64", "full", 2, 6000, 64, 5, torch.float32),     # full D > 16: whitening E-step, Gram statistics
+    ("whitening-full-d100", "full", 1, 5000, 100, 3, torch.float32),   # DP 128, one-workgroup Cholesky
 ]
 
 

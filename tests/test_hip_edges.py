@@ -40,6 +40,24 @@ def test_few_rows(hip, cov, n):
     assert_labels(labels, x, means, covs, w, cov, 1e-5)
 
 
+@pytest.mark.parametrize("n", [1, 31, 33, 129])
+def test_few_rows_full_whitening(hip, n):
+    """Full covariance at D = 20 (the whitening kernels, DP 32): a partial
+    32-row block, one wave's rows past N, a four-wave workgroup's tail."""
+    print(f"[edges] few rows full D=20 N={n}", flush=True)
+    x, means, covs, w = make_problem("full", 2, max(n, 8), 20, 3, seed=63)
+    x = x[:, :n].contiguous()
+    nk, sx, sq, ll = hip.estep_stats("full", to_dev(x), to_dev(means), to_dev(covs), to_dev(w))
+    e_nk, e_sx, e_sq, e_ll = torch_ref.estep_stats(x, "full", means, covs, w)
+    _close(nk, e_nk)
+    _close(sx, e_sx)
+    _close(sq, e_sq)
+    assert float(ll) == pytest.approx(float(e_ll), rel=1e-5, abs=1e-4)
+    scores, labels = hip.score("full", to_dev(x), to_dev(means), to_dev(covs), to_dev(w))
+    _close(scores, torch_ref.score_samples(x, means, covs, w, "full"), 1e-5)
+    assert_labels(labels, x, means, covs, w, "full", 1e-5)
+
+
 @pytest.mark.parametrize("cov", COVS)
 def test_single_component(hip, cov):
     """K = 1: every responsibility is 1 and the M-step gives the sample moments."""
@@ -152,6 +170,41 @@ def test_estimator_approx_top_k_large_k(hip):
                backend="hip", approx_top_k=6, device=DEV, compute_labels_on_fit=False)
     m2.fit(torch.randn(192, 8, device=DEV))
     assert m2.approximate_em_enabled_ is False and m2.approx_top_k_ is None
+
+
+@pytest.mark.parametrize("d", [40, 100])
+def test_full_jitter_ladder_indefinite_covariance(hip, d):
+    """Full covariance at D > 16 (whitening kernels): one component's covariance
+    is indefinite (eigenvalues in [1e-3, 3e-3] and one of -5e-4), the others are
+    well conditioned on the same scale.  The batch-global ladder takes every
+    component's factorisation to jitter 1e-3 (level 4) in both implementations
+    (torch_fallback.py:316-334); scores, labels and one EM step match the oracle."""
+    print(f"[edges] full jitter ladder D={d}", flush=True)
+    k = 3
+    x, means, _, w = make_problem("full", 1, 6000, d, k, seed=68)
+    x, means = 0.03 * x, 0.03 * means
+    g = torch.Generator().manual_seed(69)
+    covs = []
+    for i in range(k):
+        q, _ = torch.linalg.qr(torch.randn(d, d, generator=g, dtype=torch.float64))
+        lam = 1e-3 * (1.0 + 2.0 * torch.rand(d, generator=g, dtype=torch.float64))
+        if i == 1:
+            lam[0] = -5e-4
+        c = (q * lam) @ q.T
+        covs.append(0.5 * (c + c.T))
+    covs = torch.stack(covs)[None].float()
+    scores, labels = hip.score("full", to_dev(x), to_dev(means), to_dev(covs), to_dev(w))
+    e_sc = torch_ref.score_samples(x, means, covs, w, "full")
+    torch.testing.assert_close(scores.cpu(), e_sc, rtol=1e-5, atol=1e-5 * float(e_sc.abs().mean()))
+    assert_labels(labels, x, means, covs, w, "full")
+    m_d, c_d, w_d = to_dev(means), to_dev(covs), to_dev(w)
+    lb = torch.zeros(1, device=DEV)
+    hip.em_step("full", to_dev(x), m_d, c_d, w_d, lb)
+    e_m, e_c, e_w, e_lb = torch_ref.fit_one_iteration_stats(x, "full", means, covs, w)
+    assert float(lb) == pytest.approx(e_lb, rel=1e-5)
+    _close(m_d, e_m)
+    _close(c_d, e_c)
+    _close(w_d, e_w)
 
 
 @pytest.mark.parametrize("d", [40, 100])

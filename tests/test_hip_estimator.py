@@ -42,6 +42,7 @@ def estimator_init(x_dev, cov, k, seed, reg=1e-6):
     ("diag", 2, 5000, 8, 5),
     ("tied", 1, 5000, 12, 4),
     ("full", 2, 4000, 6, 3),
+    ("full", 1, 6000, 36, 3),    # D > 16: whitening kernels
 ])
 def test_fit_matches_oracle(cov, b, n, d, k):
     x = blobs(b, n, d, k, seed=11)

@@ -51,6 +51,7 @@ CASES = [
     ("diag", 15000, 24, 12, 4096, torch.float32),
     ("tied", 15000, 16, 10, 5000, torch.float32),          # XᵀX streamed once
     ("full", 12000, 8, 6, 3000, torch.float32),
+    ("full", 12000, 48, 4, 5000, torch.float32),          # D > 16: whitening kernels per chunk
 ]
 
 

@@ -174,6 +174,12 @@ CASES = [
     ("tied", 1, 20000, 128, 300, torch.float32),         # D = 128, two component tiles (two passes)
     ("full", 4, 20000, 16, 32, torch.float32),
     ("full", 2, 1000, 3, 5, torch.float32),
+    # full covariance at D > 16: whitening E-step and weighted-Gram statistics
+    ("full", 2, 6001, 24, 6, torch.float32),             # DP 32, padded columns and rows
+    ("full", 1, 8000, 40, 4, torch.float32),             # DP 64, padded
+    ("full", 1, 12000, 64, 6, torch.float32),            # DP 64, vector row loads
+    ("full", 1, 9000, 100, 3, torch.float32),            # DP 128, one-workgroup Cholesky
+    ("full", 1, 12000, 128, 4, torch.float32),           # DP 128
 ]
 
 # Over-parameterised problems (a few rows per component): after one iteration

@@ -69,7 +69,9 @@ def _prob(cov, dtype, b, n, d, k):
     ("tied", torch.float32, 128, True),
     ("tied", torch.float32, 129, False),
     ("full", torch.float32, 16, True),
-    ("full", torch.float32, 17, False),
+    ("full", torch.float32, 17, True),
+    ("full", torch.float32, 128, True),
+    ("full", torch.float32, 129, False),
 ])
 def test_supported_gate(lib, cov, dtype, d, ok):
     assert _hip.supported(cov, dtype, 2, 1000, d, 37) == ok
@@ -172,7 +174,8 @@ def test_engine_dtype_policy():
 
 def test_shape_gate_uses_library():
     assert _dispatch.hip_supported("spherical", (1, 100, 128, 1024), torch.bfloat16)
-    assert not _dispatch.hip_supported("full", (1, 100, 32, 4), torch.float32)
+    assert _dispatch.hip_supported("full", (1, 100, 32, 4), torch.float32)
+    assert not _dispatch.hip_supported("full", (1, 100, 129, 4), torch.float32)
     assert _dispatch.hip_supported("tied", (1, 100, 64), torch.float32)  # K unknown at inference
 
 
