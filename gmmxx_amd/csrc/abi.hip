@@ -251,7 +251,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_flags = take(8);
   q.o_first = take((size_t)q.chol_m * 4 + 4);   // per-matrix first levels, then the global level
   q.o_lbuf = take(q.chol_m ? (size_t)q.chol_m * chol_dp(q.D) * chol_dp(q.D) * 4 : 0);
-  q.o_prec = take((size_t)q.chol_m * q.D * q.D * 4);
+  q.o_prec = take(q.fw ? 0 : (size_t)q.chol_m * q.D * q.D * 4);
   q.o_logdet = take((size_t)q.chol_m * 4);
   q.o_gram = take(q.cov == TIED ? (size_t)q.gram_slices * q.B * q.D * q.D * 4 : 0);
   q.o_lpack = take(q.fw ? (size_t)fw_lpack_floats(q.B, q.K, q.DP) * 4 : 0);
@@ -449,7 +449,8 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
     prec = at<float>(ws, pl.o_prec);
     logdet = at<float>(ws, pl.o_logdet);
     launch_chol(covs, pl.D, pl.chol_m, at<int>(ws, pl.o_first), at<int>(ws, pl.o_first) + pl.chol_m,
-                at<float>(ws, pl.o_lbuf), prec, logdet, s, pl.fw ? at<float>(ws, pl.o_linv) : nullptr);
+                at<float>(ws, pl.o_lbuf), pl.fw ? nullptr : prec, logdet, s,
+                pl.fw ? at<float>(ws, pl.o_linv) : nullptr);
   }
   if (pl.fw) {
     FwPackArgs f{};

@@ -253,6 +253,7 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
   for (int64_t n0 = r0; n0 < r1; n0 += 32) {
     const int64_t nr = n0 + lr;
     const float rv = nr < r1 ? fast_exp2(l2[nr] - lse2[nr]) : 0.f;
+    // (unrolled four k-steps deep: all sixteen measured slower at DP 32 and 64)
 #pragma unroll 4
     for (int st = 0; st < 16; ++st) {
       const int src = 2 * st + h;   // row of this k-step for this lane's half

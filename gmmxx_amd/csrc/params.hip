@@ -483,6 +483,7 @@ __device__ __forceinline__ void chol_inverse(int D, CholLds<DP>& sh, float* Pm, 
   // zeros are written there) for the whitening E-step of the full covariance at D > 16
   if (Xm)
     for (int e = i; e < D * D; e += 64) Xm[e] = (e % D <= e / D) ? sh.X[(e / D) * RS + e % D] : 0.f;
+  if (!Pm) return;   // the caller needs X alone
 #pragma unroll
   for (int I = 0; I < NB; ++I)
 #pragma unroll
@@ -573,7 +574,8 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_finish_kernel(cons
     chol_row<DP>(cov + (size_t)m * D * D, D, jitter_of(lv), a);
     chol_blocked<DP>(a, sh[w]);
   }
-  chol_inverse<DP>(D, sh[w], prec + (size_t)m * D * D, logdet + m, linv ? linv + (size_t)m * D * D : nullptr);
+  chol_inverse<DP>(D, sh[w], prec ? prec + (size_t)m * D * D : nullptr, logdet + m,
+                   linv ? linv + (size_t)m * D * D : nullptr);
 }
 
 // Whole batch in one workgroup (M <= chol_waves): factor, batch level through
@@ -606,18 +608,20 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const f
     chol_row<DP>(C, D, jitter_of(lv), a);
     chol_blocked<DP>(a, sh[w]);
   }
-  chol_inverse<DP>(D, sh[w], prec + (size_t)w * D * D, logdet + w, linv ? linv + (size_t)w * D * D : nullptr);
+  chol_inverse<DP>(D, sh[w], prec ? prec + (size_t)w * D * D : nullptr, logdet + w,
+                   linv ? linv + (size_t)w * D * D : nullptr);
 }
 
 // ---------------------------------------------------------------------------
-// 64 < D <= 128 (tied): one workgroup of kChol128Threads per matrix, the matrix
-// in LDS.  Unblocked right-looking factorisation (column scale, then the
-// trailing update, two barriers per column), the same ladder as above:
-// chol128_try finds each matrix's first factorising level, chol128_finish
-// factorises at the batch level and writes X = L^-1 (one thread per column,
-// forward substitution), P = XᵀX and 2 Σ log L_jj.  A wave per matrix cannot
-// hold a 128-row panel, and these sizes are rare (tied covariance has one
-// matrix per problem), so simplicity wins over the blocked MFMA path.
+// 64 < D <= 128 (tied, full): one workgroup of kChol128Threads per matrix, the
+// matrix in LDS.  Unblocked right-looking factorisation (column scale, then the
+// trailing update from a copy of the scaled column, two barriers per column),
+// the same ladder as above: chol128_try finds each matrix's first factorising
+// level and keeps that factor, chol128_finish takes it when the batch level is
+// the matrix's own (else factorises at the batch level) and writes X = L^-1
+// (one thread per column, forward substitution), P = XᵀX and 2 Σ log L_jj.  A
+// wave per matrix cannot hold a 128-row panel, and these sizes are rare, so
+// simplicity wins over the blocked MFMA path.
 // ---------------------------------------------------------------------------
 
 constexpr int kChol128Threads = 256;
@@ -626,6 +630,7 @@ constexpr int kChol128RS = 129;   // row stride (floats)
 // A = sym(C) + jitter·I (lower triangle) into LDS, then factorised in place;
 // returns false when a pivot is not positive (or not finite).
 __device__ bool chol128_factor(const float* C, int D, float jitter, float* A) {
+  __shared__ float colk[128];
   const int t = threadIdx.x;
   for (int e = t; e < D * D; e += kChol128Threads) {
     const int r = e / D, c = e % D;
@@ -640,19 +645,27 @@ __device__ bool chol128_factor(const float* C, int D, float jitter, float* A) {
     const float inv = 1.f / lkk;
     __syncthreads();                           // every thread has read the pivot
     if (t == 0) A[k * kChol128RS + k] = lkk;
-    for (int i = k + 1 + t; i < D; i += kChol128Threads) A[i * kChol128RS + k] *= inv;
+    for (int i = k + 1 + t; i < D; i += kChol128Threads) {
+      const float v = A[i * kChol128RS + k] * inv;
+      A[i * kChol128RS + k] = v;
+      colk[i] = v;
+    }
     __syncthreads();
-    // trailing update A[i][j] -= L[i][k] L[j][k], k < j <= i: row k + 1 + t/2, columns of parity t & 1
+    // trailing update A[i][j] -= L[i][k] L[j][k], k < j <= i: row k + 1 + t/2, columns of
+    // parity t & 1; the column is read from colk, a separate array, so the loads of one
+    // row's updates need not wait for its stores
     for (int i = k + 1 + (t >> 1); i < D; i += kChol128Threads / 2) {
-      const float lik = A[i * kChol128RS + k];
-      for (int j = k + 1 + (t & 1); j <= i; j += 2) A[i * kChol128RS + j] = fmaf(-lik, A[j * kChol128RS + k], A[i * kChol128RS + j]);
+      const float lik = colk[i];
+      for (int j = k + 1 + (t & 1); j <= i; j += 2) A[i * kChol128RS + j] = fmaf(-lik, colk[j], A[i * kChol128RS + j]);
     }
     __syncthreads();
   }
   return true;
 }
 
-__global__ __launch_bounds__(kChol128Threads) void chol128_try_kernel(const float* cov, int D, int M, int* first_ok) {
+// lbuf: M x 128 x 128, the factor at the matrix's first level (lower triangle).
+__global__ __launch_bounds__(kChol128Threads) void chol128_try_kernel(const float* cov, int D, int M, int* first_ok,
+                                                                      float* lbuf) {
   __shared__ float A[128 * kChol128RS];
   const int m = blockIdx.x;
   if (m >= M) return;
@@ -666,14 +679,19 @@ __global__ __launch_bounds__(kChol128Threads) void chol128_try_kernel(const floa
     __syncthreads();   // the failed attempt's readers are done before the next fill
   }
   if (threadIdx.x == 0) first_ok[m] = first;
+  if (first < 7)
+    for (int e = threadIdx.x; e < D * D; e += kChol128Threads) {
+      const int r = e / D, c = e % D;
+      if (c <= r) lbuf[((size_t)m * 128 + r) * 128 + c] = A[r * kChol128RS + c];
+    }
 }
 
 // inline_level: the batch level is the maximum of first_ok over the batch
 // (M <= kCholLevelInline), written to *level by block 0; else read from *level.
 __global__ __launch_bounds__(kChol128Threads) void chol128_finish_kernel(const float* cov, int D, int M,
                                                                          const int* first_ok, int* level,
-                                                                         bool inline_level, float* prec,
-                                                                         float* logdet, float* linv) {
+                                                                         bool inline_level, const float* lbuf,
+                                                                         float* prec, float* logdet, float* linv) {
   __shared__ float A[128 * kChol128RS];
   __shared__ float X[128 * kChol128RS];
   __shared__ int lvs;
@@ -692,8 +710,16 @@ __global__ __launch_bounds__(kChol128Threads) void chol128_finish_kernel(const f
   }
   __syncthreads();
   const int lv = lvs;
-  // a matrix that factorises at no level keeps the partial factor, as the reference does
-  (void)chol128_factor(cov + (size_t)m * D * D, D, jitter_of(lv), A);
+  if (first_ok[m] == lv) {
+    // the try kernel's factor at this level
+    for (int e = t; e < D * D; e += kChol128Threads) {
+      const int r = e / D, c = e % D;
+      if (c <= r) A[r * kChol128RS + c] = lbuf[((size_t)m * 128 + r) * 128 + c];
+    }
+  } else {
+    // a matrix that factorises at no level keeps the partial factor, as the reference does
+    (void)chol128_factor(cov + (size_t)m * D * D, D, jitter_of(lv), A);
+  }
   __syncthreads();
   // X = L^-1, thread c owns column c
   if (t < D) {
@@ -708,9 +734,10 @@ __global__ __launch_bounds__(kChol128Threads) void chol128_finish_kernel(const f
   __syncthreads();
   if (linv)
     for (int e = t; e < D * D; e += kChol128Threads) linv[(size_t)m * D * D + e] = X[(e / D) * kChol128RS + e % D];
-  // P = XᵀX, entries (i >= j) mirrored: the same products in the same order on both sides
-  float* P = prec + (size_t)m * D * D;
-  for (int e = t; e < D * D; e += kChol128Threads) {
+  // P = XᵀX, entries (i >= j) mirrored: the same products in the same order on
+  // both sides (skipped when the caller needs X alone)
+  float* P = prec ? prec + (size_t)m * D * D : nullptr;
+  for (int e = t; P && e < D * D; e += kChol128Threads) {
     const int i = e / D, j = e % D;
     if (i < j) continue;
     float acc = 0.f;
@@ -1246,11 +1273,11 @@ void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, floa
                  float* logdet, hipStream_t s, float* linv) {
   if (D > 64) {
     if (M <= 0) return;
-    chol128_try_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok);
+    chol128_try_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok, lbuf);
     const bool inline_level = M <= kCholLevelInline;
     if (!inline_level) chol_level_kernel<<<1, 256, 0, s>>>(first_ok, M, level);
-    chol128_finish_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok, level, inline_level, prec, logdet,
-                                                        linv);
+    chol128_finish_kernel<<<M, kChol128Threads, 0, s>>>(cov, D, M, first_ok, level, inline_level, lbuf, prec,
+                                                        logdet, linv);
     return;
   }
   switch (chol_dp(D)) {

@@ -85,7 +85,7 @@ void launch_prep(const PrepArgs& a, hipStream_t s);
 int chol_dp(int D);
 // first_ok: M per-matrix first levels, then the batch level (written by every path).
 // linv (optional, M x D x D): X = L^-1 of the factor at the batch level, zeros
-// above the diagonal.
+// above the diagonal; prec may then be null (X alone).
 void launch_chol(const float* cov, int D, int M, int* first_ok, int* level, float* lbuf, float* prec,
                  float* logdet, hipStream_t s, float* linv = nullptr);
 void launch_rowquad(const float* x, int B, int64_t N, int D, const float* prec, float* rowq, hipStream_t s);
