@@ -19,7 +19,8 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libgmmxx_hip.so")
-SOURCES = ("em_tile.hip", "em_sph_bf16.hip", "em_fused.hip", "em_coop.hip", "em_full_wide.hip", "params.hip",
+SOURCES = ("em_tile.hip", "em_sph_bf16.hip", "em_fused.hip", "em_coop.hip", "em_full_wide.hip", "em_full_infer.hip",
+           "params.hip",
            "kmeans.hip", "abi.hip")
 ARCH = os.environ.get("GMMXX_HIP_ARCH", "gfx950")
 

@@ -68,6 +68,9 @@ struct Plan {
   int fw_eblk = 0, fw_slices = 0;
   int64_t fw_rows = 0;
   size_t o_lpack = 0, o_lpaug = 0, o_l2w = 0, o_linv = 0;
+  // full covariance at D <= 16, K <= 32: whitening inference (score, labels, proba)
+  bool w16 = false;
+  size_t o_w16parts = 0, o_w16b = 0, o_w16c = 0;
   size_t o_rowaux = 0, o_pstats = 0, o_stats = 0, o_ll = 0, o_first = 0, o_lbuf = 0, o_prec = 0, o_logdet = 0,
          o_gram = 0, total = 0;
 };
@@ -107,6 +110,11 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   // Full covariance beyond D = 16: the whitening kernels of em_full_wide.hip
   // (the tile kernel's augmented features are built for D = 16).
   q.fw = q.cov == FULL && q.DP > 16;
+  // Full covariance at D <= 16 with every component in one wave: inference by
+  // whitening (em_full_infer.hip) instead of the tile kernel's 136 products per
+  // row.  GMMXX_HIP_NO_WHITEN=1 keeps the tile kernels (the tests compare both).
+  const char* no_whiten = getenv("GMMXX_HIP_NO_WHITEN");
+  q.w16 = q.cov == FULL && q.DP == 16 && q.K <= kFull16MaxK && !(no_whiten && no_whiten[0] == '1');
   const bool sph_bf = q.bf && q.cov == SPH;          // dedicated kernel, DP >= 32
   if (sph_bf) q.DP = std::max(q.DP, 32);
   const int S = q.DP * (q.DP + 1) / 2;
@@ -257,7 +265,10 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_lpack = take(q.fw ? (size_t)fw_lpack_floats(q.B, q.K, q.DP) * 4 : 0);
   q.o_lpaug = take(q.fw ? BK * (q.DP / 32) * 64 * 4 : 0);
   q.o_l2w = take(q.fw ? BK * (size_t)q.N * 4 : 0);
-  q.o_linv = take(q.fw ? BK * q.D * q.D * 4 : 0);
+  q.o_linv = take((q.fw || q.w16) ? BK * q.D * q.D * 4 : 0);
+  q.o_w16parts = take(q.w16 ? BK * 3 * 512 * 2 : 0);   // three 1 KB MFMA operands per component
+  q.o_w16b = take(q.w16 ? BK * 16 * 4 : 0);
+  q.o_w16c = take(q.w16 ? BK * 4 : 0);
   q.total = off;
   return GMMXX_OK;
 }
@@ -425,6 +436,34 @@ FwArgs fw_args(const Plan& pl, const void* x, void* ws) {
   a.rows_per_slice = pl.fw_rows;
   return a;
 }
+// Full covariance at D <= 16, K <= 32, inference: Cholesky (L^-1 and log det at the
+// batch jitter level), operand packing, then one pass for scores / labels / proba.
+int run_w16(const Plan& pl, const void* x, const float* means, const float* covs, const float* weights, void* ws,
+            float* scores, int64_t* labels, float* proba, hipStream_t s) {
+  launch_chol(covs, pl.D, pl.chol_m, at<int>(ws, pl.o_first), at<int>(ws, pl.o_first) + pl.chol_m,
+              at<float>(ws, pl.o_lbuf), nullptr, at<float>(ws, pl.o_logdet), s, at<float>(ws, pl.o_linv));
+  Full16Args a{};
+  a.x = reinterpret_cast<const float*>(x);
+  a.vec_ok = pl.D == 16 && (uintptr_t)x % 16 == 0;
+  a.N = pl.N;
+  a.D = pl.D;
+  a.K = pl.K;
+  a.B = pl.B;
+  a.linv = at<float>(ws, pl.o_linv);
+  a.means = means;
+  a.weights = weights;
+  a.logdet = at<float>(ws, pl.o_logdet);
+  a.lparts = at<void>(ws, pl.o_w16parts);
+  a.bneg = at<float>(ws, pl.o_w16b);
+  a.c2 = at<float>(ws, pl.o_w16c);
+  a.scores = scores;
+  a.labels = labels;
+  a.proba = proba;
+  launch_full16_pack(a, s);
+  launch_full16_infer(a, s);
+  return check_hip("full-covariance inference");
+}
+
 int run_fw(const Plan& pl, int phase, const FwArgs& a, hipStream_t s) {
   if (launch_fw(pl.DP, phase, a, pl.fw_slices, s) != 0) return fail(GMMXX_ERR_UNSUPPORTED, "no full-covariance kernel for this D");
   return check_hip(phase == 0 ? "full-covariance E-step" : "full-covariance statistics");
@@ -872,7 +911,8 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   if (top_k < 1 || top_k >= pl.K)
     return fail(GMMXX_ERR_INVALID_ARGUMENT, "top_k must be in [1, K-1] (top_k >= K is exact EM)");
-  if (pl.fw) return fail(GMMXX_ERR_UNSUPPORTED, "approximate top-k EM is not available for full covariance at D > 16");
+  if (pl.fw && top_k != 1)
+    return fail(GMMXX_ERR_UNSUPPORTED, "approximate top-k EM with top_k > 1 is not available for full covariance at D > 16");
   const hipStream_t s = (hipStream_t)stream;
   // Parameters with the iteration prelude; tied rows get xᵀPx, so the logits
   // (and the log-normalisers) are complete.
@@ -881,7 +921,18 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   // that the log-normaliser pass stores.
   float* thr = at<float>(ws, tl.o_thr);
   int* thri = at<int>(ws, tl.o_thri);
-  if (top_k == 1) {
+  if (pl.fw) {
+    // hard assignment: first argmax per row, then the one-hot statistics
+    FwArgs a = fw_args(pl, x, ws);
+    a.l2 = nullptr;
+    a.hard = 1;
+    a.hard_idx = thri;
+    a.lse2 = thr;
+    if ((rc = run_fw(pl, 0, a, s)) || (rc = run_fw(pl, 1, a, s))) return rc;
+    const LlFold ll = ll_fold(pl, ws, ll_parts(pl), 1.0, ll_sum);
+    launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
+                         at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl), &ll);
+  } else if (top_k == 1) {
     // Hard assignment: the first-argmax pass gives each row's maximum (the
     // log-normaliser of a single component) and its index; the statistics pass
     // then gives that component r = 1 by index, no logits stored.
@@ -988,6 +1039,7 @@ int gmmxx_hip_score(const gmmxx_problem* p, const void* x, const float* means, c
   if (rc) return rc;
   if (!means || !covs || !weights) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL parameter buffer");
   const hipStream_t s = (hipStream_t)stream;
+  if (pl.w16) return run_w16(pl, x, means, covs, weights, ws, scores, labels, nullptr, s);
   if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
   if (pl.fw) {
     FwArgs a = fw_args(pl, x, ws);
@@ -1009,6 +1061,7 @@ int gmmxx_hip_predict_proba_score(const gmmxx_problem* p, const void* x, const f
   if (!means || !covs || !weights) return fail(GMMXX_ERR_INVALID_ARGUMENT, "NULL parameter buffer");
   if (!proba && !scores) return fail(GMMXX_ERR_INVALID_ARGUMENT, "proba and scores are both NULL");
   const hipStream_t s = (hipStream_t)stream;
+  if (pl.w16) return run_w16(pl, x, means, covs, weights, ws, scores, nullptr, proba, s);
   if ((rc = prepare(pl, x, means, covs, weights, 0.0, 1e-8, 0, ws, s))) return rc;
   if (pl.fw) {
     FwArgs a = fw_args(pl, x, ws);

@@ -201,10 +201,11 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_estep_kernel(FwArgs a) {
     }
     if (a.l2 && h == 0 && valid) a.l2[bk * N + n] = l2;
   }
-  const float lse = m + __log2f(s);
+  const float lse = a.hard ? best : m + __log2f(s);
   double ll = 0.0;
   if (h == 0 && valid) {
     a.lse2[(size_t)b * N + n] = lse;
+    if (a.hard) a.hard_idx[(size_t)b * N + n] = bidx;
     if (a.scores) a.scores[(size_t)b * N + n] = lse * kLn2;
     if (a.labels) a.labels[(size_t)b * N + n] = bidx;
     ll = (double)lse * (double)kLn2;
@@ -239,8 +240,9 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
   const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_slice;
   const int64_t r1 = (r0 + a.rows_per_slice < N) ? r0 + a.rows_per_slice : N;
   const float* xb = a.x + (size_t)b * N * D;
-  const float* l2 = a.l2 + bk * N;
+  const float* l2 = a.l2 + bk * N;   // (not read in hard mode)
   const float* lse2 = a.lse2 + (size_t)b * N;
+  const int* hidx = a.hard_idx + (size_t)b * N;
 
   f32x16 acc[NTT];
 #pragma unroll
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
 
   for (int64_t n0 = r0; n0 < r1; n0 += 32) {
     const int64_t nr = n0 + lr;
-    const float rv = nr < r1 ? fast_exp2(l2[nr] - lse2[nr]) : 0.f;
+    const float rv = nr >= r1 ? 0.f : (a.hard ? (hidx[nr] == k ? 1.f : 0.f) : fast_exp2(l2[nr] - lse2[nr]));
     // (unrolled four k-steps deep: all sixteen measured slower at DP 32 and 64)
 #pragma unroll 4
     for (int st = 0; st < 16; ++st) {

@@ -121,6 +121,11 @@ struct FwArgs {
   float* part_stats;           // [slices][B][K][JP]
   int JP, nk_col;
   int64_t rows_per_slice;      // statistics kernel: rows per slice
+  // Hard assignment (approximate top-k EM with k = 1): the E-step writes each
+  // row's first argmax to hard_idx and its maximum as the log-normaliser; the
+  // statistics take r = 1 for that component, 0 elsewhere (no logits stored).
+  int hard;
+  int* hard_idx;               // [B][N]
 };
 int64_t fw_lpack_floats(int B, int K, int DP);
 int fw_eblocks(int64_t N);
@@ -129,6 +134,29 @@ void launch_fw_pack(const FwPackArgs& a, hipStream_t s);
 // slices x ceil(K / 4) x B.  Returns -1 for an unsupported dp.
 int launch_fw(int dp, int phase, const FwArgs& a, int slices, hipStream_t s);
 void launch_fw_proba(const float* l2, const float* lse2, float* proba, int B, int64_t N, int K, hipStream_t s);
+
+// Full-covariance inference at D <= 16, K <= 32 (em_full_infer.hip): whitening
+// with split bf16 operands, every component of a row in one wave.
+constexpr int kFull16MaxK = 32;
+struct Full16Args {
+  const float* x;              // [B][N][D] fp32
+  int vec_ok;                  // D == 16 and x 16-byte aligned
+  int64_t N;
+  int D, K, B;
+  const float* linv;           // pack inputs: [B][K][D][D] L^-1, means, weights (as given), log det
+  const float* means;
+  const float* weights;
+  const float* logdet;
+  void* lparts;                // [B][K][3][16][16] bf16 parts of L^-1
+  float* bneg;                 // [B][K][16] -L^-1 μ
+  float* c2;                   // [B][K] log2 w - ½ log2(e) (D log 2π + log det)
+  float* scores;               // [B][N] natural-log scores, or null
+  float* lse2;                 // [B][N] log2 log-normalisers, or null
+  int64_t* labels;             // [B][N] first argmax, or null
+  float* proba;                // [B][N][K] responsibilities, or null
+};
+void launch_full16_pack(const Full16Args& a, hipStream_t s);
+void launch_full16_infer(const Full16Args& a, hipStream_t s);
 
 // Greedy k-means++ seeding (kmeans.hip).  Row sample [B][S][D] fp32; the first
 // centre's row index per batch and T uniform draws per later centre are inputs.

@@ -408,3 +408,30 @@ def test_one_tile_single_pass_matches_two_pass(hip, monkeypatch, cov, b, n, d, k
     for a, e in zip(s1, s2):
         if e is not None:
             torch.testing.assert_close(a, e, rtol=1e-5, atol=1e-5 * float(e.abs().max()))
+
+
+@pytest.mark.parametrize("b,n,d,k", [(3, 6001, 16, 32), (2, 5000, 11, 7), (1, 3000, 16, 1)])
+def test_full_whitening_inference_matches_tile_kernels(hip, monkeypatch, b, n, d, k):
+    """Full covariance at D <= 16, K <= 32: scores, labels and responsibilities by
+    whitening (the default) and by the tile kernels' augmented products
+    (GMMXX_HIP_NO_WHITEN=1) agree to the fp32 bars, and both match the oracle."""
+    print(f"[whiten-infer] B={b} N={n} D={d} K={k}", flush=True)
+    x, means, covs, w = make_problem("full", b, n, d, k, seed=23)
+    xd = to_dev(x)
+    out = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("GMMXX_HIP_NO_WHITEN", mode)
+        scores, labels = hip.score("full", xd, to_dev(means), to_dev(covs), to_dev(w))
+        proba, scores2 = hip.predict_proba_score("full", xd, to_dev(means), to_dev(covs), to_dev(w))
+        torch.cuda.synchronize()
+        out[mode] = (scores.cpu(), labels.cpu(), proba.cpu(), scores2.cpu())
+    e_scores = torch_ref.score_samples(x, means, covs, w, "full")
+    e_proba = torch_ref.predict_proba(x, means, covs, w, "full")
+    for mode, (scores, labels, proba, scores2) in out.items():
+        torch.testing.assert_close(scores, e_scores, rtol=1e-5, atol=1e-5 * float(e_scores.abs().mean()))
+        torch.testing.assert_close(scores2, scores, rtol=0, atol=0)
+        torch.testing.assert_close(proba, e_proba, rtol=0, atol=2e-4)
+        torch.testing.assert_close(proba.sum(-1), torch.ones(b, n), rtol=0, atol=1e-4)
+        assert_labels(labels, x, means, covs, w, "full")
+    torch.testing.assert_close(out["0"][0], out["1"][0], rtol=1e-5, atol=1e-5 * float(e_scores.abs().mean()))
+    torch.testing.assert_close(out["0"][2], out["1"][2], rtol=0, atol=2e-4)
