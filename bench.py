@@ -51,7 +51,7 @@ sys.path.insert(0, ROOT)
 # bf16 MFMAs on three-way bf16 splits of both operands, so their algorithmic
 # fp32 FLOPs top out at the bf16 peak / 6.
 PEAK = {"bf16": 2516.6, "fp32": 157.3, "fp32x3": 2516.6 / 6.0, "hbm": 8000.0}
-PEAK_BASIS = {"bf16": "dense bf16 MFMA peak 2516.6 TFLOP/s",
+PEAK_BASIS = {"bf16": "dense bf16 MFMA peak 2516.6 TFLOP/s", "fp32": "dense fp32 MFMA peak 157.3 TFLOP/s",
               "fp32x3": "dense bf16 MFMA peak / 6 = 419.4 TFLOP/s (six bf16 MFMAs per fp32-accurate product)",
               "hbm": "HBM3E 8 TB/s"}
 METRIC = "EM iter/s + % bf16 MFMA peak, spherical bf16 N=4M D=128 K=1024"
@@ -70,11 +70,16 @@ CONFIGS = {
                desc="full fp32 B=16 N=262144 D=16 K=32, 10 iterations + predict_proba + score_samples"),
     "c1l": dict(cov="spherical", B=1, N=1 << 24, D=32, K=64, dtype="bf16", iters=20, seed=0, bound="hbm",
                 desc="spherical bf16 N=16777216 D=32 K=64 (C1 recipe, large N), 20 iterations"),
+    # Supplementary (not in the default run, `--only c5w`): full covariance beyond
+    # D = 16 on the whitening kernels (fp32 MFMA), C5's recipe at D = 64, one problem.
+    "c5w": dict(cov="full", B=1, N=262_144, D=64, K=32, dtype="fp32", iters=10, seed=4, bound="fp32",
+                desc="full fp32 B=1 N=262144 D=64 K=32 (C5 recipe), 10 iterations"),
 }
+DEFAULT_CONFIGS = ("c1", "c2", "c3", "c4", "c5", "c1l")
 # CPU-baseline samples: rows per batch and oracle iterations, about 10 s of CPU
 # work for the headline (C2) and 1-4 s for the others on the GPU box's 16 cores.
 CPU_SAMPLE = {"c1": (100_000, 20), "c2": (524_288, 2), "c3": (524_288, 2), "c4": (524_288, 2),
-              "c5": (65_536, 2), "c1l": (4_194_304, 2)}
+              "c5": (65_536, 2), "c1l": (4_194_304, 2), "c5w": (32_768, 2)}
 
 
 def flops(cfg):
@@ -196,7 +201,7 @@ def make_data(name, device, n=None):
             x[0, s:e] = centers[lab[s:e]] + z @ chol.T
         means0 = _distinct_rows(x, k, g)
         covs0 = _global_cov(x)
-    elif name == "c5":
+    elif name in ("c5", "c5w"):
         # per problem and component L lower-triangular ~ N(0, 0.5²), Σ = LLᵀ + 0.05I;
         # centres ~ U[-6, 6]^D; Dirichlet(2) weights; means = K distinct rows per
         # problem, the problem's global covariance for every component, weights 1/K.
@@ -246,6 +251,8 @@ def single_pass(cfg):
         if cfg["D"] == 128 and 256 < cfg["K"] <= 1024 and os.environ.get("GMMXX_HIP_NO_COOP") != "1":
             return "sph_bf16_coop_kernel"
         return None
+    if cfg["cov"] == "full" and cfg["D"] > 16:
+        return None   # whitening E-step, then the statistics kernel
     # fp32 x: one tile pass when a workgroup (8 waves of CW components) holds all K;
     # with 2..4 such component tiles (spherical, tied, diag at D <= 64) the tiles
     # exchange row partials in one cooperative pass
@@ -262,6 +269,8 @@ def single_pass(cfg):
 
 def kernel_label(cfg, phase):
     """Name of the kernel that runs in `phase` for this config (see gmmxx_amd/csrc)."""
+    if cfg["cov"] == "full" and cfg["D"] > 16:
+        return "fw_estep_kernel" if phase == "lse_tile" else "fw_stats_kernel"
     one = single_pass(cfg)
     if one:
         return f"{one} (single pass)"
@@ -499,7 +508,7 @@ def main():
     from gmmxx_amd import _hip
     _hip.require_hip()
     dev = torch.device("cuda:0")
-    names = args.only.split(",") if args.only else list(CONFIGS)
+    names = args.only.split(",") if args.only else list(DEFAULT_CONFIGS)
     for nm in names:
         if nm not in CONFIGS:
             sys.exit(f"unknown config {nm!r}; choose from {sorted(CONFIGS)}")

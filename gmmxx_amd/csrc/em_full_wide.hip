@@ -171,7 +171,9 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_estep_kernel(FwArgs a) {
     float q = 0.f;
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
-      f32x16 acc = f32x16{};
+      // two accumulators (even and odd k-steps), so consecutive MFMAs do not
+      // depend on each other
+      f32x16 acc = f32x16{}, acc2 = f32x16{};
 #pragma unroll
       for (int c = 0; c <= tt; ++c) {
         f32x4 cur[4];
@@ -181,11 +183,17 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_estep_kernel(FwArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) nx[r] = *reinterpret_cast<const f32x4*>(lp + 4 * r);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) acc = mfma32f(cur[u / 4][u % 4], xr[c][u], acc);
+        for (int u = 0; u < 16; u += 2) {
+          acc = mfma32f(cur[u / 4][u % 4], xr[c][u], acc);
+          acc2 = mfma32f(cur[u / 4][u % 4 + 1], xr[c][u + 1], acc2);
+        }
       }
-      acc = mfma32f(augv[tt], one, acc);
+      acc2 = mfma32f(augv[tt], one, acc2);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) q = fmaf(acc[v], acc[v], q);
+      for (int v = 0; v < 16; ++v) {
+        const float y = acc[v] + acc2[v];
+        q = fmaf(y, y, q);
+      }
     }
     q = half_sum(q);
     const float l2 = a.cconst[bk].x - 0.5f * kLog2e * q;
@@ -255,18 +263,19 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
   for (int64_t n0 = r0; n0 < r1; n0 += 32) {
     const int64_t nr = n0 + lr;
     const float rv = nr >= r1 ? 0.f : (a.hard ? (hidx[nr] == k ? 1.f : 0.f) : fast_exp2(l2[nr] - lse2[nr]));
+    const float* xblk = xb + (size_t)n0 * D;           // the block's rows, 32-bit offsets below
+    const int nrows = (int)((r1 - n0) < 32 ? (r1 - n0) : 32);
     // (unrolled four k-steps deep: all sixteen measured slower at DP 32 and 64)
 #pragma unroll 4
     for (int st = 0; st < 16; ++st) {
       const int src = 2 * st + h;   // row of this k-step for this lane's half
       const float r = __shfl(rv, src);
-      const int64_t n = n0 + src;
-      const bool rowok = n < r1;
+      const bool rowok = src < nrows;
       float xv[NT], z[NT];
 #pragma unroll
       for (int c = 0; c < NT; ++c) {
         const int col = 32 * c + lr;
-        xv[c] = (rowok && col < D) ? xb[(size_t)n * D + col] : 0.f;
+        xv[c] = (rowok && col < D) ? xblk[src * D + col] : 0.f;
         z[c] = r * xv[c];
         sx[c] += z[c];
       }
