@@ -264,11 +264,12 @@ __global__ __launch_bounds__(64 * kWaves) void full16_infer_kernel(Full16Args a)
     if (a.proba) {
       const float inv = 1.f / s;
       float* pr = a.proba + ((size_t)b * N + n) * K + g * KQ;
-      if constexpr (KQ == 8) {
-        // K = 32: the group's eight components are a 32-byte aligned run
+      if (KQ == 8 && K == 32) {
+        // the group's eight components are a 32-byte aligned run of the row
         *reinterpret_cast<f32x4*>(pr) = f32x4{e[0] * inv, e[1] * inv, e[2] * inv, e[3] * inv};
         *reinterpret_cast<f32x4*>(pr + 4) = f32x4{e[4] * inv, e[5] * inv, e[6] * inv, e[7] * inv};
       } else {
+        // (K < 4·KQ: the last group's run stops at K)
 #pragma unroll
         for (int j = 0; j < KQ; ++j)
           if (g * KQ + j < K) pr[j] = e[j] * inv;

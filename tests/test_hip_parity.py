@@ -410,7 +410,7 @@ def test_one_tile_single_pass_matches_two_pass(hip, monkeypatch, cov, b, n, d, k
             torch.testing.assert_close(a, e, rtol=1e-5, atol=1e-5 * float(e.abs().max()))
 
 
-@pytest.mark.parametrize("b,n,d,k", [(3, 6001, 16, 32), (2, 5000, 11, 7), (1, 3000, 16, 1)])
+@pytest.mark.parametrize("b,n,d,k", [(3, 6001, 16, 32), (2, 5000, 11, 7), (1, 3000, 16, 1), (2, 4099, 16, 30)])
 def test_full_whitening_inference_matches_tile_kernels(hip, monkeypatch, b, n, d, k):
     """Full covariance at D <= 16, K <= 32: scores, labels and responsibilities by
     whitening (the default) and by the tile kernels' augmented products
