@@ -911,8 +911,6 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   if (!(min_weight > 0.0)) return fail(GMMXX_ERR_INVALID_ARGUMENT, "min_weight must be positive");
   if (top_k < 1 || top_k >= pl.K)
     return fail(GMMXX_ERR_INVALID_ARGUMENT, "top_k must be in [1, K-1] (top_k >= K is exact EM)");
-  if (pl.fw && top_k != 1)
-    return fail(GMMXX_ERR_UNSUPPORTED, "approximate top-k EM with top_k > 1 is not available for full covariance at D > 16");
   const hipStream_t s = (hipStream_t)stream;
   // Parameters with the iteration prelude; tied rows get xᵀPx, so the logits
   // (and the log-normalisers) are complete.
@@ -921,7 +919,7 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
   // that the log-normaliser pass stores.
   float* thr = at<float>(ws, tl.o_thr);
   int* thri = at<int>(ws, tl.o_thri);
-  if (pl.fw) {
+  if (pl.fw && top_k == 1) {
     // hard assignment: first argmax per row, then the one-hot statistics
     FwArgs a = fw_args(pl, x, ws);
     a.l2 = nullptr;
@@ -932,6 +930,24 @@ int gmmxx_hip_estep_stats_topk(const gmmxx_problem* p, const void* x, const floa
     const LlFold ll = ll_fold(pl, ws, ll_parts(pl), 1.0, ll_sum);
     launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
                          at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl), &ll);
+  } else if (pl.fw) {
+    // the E-step's (B, K, N) log2 logits, transposed to (B, N, K) for the per-row
+    // top-k selection (threshold, index, top-k log-normaliser), then the statistics
+    // over each row's kept components
+    FwArgs a = fw_args(pl, x, ws);
+    a.ll_part = nullptr;
+    if ((rc = run_fw(pl, 0, a, s))) return rc;
+    float* logits = at<float>(ws, tl.o_logits);
+    launch_fw_proba(a.l2, a.lse2, logits, pl.B, pl.N, pl.K, s, /*raw=*/true);
+    double* tll = at<double>(ws, tl.o_ll);
+    const int sel_blocks = topk_select_blocks(pl.N);
+    launch_topk_select(logits, pl.B, pl.N, pl.K, top_k, a.lse2, thr, thri, tll, sel_blocks, s);
+    a.thr2 = thr;
+    a.thr_idx = thri;
+    if ((rc = run_fw(pl, 1, a, s))) return rc;
+    launch_reduce_slices(at<float>(ws, pl.o_pstats), stat_slices(pl), (int64_t)pl.B * pl.K * pl.JP,
+                         at<float>(ws, pl.o_stats), s, red_tmp(pl, ws), red_tmp_floats(pl));
+    launch_ll_reduce(tll, pl.B * sel_blocks, 1.0, ll_sum, s);
   } else if (top_k == 1) {
     // Hard assignment: the first-argmax pass gives each row's maximum (the
     // log-normaliser of a single component) and its index; the statistics pass

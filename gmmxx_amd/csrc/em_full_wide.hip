@@ -26,7 +26,8 @@
 //                    the lower tiles of (r ⊙ X)ᵀ X over 2-row k-steps, Σ r x and
 //                    Σ r beside it on the VALU, r = 2^(l2 - lse2) from the
 //                    E-step's buffers;
-//   fw_proba_kernel  predict_proba: r = 2^(l2 - lse2) transposed to (B, N, K).
+//   fw_proba_kernel  predict_proba: r = 2^(l2 - lse2) transposed to (B, N, K) (or
+//                    the logits themselves, for the top-k selection).
 //
 // 32x32x2 fp32 MFMA operand layout: lane l supplies A[i = l % 32][k = l / 32]
 // and B[k = l / 32][j = l % 32]; accumulator register v of lane l holds
@@ -248,9 +249,11 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
   const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_slice;
   const int64_t r1 = (r0 + a.rows_per_slice < N) ? r0 + a.rows_per_slice : N;
   const float* xb = a.x + (size_t)b * N * D;
-  const float* l2 = a.l2 + bk * N;   // (not read in hard mode)
+  const float* l2 = a.hard ? nullptr : a.l2 + bk * N;
   const float* lse2 = a.lse2 + (size_t)b * N;
-  const int* hidx = a.hard_idx + (size_t)b * N;
+  const int* hidx = a.hard ? a.hard_idx + (size_t)b * N : nullptr;
+  const float* thr = a.thr2 ? a.thr2 + (size_t)b * N : nullptr;   // top-k mode
+  const int* thri = a.thr2 ? a.thr_idx + (size_t)b * N : nullptr;
 
   f32x16 acc[NTT];
 #pragma unroll
@@ -262,7 +265,16 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
 
   for (int64_t n0 = r0; n0 < r1; n0 += 32) {
     const int64_t nr = n0 + lr;
-    const float rv = nr >= r1 ? 0.f : (a.hard ? (hidx[nr] == k ? 1.f : 0.f) : fast_exp2(l2[nr] - lse2[nr]));
+    float rv = 0.f;
+    if (nr < r1) {
+      if (a.hard) {
+        rv = hidx[nr] == k ? 1.f : 0.f;
+      } else {
+        const float l = l2[nr];
+        const bool keep = !thr || l > thr[nr] || (l == thr[nr] && k <= thri[nr]);
+        rv = keep ? fast_exp2(l - lse2[nr]) : 0.f;
+      }
+    }
     const float* xblk = xb + (size_t)n0 * D;           // the block's rows, 32-bit offsets below
     const int nrows = (int)((r1 - n0) < 32 ? (r1 - n0) : 32);
     // (unrolled four k-steps deep: all sixteen measured slower at DP 32 and 64)
@@ -315,7 +327,7 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
 // ---------------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void fw_proba_kernel(const float* l2, const float* lse2, float* proba,
-                                                       int64_t N, int K) {
+                                                       int64_t N, int K, bool raw) {
   __shared__ float tile[32][33];
   const int b = blockIdx.z;
   const int64_t n0 = (int64_t)blockIdx.x * 32;
@@ -325,7 +337,10 @@ __global__ __launch_bounds__(256) void fw_proba_kernel(const float* l2, const fl
     const int64_t n = n0 + tx;
     const int k = k0 + kk;
     float v = 0.f;
-    if (n < N && k < K) v = fast_exp2(l2[((size_t)b * K + k) * N + n] - lse2[(size_t)b * N + n]);
+    if (n < N && k < K) {
+      const float l = l2[((size_t)b * K + k) * N + n];
+      v = raw ? l : fast_exp2(l - lse2[(size_t)b * N + n]);
+    }
     tile[kk][tx] = v;
   }
   __syncthreads();
@@ -368,8 +383,9 @@ int launch_fw(int dp, int phase, const FwArgs& a, int slices, hipStream_t s) {
   }
 }
 
-void launch_fw_proba(const float* l2, const float* lse2, float* proba, int B, int64_t N, int K, hipStream_t s) {
-  fw_proba_kernel<<<dim3((unsigned)((N + 31) / 32), (K + 31) / 32, B), 256, 0, s>>>(l2, lse2, proba, N, K);
+void launch_fw_proba(const float* l2, const float* lse2, float* proba, int B, int64_t N, int K, hipStream_t s,
+                     bool raw) {
+  fw_proba_kernel<<<dim3((unsigned)((N + 31) / 32), (K + 31) / 32, B), 256, 0, s>>>(l2, lse2, proba, N, K, raw);
 }
 
 }  // namespace gx

@@ -126,6 +126,11 @@ struct FwArgs {
   // statistics take r = 1 for that component, 0 elsewhere (no logits stored).
   int hard;
   int* hard_idx;               // [B][N]
+  // Approximate top-k EM with k > 1 (statistics kernel): r = 2^(l2 - lse2) for
+  // the components a row keeps (logit above thr2, or equal and index <= thr_idx),
+  // lse2 then being the top-k log-normaliser; 0 elsewhere.
+  const float* thr2;           // [B][N] or null
+  const int* thr_idx;          // [B][N]
 };
 int64_t fw_lpack_floats(int B, int K, int DP);
 int fw_eblocks(int64_t N);
@@ -133,7 +138,9 @@ void launch_fw_pack(const FwPackArgs& a, hipStream_t s);
 // phase 0: the E-step over fw_eblocks(N) x B workgroups; 1: the statistics over
 // slices x ceil(K / 4) x B.  Returns -1 for an unsupported dp.
 int launch_fw(int dp, int phase, const FwArgs& a, int slices, hipStream_t s);
-void launch_fw_proba(const float* l2, const float* lse2, float* proba, int B, int64_t N, int K, hipStream_t s);
+// proba[b][n][k] = 2^(l2[b][k][n] - lse2[b][n]), or (raw) the log2 logits l2 themselves, transposed.
+void launch_fw_proba(const float* l2, const float* lse2, float* proba, int B, int64_t N, int K, hipStream_t s,
+                     bool raw = false);
 
 // Full-covariance inference at D <= 16, K <= 32 (em_full_infer.hip): whitening
 // with split bf16 operands, every component of a row in one wave.

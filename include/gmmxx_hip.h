@@ -178,8 +178,7 @@ int gmmxx_hip_estep_stats(const gmmxx_problem* p, const void* x, const float* me
  * row's responsibilities cover only its top_k components (largest logits,
  * ties to the lower component index), normalised over those, and ll_sum sums
  * the top-k log-normalisers.  1 <= top_k <= K-1 (top_k >= K is exact EM: use
- * gmmxx_hip_estep_stats); for full covariance at D > 16 only top_k = 1
- * (GMMXX_ERR_UNSUPPORTED otherwise).  For top_k > 1 the (B, N, K) logits are materialised
+ * gmmxx_hip_estep_stats).  For top_k > 1 the (B, N, K) logits are materialised
  * in the workspace, whose size is gmmxx_hip_topk_workspace_bytes(p, top_k);
  * callers bound it by passing row chunks, as the reference does with
  * chunk_size_N.  top_k = 1 (hard assignment to the first maximum) stores no

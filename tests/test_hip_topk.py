@@ -38,6 +38,8 @@ CASES = [
     ("full", 2, 1000, 3, 5, torch.float32, 1),
     ("full", 1, 6000, 16, 32, torch.float32, 3),
     ("full", 2, 5000, 40, 6, torch.float32, 1),              # D > 16: hard assignment on the whitening kernels
+    ("full", 1, 6000, 64, 5, torch.float32, 2),              # D > 16: transposed logits, top-k selection
+    ("full", 2, 3000, 24, 9, torch.float32, 8),              # D > 16, top_k = K - 1
 ]
 
 
@@ -47,13 +49,6 @@ def _id(c):
 
 def _close(got, exp, tol):
     torch.testing.assert_close(got.cpu(), exp, rtol=tol, atol=tol * float(exp.abs().max()))
-
-
-def test_topk_above_one_full_wide_is_unsupported(hip):
-    """Full covariance at D > 16 provides top_k = 1 only: a larger top_k is refused."""
-    x, means, covs, w = make_problem("full", 1, 500, 24, 4, seed=42)
-    with pytest.raises(hip.HipRuntimeError, match="top_k > 1"):
-        hip.estep_stats_topk("full", to_dev(x), to_dev(means), to_dev(covs), to_dev(w), 2)
 
 
 @pytest.mark.parametrize("case", CASES, ids=_id)
