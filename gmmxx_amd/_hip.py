@@ -21,10 +21,12 @@ import torch
 
 _LIB_NAME = "libgmmxx_hip.so"
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 COV_CODES = {"spherical": 0, "diag": 1, "tied": 2, "full": 3}
 _DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1}
+# parameter dtypes (gmmxx_problem.param_dtype): None / float32 keeps the parameters unrounded
+_PARAM_CODES = {None: 0, torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
 
 class HipBackendUnavailable(RuntimeError):
@@ -62,7 +64,7 @@ class DevInfo(ctypes.Structure):
 class _Problem(ctypes.Structure):
     _fields_ = [("covariance_type", ctypes.c_int32), ("x_dtype", ctypes.c_int32),
                 ("B", ctypes.c_int64), ("N", ctypes.c_int64), ("D", ctypes.c_int64),
-                ("K", ctypes.c_int64)]
+                ("K", ctypes.c_int64), ("param_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 _lib = None
@@ -173,12 +175,19 @@ def _check(rc: int, what: str) -> None:
         raise cls(f"{what} failed (status {rc}): {last_error()}")
 
 
-def problem(covariance_type: str, x_dtype: torch.dtype, B: int, N: int, D: int, K: int) -> _Problem:
+def problem(covariance_type: str, x_dtype: torch.dtype, B: int, N: int, D: int, K: int,
+            param_dtype: Optional[torch.dtype] = None) -> _Problem:
+    """The problem descriptor.  ``param_dtype`` (bfloat16 / float16) keeps the
+    parameters in that dtype between iterations, as the reference does for a
+    half-precision x computed in fp32 (see gmmxx_problem in include/gmmxx_hip.h)."""
     if covariance_type not in COV_CODES:
         raise ValueError(f"unknown covariance_type {covariance_type!r}")
     if x_dtype not in _DTYPE_CODES:
         raise ValueError(f"x dtype must be float32 or bfloat16, got {x_dtype}")
-    return _Problem(COV_CODES[covariance_type], _DTYPE_CODES[x_dtype], int(B), int(N), int(D), int(K))
+    if param_dtype not in _PARAM_CODES:
+        raise ValueError(f"param_dtype must be None, float32, bfloat16 or float16, got {param_dtype}")
+    return _Problem(COV_CODES[covariance_type], _DTYPE_CODES[x_dtype], int(B), int(N), int(D), int(K),
+                    _PARAM_CODES[param_dtype], 0)
 
 
 def supported(covariance_type: str, x_dtype: torch.dtype, B: int, N: int, D: int, K: int) -> bool:
@@ -307,10 +316,10 @@ def gram(x: torch.Tensor, ws: Optional[Workspace] = None) -> torch.Tensor:
 def em_step(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
             weights: torch.Tensor, lower_bound_out: torch.Tensor, *, reg_covar: float = 1e-6,
             min_weight: float = 1e-8, gram_xx: Optional[torch.Tensor] = None,
-            ws: Optional[Workspace] = None) -> None:
+            ws: Optional[Workspace] = None, param_dtype: Optional[torch.dtype] = None) -> None:
     """One in-place soft-EM iteration on (means, covs, weights); fp32 contiguous
     device tensors.  ``lower_bound_out`` (1 float, device) receives the mean
-    log-likelihood under the entry parameters."""
+    log-likelihood under the entry parameters.  ``param_dtype``: see ``problem``."""
     require_hip()
     x = _device_tensor(x, "x")
     B, N, D, K = _shape(x, means)
@@ -318,7 +327,7 @@ def em_step(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: to
         if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
             raise ValueError(f"{nm} must be a contiguous float32 GPU tensor")
     _check_params(covariance_type, means, covs, weights, B, K, D)
-    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    prob = problem(covariance_type, x.dtype, B, N, D, K, param_dtype)
     ws = ws or Workspace(prob, x.device)
     if covariance_type == "tied" and gram_xx is None:
         raise ValueError("tied EM needs gram_xx = XᵀX")
@@ -359,7 +368,7 @@ EM_PHASES = ("prepare", "lse_tile", "combine", "stats_tile", "reduce", "finalize
 def em_phase(phase: str, covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
              weights: torch.Tensor, lower_bound_out: torch.Tensor, ws: Workspace, *,
              reg_covar: float = 1e-6, min_weight: float = 1e-8,
-             gram_xx: Optional[torch.Tensor] = None) -> None:
+             gram_xx: Optional[torch.Tensor] = None, param_dtype: Optional[torch.dtype] = None) -> None:
     """Runs one phase of em_step (see EM_PHASES) on the current stream; the
     workspace carries the state between phases."""
     require_hip()
@@ -371,7 +380,7 @@ def em_phase(phase: str, covariance_type: str, x: torch.Tensor, means: torch.Ten
         if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
             raise ValueError(f"{nm} must be a contiguous float32 GPU tensor")
     _check_params(covariance_type, means, covs, weights, B, K, D)
-    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    prob = problem(covariance_type, x.dtype, B, N, D, K, param_dtype)
     _check(_lib.gmmxx_hip_em_phase(ctypes.byref(prob), EM_PHASES.index(phase), _ptr(x), _ptr(means), _ptr(covs),
                                    _ptr(weights), _ptr(gram_xx), float(reg_covar), float(min_weight),
                                    _ptr(lower_bound_out), ws.ptr, ws.nbytes, _stream(x.device)),
@@ -380,8 +389,9 @@ def em_phase(phase: str, covariance_type: str, x: torch.Tensor, means: torch.Ten
 
 def estep_stats(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
                 weights: torch.Tensor, *, reg_covar: float = 1e-6, min_weight: float = 1e-8,
-                ws: Optional[Workspace] = None):
-    """Sufficient statistics of one E-step: (nk, sum_x, sum_q, ll_sum)."""
+                ws: Optional[Workspace] = None, param_dtype: Optional[torch.dtype] = None):
+    """Sufficient statistics of one E-step: (nk, sum_x, sum_q, ll_sum).
+    ``param_dtype``: the prelude's weights kept in it (see ``problem``)."""
     require_hip()
     x = _device_tensor(x, "x")
     means = _device_tensor(means, "means", torch.float32)
@@ -389,7 +399,7 @@ def estep_stats(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs
     weights = _device_tensor(weights, "weights", torch.float32)
     B, N, D, K = _shape(x, means)
     _check_params(covariance_type, means, covs, weights, B, K, D)
-    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    prob = problem(covariance_type, x.dtype, B, N, D, K, param_dtype)
     ws = ws or Workspace(prob, x.device)
     dev = x.device
     nk = torch.empty((B, K), dtype=torch.float32, device=dev)
@@ -405,7 +415,7 @@ def estep_stats(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs
 
 def estep_stats_topk(covariance_type: str, x: torch.Tensor, means: torch.Tensor, covs: torch.Tensor,
                      weights: torch.Tensor, top_k: int, *, reg_covar: float = 1e-6, min_weight: float = 1e-8,
-                     ws: Optional[Workspace] = None):
+                     ws: Optional[Workspace] = None, param_dtype: Optional[torch.dtype] = None):
     """Approximate top-k E-step statistics (nk, sum_x, sum_q, ll_sum): each row's
     responsibility mass is spread over its ``top_k`` largest logits only (ties by
     lower component index), normalised over them; ``ll_sum`` sums the top-k
@@ -421,7 +431,7 @@ def estep_stats_topk(covariance_type: str, x: torch.Tensor, means: torch.Tensor,
     _check_params(covariance_type, means, covs, weights, B, K, D)
     if not 1 <= int(top_k) < K:
         raise ValueError(f"top_k must satisfy 1 <= top_k < K={K}, got {top_k}")
-    prob = problem(covariance_type, x.dtype, B, N, D, K)
+    prob = problem(covariance_type, x.dtype, B, N, D, K, param_dtype)
     ws = ws or Workspace(prob, x.device, top_k=int(top_k))
     dev = x.device
     nk = torch.empty((B, K), dtype=torch.float32, device=dev)
@@ -470,11 +480,11 @@ def finalize_stats(covariance_type: str, nk: torch.Tensor, sum_x: torch.Tensor, 
                    means: torch.Tensor, covs: torch.Tensor, weights: torch.Tensor, n_rows: int, *,
                    gram_xx: Optional[torch.Tensor] = None, reg_covar: float = 1e-6,
                    min_weight: float = 1e-8, ws: Optional[Workspace] = None,
-                   x_dtype: torch.dtype = torch.float32) -> None:
+                   x_dtype: torch.dtype = torch.float32, param_dtype: Optional[torch.dtype] = None) -> None:
     """M-step in place on (means, covs, weights) from sufficient statistics summed
     over row chunks (``estep_stats`` layout); ``n_rows`` is the total row count.
     ``x_dtype`` is the statistics' input dtype: spherical bf16 x stores the means
-    rounded to bf16, as ``em_step`` does."""
+    rounded to bf16, as ``em_step`` does; ``param_dtype``: see ``problem``."""
     require_hip()
     for t, nm in ((means, "means"), (covs, "covariances"), (weights, "weights")):
         if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()):
@@ -487,7 +497,7 @@ def finalize_stats(covariance_type: str, nk: torch.Tensor, sum_x: torch.Tensor, 
         sum_q = _device_tensor(sum_q, "sum_q", torch.float32)
     if gram_xx is not None:
         gram_xx = _device_tensor(gram_xx, "gram_xx", torch.float32)
-    prob = problem(covariance_type, x_dtype, B, int(n_rows), D, K)
+    prob = problem(covariance_type, x_dtype, B, int(n_rows), D, K, param_dtype)
     ws = ws or Workspace(problem(covariance_type, x_dtype, B, 1, D, K), means.device)
     _check(_lib.gmmxx_hip_finalize_stats(ctypes.byref(prob), _ptr(nk), _ptr(sum_x), _ptr(sum_q), _ptr(gram_xx),
                                          float(reg_covar), float(min_weight), _ptr(means), _ptr(covs),

@@ -65,6 +65,7 @@ struct Plan {
   size_t o_xch = 0, o_flags = 0;
   // full covariance at D > 16 (whitening E-step, weighted-Gram statistics)
   bool fw = false;
+  int pdt = 0;   // param_dtype
   int fw_eblk = 0, fw_slices = 0;
   int64_t fw_rows = 0;
   size_t o_lpack = 0, o_lpaug = 0, o_l2w = 0, o_linv = 0;
@@ -91,6 +92,11 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
     return fail(GMMXX_ERR_INVALID_ARGUMENT, "covariance_type must be 0..3");
   if (p->x_dtype != GMMXX_F32 && p->x_dtype != GMMXX_BF16)
     return fail(GMMXX_ERR_INVALID_ARGUMENT, "x_dtype must be GMMXX_F32 or GMMXX_BF16");
+  if (p->param_dtype != GMMXX_F32 && p->param_dtype != GMMXX_BF16 && p->param_dtype != GMMXX_F16)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "param_dtype must be GMMXX_F32, GMMXX_BF16 or GMMXX_F16");
+  if (p->x_dtype == GMMXX_BF16 && p->param_dtype == GMMXX_F16)
+    return fail(GMMXX_ERR_INVALID_ARGUMENT, "bf16 x keeps its means in bf16: param_dtype must not be GMMXX_F16");
+  if (p->reserved != 0) return fail(GMMXX_ERR_INVALID_ARGUMENT, "reserved must be 0");
   if (p->B < 1 || p->N < 1 || p->D < 1 || p->K < 1)
     return fail(GMMXX_ERR_INVALID_ARGUMENT, "B, N, D and K must be positive");
   if (p->B > 65535) return fail(GMMXX_ERR_UNSUPPORTED, "B > 65535");
@@ -99,6 +105,7 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   Plan& q = *pl;
   q.cov = p->covariance_type;
   q.bf = p->x_dtype == GMMXX_BF16;
+  q.pdt = p->param_dtype;
   q.B = (int)p->B;
   q.N = p->N;
   q.D = (int)p->D;
@@ -498,6 +505,7 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
     f.D = pl.D;
     f.DP = pl.DP;
     f.prelude = prelude;
+    f.param_round = prelude ? pl.pdt : 0;
     f.min_weight = (float)minw;
     f.means = means;
     f.weights = weights;
@@ -513,6 +521,7 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   a.cov = pl.cov;
   a.bf = pl.bf;
   a.prelude = prelude;
+  a.param_round = prelude ? pl.pdt : 0;
   a.B = pl.B;
   a.K = pl.K;
   a.D = pl.D;
@@ -598,6 +607,7 @@ FinalizeArgs finalize_args(const Plan& pl, void* ws, const float* gram, double r
   f.weights = weights;
   f.skip = skip;
   f.bf_means = pl.bf && pl.cov == SPH;
+  f.param_round = pl.pdt;
   return f;
 }
 

@@ -35,6 +35,8 @@
 
 #include <math.h>
 
+#include <hip/hip_fp16.h>
+
 #include "common.hpp"
 #include "engine.hpp"
 
@@ -82,6 +84,8 @@ __global__ __launch_bounds__(256) void fw_pack_kernel(FwPackArgs a) {
     __syncthreads();
     const float total = (float)red[0] + (float)red[1] + (float)red[2] + (float)red[3];
     wk = clamp_lo(wk, a.min_weight) / total;
+    if (a.param_round == 1) wk = (float)(__bf16)wk;
+    else if (a.param_round == 2) wk = (float)(__half)wk;
   }
   const float* X = a.linv + bk * D * D;
   const float* mu = a.means + bk * D;

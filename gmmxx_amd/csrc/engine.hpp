@@ -96,6 +96,7 @@ int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s);
 // weighted-Gram statistics on the fp32 MFMA, DP in {32, 64, 128}.
 struct FwPackArgs {
   int B, K, D, DP, prelude;
+  int param_round;             // 1 bf16, 2 fp16: the prelude's normalised weights kept in that dtype
   float min_weight;
   const float* means;          // [B][K][D]
   const float* weights;        // [B][K]

@@ -6,6 +6,8 @@
 
 #include <math.h>
 
+#include <hip/hip_fp16.h>
+
 #include <algorithm>
 
 #include "common.hpp"
@@ -52,6 +54,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ float jitter_of(int level);
 
+// v rounded to the parameter dtype (1 bf16, 2 fp16; 0 leaves it).
+__device__ __forceinline__ float round_param(float v, int mode) {
+  return mode == 1 ? (float)(__bf16)v : (mode == 2 ? (float)(__half)v : v);
+}
+
 __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
   __shared__ float scratch[32];
   __shared__ float mus[kMaxPrepD];
@@ -64,7 +71,9 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
   const float floor_v = a.prelude ? a.min_weight : -INFINITY;
   const float total = a.prelude ? weight_total(wrow, K, floor_v, scratch) : 1.f;
   const size_t bk = (size_t)b * K + k;
-  const float wk = a.prelude ? clamp_lo(wrow[k], floor_v) / total : wrow[k];
+  // (with a parameter dtype the normalised weight is kept in it, as the
+  // reference's prelude divides in x's dtype)
+  const float wk = a.prelude ? round_param(clamp_lo(wrow[k], floor_v) / total, a.param_round) : wrow[k];
   const float lw = logf(wk);
   const float* mu = a.means + bk * D;
   // bf16 x (spherical) computes with bf16 means, as the reference keeps them in
@@ -1029,13 +1038,16 @@ __device__ void finalize_comp(const FinalizeArgs& a, int b, int k, float total) 
   float msq = 0.f;
   for (int d = lane; d < D; d += 64) {
     const float m = active ? sk[d] / nk_safe : mu[d];
-    // bf16 x: the means are stored in bf16 (torch_fallback.py:2295); the variance
-    // below is formed from the unrounded mean.
-    mu[d] = a.bf_means ? (float)(__bf16)m : m;
+    // bf16 x: the means are stored in bf16 (torch_fallback.py:2295); the spherical
+    // variance below is formed from the unrounded mean.  A parameter dtype rounds
+    // the means (and the diag variances, formed from the rounded means as
+    // :2654-2666 does) to it.
+    const float mr = a.bf_means ? (float)(__bf16)m : round_param(m, a.param_round);
+    mu[d] = mr;
     msq = fmaf(m, m, msq);
     if (a.cov == DIAG) {
-      const float v = clamp_lo(sk[a.DP + d] / nk_safe - m * m, a.reg_covar);
-      a.covs[bk * D + d] = active ? v : a.covs_used[bk * D + d];
+      const float v = clamp_lo(sk[a.DP + d] / nk_safe - mr * mr, a.reg_covar);
+      a.covs[bk * D + d] = active ? round_param(v, a.param_round) : a.covs_used[bk * D + d];
     }
   }
   if (a.cov == SPH) {
@@ -1046,7 +1058,10 @@ __device__ void finalize_comp(const FinalizeArgs& a, int b, int k, float total) 
     v = clamp_lo(v, a.reg_covar);
     if (lane == 0) a.covs[bk] = active ? v : a.covs_used[bk];
   }
-  if (lane == 0) a.weights[bk] = clamp_lo(nk / (float)a.N, a.min_weight) / total;
+  if (lane == 0) {
+    const float wn = clamp_lo(nk / (float)a.N, a.min_weight) / total;
+    a.weights[bk] = a.cov == SPH ? wn : round_param(wn, a.param_round);   // (spherical weights stay fp32)
+  }
 }
 
 // One wave per component, kFinWaves components per block.
@@ -1093,7 +1108,7 @@ __global__ __launch_bounds__(64 * kTiedWaves) void finalize_tied_kernel(Finalize
   const float* G = a.gram + (size_t)b * D * D;
   const float ade = (G[d * D + e] - sde) / (float)a.N;
   const float aed = (G[e * D + d] - sde) / (float)a.N;
-  a.covs[(size_t)b * D * D + d * D + e] = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
+  a.covs[(size_t)b * D * D + d * D + e] = round_param(0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f), a.param_round);
 }
 
 // Full: Σ_k = sym((Σ r xxᵀ − n_k μμᵀ) / max(n_k, floor)) + reg·I, kept if inactive (:3150-3158)
@@ -1114,7 +1129,7 @@ __global__ void finalize_full_kernel(FinalizeArgs a) {
     const float ade = (sxx - nk * (mu[d] * mu[e])) / nk_safe;
     const float aed = (sxx - nk * (mu[e] * mu[d])) / nk_safe;
     const float v = 0.5f * (ade + aed) + (d == e ? a.reg_covar : 0.f);
-    if (active) C[t] = v;  // inactive components keep their previous covariance
+    if (active) C[t] = round_param(v, a.param_round);  // inactive components keep their previous covariance
   }
 }
 

@@ -8,6 +8,7 @@ namespace gx {
 
 struct PrepArgs {
   int cov, bf, prelude;
+  int param_round;         // 1 bf16, 2 fp16: the prelude's normalised weights kept in that dtype
   int B, K, D, DP, EP;
   float reg_covar, min_weight;
   const float* means;      // [B][K][D]
@@ -54,6 +55,8 @@ struct FinalizeArgs {
   float* weights;
   const unsigned* skip;    // nonzero *skip: leave the parameters unchanged (or null)
   int bf_means;            // spherical bf16 x: store the means rounded to bf16
+  int param_round;         // 1 bf16, 2 fp16: store the means (and, diag/tied/full, the
+                           // covariances and weights) rounded to that dtype
 };
 
 struct UnpackArgs {

@@ -86,6 +86,20 @@ def _engine_means(means: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     return means.to(torch.bfloat16).to(torch.float32) if x.dtype == torch.bfloat16 else means
 
 
+def round_params(means, covs, weights, covariance_type, param_dtype):
+    """The parameters as kept in ``param_dtype`` (None: unchanged), as fp32
+    tensors: the means, and for diag/tied/full the covariances and weights too,
+    as the reference keeps a half-precision x's parameters in its dtype
+    (torch_fallback.py:1661-1682 at entry, :2295, :2654-2666, :3143-3167 after
+    every M-step; spherical variances and weights stay fp32)."""
+    if param_dtype is None or param_dtype == torch.float32:
+        return means, covs, weights
+    r = lambda t: t.to(param_dtype).to(torch.float32).contiguous()
+    if covariance_type == "spherical":
+        return r(means), covs, weights
+    return r(means), r(covs), r(weights)
+
+
 def _init_weights(init_weights, bsz, k, device):
     w = (torch.full((bsz, k), 1.0 / float(k), device=device) if init_weights is None
          else _f32(init_weights, device))
@@ -115,8 +129,10 @@ def flash_kmeans_emulated() -> bool:
 def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init_means=None,
                init_covs=None, init_weights=None, reg_covar: float = 1e-6,
                init_params: str = "kmeans", generator: Optional[torch.Generator] = None,
-               kmeans_init_iters: int = 10, kmeans_init_tol: float = 1e-4):
-    """Initial (means, covariances, weights, source), fp32 on x's device.
+               kmeans_init_iters: int = 10, kmeans_init_tol: float = 1e-4,
+               param_dtype: Optional[torch.dtype] = None):
+    """Initial (means, covariances, weights, source), fp32 on x's device
+    (holding ``param_dtype`` values when one is given, ``round_params``).
 
     Explicit parameters get the reference's entry clamps
     (torch_fallback.py:1661-1682, :1731-1742, :1791-1802, :1851-1862).  Without
@@ -143,7 +159,8 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
             means, covs, weights = kmeans.kmeans_initialize(
                 x, covariance_type, k, max_iters=kmeans_init_iters, tol=kmeans_init_tol, reg_covar=reg_covar,
                 generator=generator)
-            return _engine_means(means, x), covs, weights, "kmeans"
+            return (*round_params(_engine_means(means, x), covs, weights, covariance_type, param_dtype),
+                    "kmeans")
         idx = torch.randint(0, n, (bsz, k), device=dev, generator=generator)
         means = torch.gather(x, 1, idx[..., None].expand(-1, -1, d)).to(torch.float32).contiguous()
         source = "random"
@@ -170,7 +187,9 @@ def initialize(x: torch.Tensor, covariance_type: str, n_components: int, *, init
             raise ValueError("init_variances must have shape (B, K, D, D) for full covariance")
         covs = _sym(covs)
     weights = _init_weights(init_weights, bsz, k, dev)
-    return _engine_means(means, x).contiguous(), covs.contiguous(), weights, source
+    means, covs, weights = round_params(_engine_means(means, x).contiguous(), covs.contiguous(), weights,
+                                        covariance_type, param_dtype)
+    return means, covs, weights, source
 
 
 def resolve_approx_top_k(approx_top_k: Optional[int], n_components: int) -> Optional[int]:
@@ -201,8 +220,9 @@ class _TopkStep:
     branches of the reference's EM loops (gmmxx/torch_fallback.py:2097-2145,
     :2500-2526, :2911-2936), which likewise accumulate over row chunks."""
 
-    def __init__(self, x, covariance_type, k, top_k):
+    def __init__(self, x, covariance_type, k, top_k, param_dtype=None):
         self.x, self.cov, self.k, self.top_k = x, covariance_type, k, top_k
+        self.param_dtype = param_dtype
         bsz, n, d = x.shape
         self.n = n
         # top-1 (hard assignment) keeps no logits: one chunk
@@ -233,14 +253,15 @@ class _TopkStep:
         tot = None
         for xc, ws in self.chunks():
             part = _hip.estep_stats_topk(self.cov, xc, means, covs, weights, self.top_k, reg_covar=reg_covar,
-                                         min_weight=min_weight, ws=ws)
+                                         min_weight=min_weight, ws=ws, param_dtype=self.param_dtype)
             tot = list(part) if tot is None else [a if a is None else a + b for a, b in zip(tot, part)]
         return tot
 
     def step(self, means, covs, weights, lb_out, gram, reg_covar, min_weight):
         nk, sum_x, sum_q, ll = self.stats(means, covs, weights, reg_covar, min_weight)
         _hip.finalize_stats(self.cov, nk, sum_x, sum_q, means, covs, weights, self.n, gram_xx=gram,
-                            reg_covar=reg_covar, min_weight=min_weight, ws=self.fin_ws, x_dtype=self.x.dtype)
+                            reg_covar=reg_covar, min_weight=min_weight, ws=self.fin_ws, x_dtype=self.x.dtype,
+                            param_dtype=self.param_dtype)
         torch.div(ll, float(self.x.shape[0] * self.n), out=lb_out)
 
 
@@ -250,7 +271,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         init_params: str = "kmeans", reg_covar: float = 1e-6, min_weight: float = 1e-8,
         compute_labels: bool = True, generator: Optional[torch.Generator] = None,
         approx_top_k: Optional[int] = None, kmeans_init_iters: int = 10, kmeans_init_tol: float = 1e-4,
-        record_all_lower_bounds: bool = False,
+        record_all_lower_bounds: bool = False, param_dtype: Optional[torch.dtype] = None,
         ) -> Tuple[Optional[torch.Tensor], torch.Tensor, torch.Tensor, torch.Tensor, Dict[str, object]]:
     """Soft EM on the HIP engine; see the module docstring.  ``approx_top_k``
     (1 <= k < K) restricts each row's responsibilities to its k largest logits,
@@ -261,7 +282,11 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
     lower bound is recorded and the others are 0.0
     (gmmxx/torch_fallback.py:2484-2485, :2668-2679, :3169-3180); spherical
     records every iteration.  ``record_all_lower_bounds=True`` records every
-    iteration for every type (the engine computes them all anyway)."""
+    iteration for every type (the engine computes them all anyway).
+
+    ``param_dtype`` (bfloat16 / float16, fp32 x) keeps the parameters in that
+    dtype between iterations, as the reference keeps a half-precision x's
+    (``round_params``; the library rounds them in its M-step)."""
     if covariance_type not in _COVS:
         raise ValueError("covariance_type must be 'spherical', 'diag', 'tied' or 'full'")
     if n_components <= 0:
@@ -278,7 +303,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
     means, covs, weights, source = initialize(
         x, covariance_type, n_components, init_means=init_means, init_covs=init_covs,
         init_weights=init_weights, reg_covar=reg_covar, init_params=init_params, generator=generator,
-        kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol)
+        kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol, param_dtype=param_dtype)
     k = means.shape[1]
     if not _hip.supported(covariance_type, x.dtype, bsz, n, d, k):
         raise _hip.HipRuntimeError(
@@ -291,7 +316,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
         gram = _hip.gram(x, ws) if covariance_type == "tied" else None
     else:
         ws = None
-        topk_step = _TopkStep(x, covariance_type, k, top_k)
+        topk_step = _TopkStep(x, covariance_type, k, top_k, param_dtype)
         gram = topk_step.gram() if covariance_type == "tied" else None
     lb = torch.zeros((max_iters,), dtype=torch.float32, device=x.device)
     spherical = covariance_type == "spherical"
@@ -301,7 +326,7 @@ def fit(x: torch.Tensor, n_components: int, covariance_type: str, *, max_iters: 
     for it in range(max_iters):
         if topk_step is None:
             _hip.em_step(covariance_type, x, means, covs, weights, lb[it:it + 1], reg_covar=reg_covar,
-                         min_weight=min_weight, gram_xx=gram, ws=ws)
+                         min_weight=min_weight, gram_xx=gram, ws=ws, param_dtype=param_dtype)
         else:
             topk_step.step(means, covs, weights, lb[it:it + 1], gram, reg_covar, min_weight)
         n_iter = it + 1

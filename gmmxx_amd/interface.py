@@ -92,7 +92,8 @@ class GMMXX:
     ``covariance_type`` is ``spherical``, ``diag``/``diagonal``, ``tied`` or
     ``full``.  Supported shapes: D <= 128; any N, K <= 65536, B <= 65535.  Half-precision input is
     computed in fp32 unless ``dtype=torch.bfloat16`` (spherical: the bf16
-    engine).  ``approx_top_k`` (1 <= k < K) opts into the reference's
+    engine); other explicit half dtypes are computed in fp32 with the
+    parameters kept in that dtype, as the reference keeps them.  ``approx_top_k`` (1 <= k < K) opts into the reference's
     approximate EM: each row's responsibilities cover only its k largest
     logits; prediction stays exact.
     """
@@ -258,6 +259,15 @@ class GMMXX:
             raise TypeError("float64 data is not supported by the hip backend; pass dtype=torch.float32")
         return torch.bfloat16 if (compute == torch.bfloat16 and self.covariance_type == "spherical") else torch.float32
 
+    def _param_dtype(self, x_b: torch.Tensor) -> Optional[torch.dtype]:
+        """The dtype the parameters are kept in: an explicit half-precision
+        ``dtype`` computed by the fp32 engine keeps them in that dtype between
+        iterations, as the reference keeps its parameters in the compute dtype
+        (the bf16 spherical engine rounds its means itself)."""
+        if self.dtype in (torch.float16, torch.bfloat16) and self._engine_dtype(x_b) == torch.float32:
+            return self.dtype
+        return None
+
     def _engine_tensor(self, x_b: torch.Tensor) -> torch.Tensor:
         """x on the estimator's GPU in the dtype the engine reads: fp32 (the
         reference's compute dtype for float32 and half-precision input,
@@ -302,7 +312,8 @@ class GMMXX:
                 verbose=self.verbose, init_params=self.init_params, reg_covar=self.reg_covar,
                 chunk_size_N=self.chunk_size_data_cpu, compute_labels=self.compute_labels_on_fit,
                 seed=self.seed, approx_top_k=self.approx_top_k, kmeans_init_iters=self.init_kmeans_iters,
-                kmeans_init_tol=self.init_kmeans_tol, compute_dtype=self._engine_dtype(x_b))
+                kmeans_init_tol=self.init_kmeans_tol, compute_dtype=self._engine_dtype(x_b),
+                param_dtype=self._param_dtype(x_b))
         else:
             x_b = self._engine_tensor(x_b)
             self.last_backend_used_ = self._resolve(x_b, self.k)
@@ -310,7 +321,7 @@ class GMMXX:
                 x_b, self.k, self.covariance_type, max_iters=self.niter, tol=self.tol, verbose=self.verbose,
                 init_params=self.init_params, reg_covar=self.reg_covar, compute_labels=self.compute_labels_on_fit,
                 approx_top_k=self.approx_top_k, kmeans_init_iters=self.init_kmeans_iters,
-                kmeans_init_tol=self.init_kmeans_tol)
+                kmeans_init_tol=self.init_kmeans_tol, param_dtype=self._param_dtype(x_b))
         self._scores_cache = None
         self.cluster_ids_b = labels_b
         self.means_b = means_b

@@ -173,13 +173,14 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
                 chunk_size_N: int = 1 << 20, min_weight: float = 1e-8, compute_labels: bool = True,
                 max_init_samples: int = 65536, init_means=None, init_covs=None, init_weights=None,
                 seed: int = 0, approx_top_k: Optional[int] = None, kmeans_init_iters: int = 10,
-                kmeans_init_tol: float = 1e-4, compute_dtype: Optional[torch.dtype] = None):
+                kmeans_init_tol: float = 1e-4, compute_dtype: Optional[torch.dtype] = None,
+                param_dtype: Optional[torch.dtype] = None):
     """Soft EM with x (1, N, D) in host memory; returns (labels, means, covariances,
     weights, info) like gmmxx/large_n.py:866-1595 (labels on the host).
     ``approx_top_k`` selects the approximate top-k E-step per chunk, as the
     reference's streamed loop does (gmmxx/large_n.py:1325-1370).  ``compute_dtype``
     (fp32, or bf16 for the spherical bf16 engine) defaults to bf16 for bf16
-    spherical input and fp32 otherwise."""
+    spherical input and fp32 otherwise; ``param_dtype`` as in ``em.fit``."""
     device = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     if covariance_type not in _COVS:
         raise ValueError("covariance_type must be 'spherical', 'diag', 'tied', or 'full'")
@@ -199,13 +200,15 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
         sample = x_cpu[:, : min(n, max(4096, int(max_init_samples)))].to(device=device, dtype=dtype)
         means, covs, weights, source = em.initialize(sample, covariance_type, n_components,
                                                      init_means=init_means, init_covs=init_covs,
-                                                     init_weights=init_weights, reg_covar=reg_covar)
+                                                     init_weights=init_weights, reg_covar=reg_covar,
+                                                     param_dtype=param_dtype)
         sample_n = int(sample.shape[1])
     else:
         means, covs, weights, source, sample_n = _sample_init(
             x_cpu, n_components, covariance_type, device, dtype, init_params=init_params,
             reg_covar=reg_covar, max_init_samples=max_init_samples, seed=seed,
             kmeans_init_iters=kmeans_init_iters, kmeans_init_tol=kmeans_init_tol)
+    means, covs, weights = em.round_params(means, covs, weights, covariance_type, param_dtype)
     k = int(means.shape[1])
     top_k = em.resolve_approx_top_k(approx_top_k, k)
     stream = ChunkStream(x_cpu, device, dtype, chunk_size_N)
@@ -239,11 +242,12 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
                 if top_k is None:
                     c_nk, c_sx, c_sq, c_ll = _hip.estep_stats(covariance_type, xp, means, covs, weights,
                                                               reg_covar=reg_covar, min_weight=min_weight,
-                                                              ws=wss.get(rows))
+                                                              ws=wss.get(rows), param_dtype=param_dtype)
                 else:
                     c_nk, c_sx, c_sq, c_ll = _hip.estep_stats_topk(covariance_type, xp, means, covs, weights,
                                                                    top_k, reg_covar=reg_covar,
-                                                                   min_weight=min_weight, ws=topk_wss.get(rows))
+                                                                   min_weight=min_weight, ws=topk_wss.get(rows),
+                                                                   param_dtype=param_dtype)
                 nk += c_nk
                 sx += c_sx
                 if sq is not None:
@@ -253,7 +257,8 @@ def fit_large_n(x_cpu: torch.Tensor, n_components: int, covariance_type: str, *,
             for ws in wss.cache.values():
                 _hip.raise_on_status(_hip.take_status(ws), "streamed EM fit")
         _hip.finalize_stats(covariance_type, nk, sx, sq, means, covs, weights, n, gram_xx=gram,
-                            reg_covar=reg_covar, min_weight=min_weight, ws=fin_ws, x_dtype=dtype)
+                            reg_covar=reg_covar, min_weight=min_weight, ws=fin_ws, x_dtype=dtype,
+                            param_dtype=param_dtype)
         value = float(ll.item()) / float(n)
         history.append(value)
         n_iter = it + 1

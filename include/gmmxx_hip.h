@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define GMMXX_HIP_ABI_VERSION 1
+#define GMMXX_HIP_ABI_VERSION 2
 
 enum gmmxx_status {
   GMMXX_OK = 0,
@@ -38,12 +38,21 @@ enum gmmxx_status {
 };
 
 enum gmmxx_covariance { GMMXX_SPHERICAL = 0, GMMXX_DIAG = 1, GMMXX_TIED = 2, GMMXX_FULL = 3 };
-enum gmmxx_dtype { GMMXX_F32 = 0, GMMXX_BF16 = 1 };
+enum gmmxx_dtype { GMMXX_F32 = 0, GMMXX_BF16 = 1, GMMXX_F16 = 2 };
 
+/* param_dtype: the dtype the parameters are kept in between iterations.  The
+ * finalize rounds the new means, and for diag/tied/full also the covariances
+ * and weights, to it (stored in the fp32 buffers), as the reference's M-step
+ * casts them to x's dtype (gmmxx/torch_fallback.py:2295, :2654-2666,
+ * :3143-3167) when a half-precision x is computed in fp32.  GMMXX_F32 (0, a
+ * zero-initialised descriptor) keeps them unrounded; bf16 x (spherical) implies
+ * bf16 means.  `reserved` must be 0. */
 typedef struct gmmxx_problem {
   int32_t covariance_type; /* enum gmmxx_covariance */
-  int32_t x_dtype;         /* enum gmmxx_dtype */
+  int32_t x_dtype;         /* enum gmmxx_dtype: GMMXX_F32 or GMMXX_BF16 */
   int64_t B, N, D, K;
+  int32_t param_dtype;     /* enum gmmxx_dtype */
+  int32_t reserved;
 } gmmxx_problem;
 
 /* ABI version of the loaded library (GMMXX_HIP_ABI_VERSION). */

@@ -127,6 +127,21 @@ def test_entry_points_validate_before_device_work(lib):
     assert lib.gmmxx_hip_canary(None, None, 0, 0, None) == 0
 
 
+def test_param_dtype_validation(lib):
+    """gmmxx_problem.param_dtype: GMMXX_F32 / BF16 / F16, not F16 with bf16 x;
+    reserved must be 0 (a rejected descriptor plans no workspace)."""
+    ok = _hip.problem("diag", torch.float32, 1, 100, 8, 4, torch.float16)
+    assert lib.gmmxx_hip_workspace_bytes(ctypes.byref(ok)) > 0
+    bad = _hip._Problem(1, 0, 1, 100, 8, 4, 3, 0)
+    assert lib.gmmxx_hip_workspace_bytes(ctypes.byref(bad)) == -1
+    bad = _hip._Problem(1, 0, 1, 100, 8, 4, 0, 1)
+    assert lib.gmmxx_hip_workspace_bytes(ctypes.byref(bad)) == -1
+    bad = _hip._Problem(0, 1, 1, 100, 128, 4, 2, 0)
+    assert lib.gmmxx_hip_workspace_bytes(ctypes.byref(bad)) == -1
+    with pytest.raises(ValueError):
+        _hip.problem("diag", torch.float32, 1, 100, 8, 4, torch.float64)
+
+
 def test_problem_rejects_unknown_dtype():
     with pytest.raises(ValueError):
         _hip.problem("spherical", torch.float16, 1, 10, 4, 2)
