@@ -90,12 +90,13 @@ class GMMXX:
     """Gaussian mixture model fitted by soft EM on MI355X (gfx950).
 
     ``covariance_type`` is ``spherical``, ``diag``/``diagonal``, ``tied`` or
-    ``full``.  Supported shapes: D <= 128; any N, K <= 65536, B <= 65535.  Half-precision input is
-    computed in fp32 unless ``dtype=torch.bfloat16`` (spherical: the bf16
-    engine); other explicit half dtypes are computed in fp32 with the
-    parameters kept in that dtype, as the reference keeps them.  ``approx_top_k`` (1 <= k < K) opts into the reference's
-    approximate EM: each row's responsibilities cover only its k largest
-    logits; prediction stays exact.
+    ``full``.  Supported shapes: D <= 128; any N, K <= 65536, B <= 65535.
+    Half-precision input is computed in fp32 unless ``dtype=torch.bfloat16``
+    (spherical: the bf16 engine); other explicit half dtypes are computed in
+    fp32 with the parameters kept in that dtype, as the reference keeps them.
+    ``approx_top_k`` (1 <= k < K) opts into the reference's approximate EM:
+    each row's responsibilities cover only its k largest logits; prediction
+    stays exact.
     """
 
     def __init__(
