@@ -117,6 +117,8 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   // Full covariance beyond D = 16: the whitening kernels of em_full_wide.hip
   // (the tile kernel's augmented features are built for D = 16).
   q.fw = q.cov == FULL && q.DP > 16;
+  // (the whitening E-step's per-problem workgroup count is an int: 128 rows each)
+  if (q.fw && q.N > ((int64_t)1 << 36)) return fail(GMMXX_ERR_UNSUPPORTED, "N too large for full covariance at D > 16");
   // Full covariance at D <= 16 with every component in one wave: inference by
   // whitening (em_full_infer.hip) instead of the tile kernel's 136 products per
   // row.  GMMXX_HIP_NO_WHITEN=1 keeps the tile kernels (the tests compare both).

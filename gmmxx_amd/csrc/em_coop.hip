@@ -58,6 +58,7 @@
 // slots would do; four are used.  A slot therefore holds block j or block
 // j - kRing, which the parity tag tells apart.
 
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -576,15 +577,17 @@ __global__ __launch_bounds__(64 * kNW) void sph_bf16_coop_kernel(CoopArgs a) {
 }
 
 int coop_capacity() {
-  // Resident workgroups of the kernel on the current device (cached per device);
-  // 256 when no device is visible (workspace sizing on a machine without a GPU).
-  static int cache[64] = {0};
+  // Resident workgroups of the kernel on the current device (cached per device;
+  // concurrent first calls store the same value); 256 when no device is visible
+  // (workspace sizing on a machine without a GPU).
+  static std::atomic<int> cache[64] = {};
   int ndev = 0, dev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0 || hipGetDevice(&dev) != hipSuccess || dev >= 64) {
     (void)hipGetLastError();
     return 256;
   }
-  if (cache[dev] > 0) return cache[dev];
+  const int cached = cache[dev].load(std::memory_order_relaxed);
+  if (cached > 0) return cached;
   int cus = 0, per = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, sph_bf16_coop_kernel<128, 4>, 64 * kNW, 0) != hipSuccess ||
@@ -592,8 +595,8 @@ int coop_capacity() {
     (void)hipGetLastError();
     return 256;
   }
-  cache[dev] = cus * per;
-  return cache[dev];
+  cache[dev].store(cus * per, std::memory_order_relaxed);
+  return cus * per;
 }
 
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s) {

@@ -25,6 +25,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "common.hpp"
 #include "engine.hpp"
@@ -320,15 +321,17 @@ void launch_full16_pack(const Full16Args& a, hipStream_t s) {
   full16_pack_kernel<<<dim3(a.K, a.B), 64, 0, s>>>(a);
 }
 
-// Resident workgroups of the inference kernel on the current device (cached per device).
+// Resident workgroups of the inference kernel on the current device (cached per
+// device; concurrent first calls store the same value).
 static int full16_capacity() {
-  static int cache[64] = {};
+  static std::atomic<int> cache[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
     (void)hipGetLastError();
     return 256;
   }
-  if (cache[dev] > 0) return cache[dev];
+  const int cached = cache[dev].load(std::memory_order_relaxed);
+  if (cached > 0) return cached;
   int cus = 0, per = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(full16_infer_kernel<8>),
@@ -337,8 +340,8 @@ static int full16_capacity() {
     (void)hipGetLastError();
     return 256;
   }
-  cache[dev] = cus * per;
-  return cache[dev];
+  cache[dev].store(cus * per, std::memory_order_relaxed);
+  return cus * per;
 }
 
 void launch_full16_infer(const Full16Args& a, hipStream_t s) {

@@ -49,6 +49,7 @@
 // bf16 inputs multiply exact bf16 x against a hi/lo bf16 split of the fp32
 // operand, which keeps the cross term at fp32-oracle noise level.
 
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1208,22 +1209,23 @@ static const void* xch_kernel(int cov, int dp) {
 int tile_xch_capacity(int cov, int dp) {
   const void* fn = xch_kernel(cov, dp);
   if (!fn) return 0;
-  static int cache[64][4][8] = {};
+  static std::atomic<int> cache[64][4][8] = {};   // concurrent first calls store the same value
   int ndev = 0, dev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0 || hipGetDevice(&dev) != hipSuccess || dev >= 64) {
     (void)hipGetLastError();
     return 256;   // no device visible: workspace sizing only
   }
-  int& c = cache[dev][cov & 3][(dp / 16) & 7];
-  if (c > 0) return c;
+  std::atomic<int>& c = cache[dev][cov & 3][(dp / 16) & 7];
+  const int cached = c.load(std::memory_order_relaxed);
+  if (cached > 0) return cached;
   int cus = 0, per = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, 64 * 8, 0) != hipSuccess || cus <= 0 || per <= 0) {
     (void)hipGetLastError();
     return 0;
   }
-  c = cus * per;
-  return c;
+  c.store(cus * per, std::memory_order_relaxed);
+  return cus * per;
 }
 
 int launch_tile_xch(int cov, int dp, const TileArgs& a, dim3 grid, int64_t nwords, hipStream_t s) {
