@@ -61,7 +61,7 @@ struct Plan {
   int gram_slices = 0;
   int64_t gram_rows = 0;
   int chol_m = 0;
-  size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_wmu = 0, o_wsc = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
+  size_t o_whi = 0, o_wlo = 0, o_waug = 0, o_wmu = 0, o_wsc = 0, o_waugs = 0, o_cconst = 0, o_covs_used = 0, o_rowq = 0, o_lse2 = 0, o_pms = 0, o_pidx = 0;
   size_t o_xch = 0, o_flags = 0;
   // full covariance at D > 16 (whitening E-step, weighted-Gram statistics)
   bool fw = false;
@@ -247,8 +247,9 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_whi = take(BK * q.EP * (q.bf ? 2 : 4));
   q.o_wlo = take(q.bf ? BK * q.EP * 2 : 0);
   q.o_waug = take(sph_bf ? BK * 32 * 2 : 0);
-  q.o_wmu = take(q.coop ? BK * q.DP * 2 : 0);
-  q.o_wsc = take(q.coop ? BK * 4 : 0);
+  q.o_wmu = take((q.coop || q.fused) ? BK * q.DP * 2 : 0);
+  q.o_wsc = take((q.coop || q.fused) ? BK * 4 : 0);
+  q.o_waugs = take(q.fused ? BK * 16 * 2 : 0);
   q.o_cconst = take(BK * 16);
   q.o_covs_used = take(q.cov == SPH ? BK * 4 : (q.cov == DIAG ? BK * q.D * 4 : 0));
   q.o_rowq = take(q.cov == TIED ? BN * 4 : 0);
@@ -315,6 +316,9 @@ TileArgs tile_args(const Plan& pl, const void* x, void* ws, bool em = false) {
   a.w_hi = at<void>(ws, pl.o_whi);
   a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
   a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
+  a.w_mu = pl.fused ? at<void>(ws, pl.o_wmu) : nullptr;
+  a.w_scale = pl.fused ? at<float>(ws, pl.o_wsc) : nullptr;
+  a.w_augs = pl.fused ? at<void>(ws, pl.o_waugs) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
   a.rowq = (pl.cov == TIED && !em) ? at<float>(ws, pl.o_rowq) : nullptr;
   a.lse2 = at<float>(ws, pl.o_lse2);
@@ -542,8 +546,9 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
   a.w_hi = at<void>(ws, pl.o_whi);
   a.w_lo = pl.bf ? at<void>(ws, pl.o_wlo) : nullptr;
   a.w_aug = (pl.bf && pl.cov == SPH) ? at<void>(ws, pl.o_waug) : nullptr;
-  a.w_mu = pl.coop ? at<void>(ws, pl.o_wmu) : nullptr;
-  a.w_scale = pl.coop ? at<float>(ws, pl.o_wsc) : nullptr;
+  a.w_mu = (pl.coop || pl.fused) ? at<void>(ws, pl.o_wmu) : nullptr;
+  a.w_scale = (pl.coop || pl.fused) ? at<float>(ws, pl.o_wsc) : nullptr;
+  a.w_augs = pl.fused ? at<void>(ws, pl.o_waugs) : nullptr;
   a.cconst = at<float4>(ws, pl.o_cconst);
   a.gram = shift ? gram : nullptr;
   a.shift = gram ? shift : nullptr;

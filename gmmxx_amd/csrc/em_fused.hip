@@ -10,8 +10,9 @@
 // single lane swap. Per block of 32 rows it
 //   1. loads each row straight from HBM (lane l: row l % 32, contiguous columns
 //      of half l / 32), forms ‖x‖² and the augmented k-chunk in registers;
-//   2. runs the E-GEMM T = W'·φᵀ (components x rows) with the augmented chunk,
-//      which yields the log2 logits directly (see em_sph_bf16.hip);
+//   2. runs the E-GEMM P = x·μ - ‖x‖²/2 + C'_k of the exact bf16 rows and means
+//      (fp32 accumulation, the last two terms through the augmented chunk), and
+//      scales it to the log2 logits l = s_k·P with s_k = log2(e)/σ²_k in fp32;
 //   3. takes the row maximum m, and subtracts it with one more rank-1 MFMA
 //      (m split into three bf16 parts, so the shift is exact) instead of one
 //      VALU subtraction per element; then e = 2^(l - m), s = Σ e, r = e / s;
@@ -28,7 +29,6 @@ namespace gx {
 
 namespace {
 
-constexpr int kAug = 32;       // augmented constants per component in the w_aug buffer
 constexpr float kHuge = 1e30f;
 constexpr int kWaves = kFusedWaves;   // waves per workgroup
 
@@ -90,7 +90,7 @@ void sph_bf16_fused_kernel(TileArgs a) {
   constexpr int JP = DP + 16;                   // statistics columns
   // LDS strides (bf16); s = stride / 2 dwords ≡ 8 or 24 (mod 32) keeps the
   // 16-byte accesses and the transposing reads free of bank conflicts.
-  constexpr int WS = 2 * DP + 16;               // [W' hi | W' lo | augmented constants 0..15]
+  constexpr int WS = DP + 16;                   // [μ | scaled augmented constants 0..15]
   constexpr int XS = DP <= 32 ? 80 : 112;       // [x | augmented columns 0..31]
   constexpr int RS = KC <= 32 ? 48 : 80;        // r row
   static_assert(DP + 32 <= XS && KC <= RS, "staging strides");
@@ -101,6 +101,7 @@ void sph_bf16_fused_kernel(TileArgs a) {
   static_assert(KC * JP * 2 <= kPool, "combine buffer");
   __shared__ __align__(16) __bf16 pool[kPool];
   __shared__ double llw[kWaves];
+  __shared__ __align__(16) float scs[KC];       // s_k = log2(e)/σ²_k (1 for the padding slots)
   __bf16* const ws = pool;
   __bf16* const xs_all = pool + KC * WS;
   __bf16* const rs_all = xs_all + kWaves * 32 * XS;
@@ -109,23 +110,24 @@ void sph_bf16_fused_kernel(TileArgs a) {
   const int lr = lane % 32, hf = lane / 32;     // data row / component of the tile; k half
   const int b = blockIdx.y;
 
-  // Stage the component operands once per workgroup. Slots past K get W' = 0
-  // and C = -1e30 (augmented column 6), so their responsibilities are 0.
+  // Stage the component operands once per workgroup. Slots past K get μ = 0,
+  // s = 1 and C' = -1e30 (augmented column 6), so their responsibilities are 0.
   constexpr int WCH = WS / 8;
   for (int i = threadIdx.x; i < KC * WCH; i += 64 * kWaves) {
     const int kk = i / WCH, c = i % WCH;
     uint4 v = make_uint4(0u, 0u, 0u, 0u);
     if (kk < a.K) {
       const size_t bk = (size_t)b * a.K + kk;
-      const __bf16* src = c < DP / 8   ? reinterpret_cast<const __bf16*>(a.w_hi) + bk * DP + 8 * c
-                          : c < DP / 4 ? reinterpret_cast<const __bf16*>(a.w_lo) + bk * DP + 8 * (c - DP / 8)
-                                       : reinterpret_cast<const __bf16*>(a.w_aug) + bk * kAug + 8 * (c - DP / 4);
+      const __bf16* src = c < DP / 8 ? reinterpret_cast<const __bf16*>(a.w_mu) + bk * DP + 8 * c
+                                     : reinterpret_cast<const __bf16*>(a.w_augs) + bk * 16 + 8 * (c - DP / 8);
       v = ld16<uint4>(src);
-    } else if (c == DP / 4) {
+    } else if (c == DP / 8) {
       v.w = pack2((__bf16)(-kHuge), (__bf16)0.f);   // augmented elements 6 and 7
     }
     *reinterpret_cast<uint4*>(ws + kk * WS + 8 * c) = v;
   }
+  for (int kk = threadIdx.x; kk < KC; kk += 64 * kWaves)
+    scs[kk] = kk < a.K ? a.w_scale[(size_t)b * a.K + kk] : 1.f;
   __syncthreads();
 
   // Wave-uniform: keeps the row bookkeeping in scalar registers. A wave past the
@@ -246,17 +248,23 @@ void sph_bf16_fused_kernel(TileArgs a) {
     if (hf == 0) *reinterpret_cast<uint4*>(row + DP) = w0;
 
     // E-GEMM: lane l, register v of tile t holds component 32t + 8(v/4) + 4hf + v%4 of row lr.
+    // The products of the exact bf16 rows and means accumulate in fp32 after the
+    // augmented chunk's -‖x‖²/2 + C'; one fp32 multiply per element scales P to l.
     f32x16 T[KT];
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
       const __bf16* wt = wl + 32 * t * WS;
-      T[t] = mfma32(ld16<bf16x8>(wt + 2 * DP + 8 * hf), phia, f32x16{});
+      T[t] = mfma32(ld16<bf16x8>(wt + DP + 8 * hf), phia, f32x16{});
 #pragma unroll
-      for (int s = 0; s < XK; ++s) {
-        const bf16x8 xv = __builtin_bit_cast(bf16x8, cur[s]);
-        const int c = 8 * (hf * XK + s);
-        T[t] = mfma32(ld16<bf16x8>(wt + c), xv, T[t]);
-        T[t] = mfma32(ld16<bf16x8>(wt + DP + c), xv, T[t]);
+      for (int s = 0; s < XK; ++s)
+        T[t] = mfma32(ld16<bf16x8>(wt + 8 * (hf * XK + s)), __builtin_bit_cast(bf16x8, cur[s]), T[t]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 sc = *reinterpret_cast<const float4*>(scs + 32 * t + 8 * j + 4 * hf);
+        T[t][4 * j] *= sc.x;
+        T[t][4 * j + 1] *= sc.y;
+        T[t][4 * j + 2] *= sc.z;
+        T[t][4 * j + 3] *= sc.w;
       }
     }
 

@@ -16,6 +16,9 @@ struct TileArgs {
   const void* w_hi;            // [B][K][EP] E-step operand (bf16 hi or fp32)
   const void* w_lo;            // [B][K][EP] bf16 lo part (bf16 path only)
   const void* w_aug;           // [B][K][32] bf16 augmented constants (spherical bf16 path)
+  const void* w_mu;            // [B][K][DP] bf16 means (fused kernel)
+  const float* w_scale;        // [B][K] log2(e)/σ², the factor of x·μ (fused kernel)
+  const void* w_augs;          // [B][K][16] bf16 [-½ -½ -½ 0 0 0 C'_h C'_m | C'_l 0 ...] (fused kernel)
   const float4* cconst;        // [B][K] (A, C, 0, 0): l2 = A*(rowq - 2S) + C (spherical, tied) or A*S + C
   const float* rowq;           // [B][N] tied: xᵀPx
   const float* lse2;           // [B][N] log2-domain log-normaliser (STATS / PROBA)

@@ -132,11 +132,30 @@ __global__ __launch_bounds__(64) void prep_kernel(PrepArgs a) {
       const __bf16 cl = (__bf16)(cy - (float)ch - (float)cm);
       const __bf16 vals[9] = {ah, ah, ah, am, am, al, ch, cm, cl};
       if (lane < 32) reinterpret_cast<__bf16*>(a.w_aug)[bk * 32 + lane] = lane < 9 ? vals[lane] : (__bf16)0.f;
-      // Cooperative pass: the exact bf16 means and the factor -2·ca, applied to
+      // Cooperative and fused passes: the exact bf16 means and the factor -2·ca, applied to
       // the fp32 product x·μ after the MFMA (no hi/lo split of the operand).
       if (a.w_mu) {
         for (int e = lane; e < DP; e += 64) reinterpret_cast<__bf16*>(a.w_mu)[bk * DP + e] = (__bf16)(e < D ? mus[e] : 0.f);
         if (lane == 0) a.w_scale[bk] = -2.f * ca;
+      }
+      // Fused pass: one accumulator chain P = x·μ - ‖x‖²/2 + C' and l2 = s·P, with
+      // s = -2·ca and C' = C / s = -‖μ‖²/2 + (log w - ½ D log(2πσ²))·σ² (float64,
+      // from the bf16 means the product uses): [-½ -½ -½ 0 0 0 C'_h C'_m | C'_l 0 ...].
+      if (a.w_augs) {
+        double mb64 = 0.0;
+        for (int d = lane; d < D; d += 64) {
+          const double mb = (double)(float)(__bf16)mus[d];
+          mb64 = fma(mb, mb, mb64);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off /= 2) mb64 += __shfl_xor(mb64, off);
+        const double cp = -0.5 * mb64 + ((double)lw - 0.5 * (double)D * (kLog2Pi + log((double)var))) * (double)var;
+        const __bf16 ph = (__bf16)(float)cp;
+        const __bf16 pm = (__bf16)(float)(cp - (double)(float)ph);
+        const __bf16 pl = (__bf16)(float)(cp - (double)(float)ph - (double)(float)pm);
+        const __bf16 half = (__bf16)(-0.5f), zero = (__bf16)0.f;
+        const __bf16 vals[9] = {half, half, half, zero, zero, zero, ph, pm, pl};
+        if (lane < 16) reinterpret_cast<__bf16*>(a.w_augs)[bk * 16 + lane] = lane < 9 ? vals[lane] : zero;
       }
     } else {
       for (int e = lane; e < EP; e += 64) put_f32(e, e < D ? mus[e] : 0.f);

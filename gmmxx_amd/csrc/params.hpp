@@ -22,8 +22,9 @@ struct PrepArgs {
   void* w_hi;              // [B][K][EP]
   void* w_lo;              // [B][K][EP] (bf16 path)
   void* w_aug;             // [B][K][32] (spherical bf16 path)
-  void* w_mu;              // [B][K][DP] spherical bf16 cooperative pass: the bf16 means (or null)
+  void* w_mu;              // [B][K][DP] spherical bf16 cooperative and fused passes: the bf16 means (or null)
   float* w_scale;          // [B][K] with w_mu: log2(e)/σ², the factor of the product x·μ
+  void* w_augs;            // [B][K][16] fused pass: the augmented constants divided by that factor (or null)
   float4* cconst;          // [B][K]
   const float* gram;       // tied EM: XᵀX [B][D][D] (or null)
   double* shift;           // with gram: [B][D] row terms -½ Σ_j P_rj (XᵀX)_rj

@@ -12,7 +12,7 @@ and is computed by the bf16 engine.  Its means are bf16, as the reference keeps
 them in x's dtype (torch_fallback.py:1451, :2295): the initial means and every
 M-step's means are rounded to bf16 (stored in fp32 tensors), while variances
 and weights stay fp32.  The E-step multiplies exact bf16 x by the bf16 means
-with fp32 accumulation (the cooperative kernel; the two-pass kernels use a
+with fp32 accumulation (the cooperative and fused kernels; the two-pass kernels use a
 hi + lo bf16 split of the fp32 operand -2·μ/σ², about 16 significand bits), and
 the responsibilities are rounded to bf16 before the M-step product -- more
 accurate than the reference's bf16 arithmetic on the same input, but not the
