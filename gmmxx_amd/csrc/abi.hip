@@ -272,8 +272,8 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.o_prec = take(q.fw ? 0 : (size_t)q.chol_m * q.D * q.D * 4);
   q.o_logdet = take((size_t)q.chol_m * 4);
   q.o_gram = take(q.cov == TIED ? (size_t)q.gram_slices * q.B * q.D * q.D * 4 : 0);
-  q.o_lpack = take(q.fw ? (size_t)fw_lpack_floats(q.B, q.K, q.DP) * 4 : 0);
-  q.o_lpaug = take(q.fw ? BK * (q.DP / 32) * 64 * 4 : 0);
+  q.o_lpack = take(q.fw ? (size_t)fw_lpack_bytes(q.B, q.K, q.DP) : 0);
+  q.o_lpaug = take(q.fw ? BK * (q.DP / 32) * 64 * 8 * 2 : 0);
   q.o_l2w = take(q.fw ? BK * (size_t)q.N * 4 : 0);
   q.o_linv = take((q.fw || q.w16) ? BK * q.D * q.D * 4 : 0);
   q.o_w16parts = take(q.w16 ? BK * 3 * 512 * 2 : 0);   // three 1 KB MFMA operands per component
@@ -437,8 +437,8 @@ FwArgs fw_args(const Plan& pl, const void* x, void* ws) {
   a.D = pl.D;
   a.K = pl.K;
   a.B = pl.B;
-  a.lpack = at<float>(ws, pl.o_lpack);
-  a.lpaug = at<float>(ws, pl.o_lpaug);
+  a.lpack = at<void>(ws, pl.o_lpack);
+  a.lpaug = at<void>(ws, pl.o_lpaug);
   a.cconst = at<float4>(ws, pl.o_cconst);
   a.l2 = at<float>(ws, pl.o_l2w);
   a.lse2 = at<float>(ws, pl.o_lse2);
@@ -517,8 +517,8 @@ int prepare(const Plan& pl, const void* x, const float* means, const float* covs
     f.weights = weights;
     f.linv = at<float>(ws, pl.o_linv);
     f.logdet = logdet;
-    f.lpack = at<float>(ws, pl.o_lpack);
-    f.lpaug = at<float>(ws, pl.o_lpaug);
+    f.lpack = at<void>(ws, pl.o_lpack);
+    f.lpaug = at<void>(ws, pl.o_lpaug);
     f.cconst = at<float4>(ws, pl.o_cconst);
     launch_fw_pack(f, s);
     return check_hip("parameter preparation");

@@ -1,5 +1,6 @@
-// Full covariance at 16 < D <= 128: whitening E-step and weighted-Gram M-step
-// on the fp32 MFMA (v_mfma_f32_32x32x2_f32).
+// Full covariance at 16 < D <= 128: whitening E-step on the bf16 MFMA with
+// split operands (v_mfma_f32_32x32x16_bf16) and weighted-Gram M-step on the fp32
+// MFMA (v_mfma_f32_32x32x2_f32).
 //
 // The augmented formulation of em_tile.hip (features = the D(D+1)/2 products
 // x_d x_e, split into bf16 parts) is built for D = 16; at larger D its feature
@@ -12,16 +13,20 @@
 // (:3143-3167).
 //
 //   fw_pack_kernel   per component: the iteration prelude's weight, b = L⁻¹μ and
-//                    the log2 constant in float64, and L⁻¹ laid out as the MFMA's
-//                    A operand (one 16-deep chunk = 64 lanes x 16 floats);
-//   fw_estep_kernel  one wave per 32-row block, every component in turn: the
+//                    the log2 constant in float64, and L⁻¹ split into three bf16
+//                    parts (v = v1 + v2 + v3 exactly) laid out as the MFMA's A
+//                    operand (one 16-deep chunk = 3 parts x 64 lanes x 8 values);
+//   fw_estep_kernel  one wave per 32-row block, its rows split into three bf16
+//                    parts as the B operand, every component in turn: the
 //                    32 x 32 output tiles of y = L⁻¹x (rows i of L⁻¹ against the
 //                    block's rows, k over x's columns; L⁻¹ is lower triangular, so
-//                    tile t needs only chunks c <= t), one more rank-1 MFMA adds
-//                    -b, and each lane sums the squares of its 16 entries; the
-//                    partner lane (l ^ 32) holds the other 16.  The row's
-//                    log-normaliser is accumulated online over the components;
-//                    the log2 logits go to a (B, K, N) buffer;
+//                    tile t needs only the 16-deep chunks c <= 2t + 1), each
+//                    product as the six bf16 MFMAs a1b3 + a3b1 + a2b2 + a1b2 +
+//                    a2b1 + a1b1 (the dropped terms are below 2⁻²⁴ relative), one
+//                    more MFMA adds -b from its three parts, and each lane sums the
+//                    squares of its 16 entries; the partner lane (l ^ 32) holds the
+//                    other 16.  The row's log-normaliser is accumulated online over
+//                    the components; the log2 logits go to a (B, K, N) buffer;
 //   fw_stats_kernel  one wave per component and row slice: Σ_n r_n x_n x_nᵀ as
 //                    the lower tiles of (r ⊙ X)ᵀ X over 2-row k-steps, Σ r x and
 //                    Σ r beside it on the VALU, r = 2^(l2 - lse2) from the
@@ -30,8 +35,9 @@
 //                    the logits themselves, for the top-k selection).
 //
 // 32x32x2 fp32 MFMA operand layout: lane l supplies A[i = l % 32][k = l / 32]
-// and B[k = l / 32][j = l % 32]; accumulator register v of lane l holds
-// C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+// and B[k = l / 32][j = l % 32]; 32x32x16 bf16: lane l supplies A[i = l % 32]
+// [k = 8 (l / 32) .. +7] and B[k = 8 (l / 32) .. +7][j = l % 32]; in both,
+// accumulator register v of lane l holds C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
 
 #include <math.h>
 
@@ -45,10 +51,26 @@ namespace gx {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f32x16 mfma32f(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x16 mfma32b(bf16x8v a, bf16x8v b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v = p1 + p2 + p3 exactly (three bf16 parts, each rounded to nearest even).
+__device__ __forceinline__ void split3v(f32x8 v, bf16x8v& p1, bf16x8v& p2, bf16x8v& p3) {
+  p1 = __builtin_convertvector(v, bf16x8v);
+  const f32x8 r1 = v - __builtin_convertvector(p1, f32x8);
+  p2 = __builtin_convertvector(r1, bf16x8v);
+  p3 = __builtin_convertvector(r1 - __builtin_convertvector(p2, f32x8), bf16x8v);
+}
+
+// Bytes of one 16-deep L⁻¹ chunk: three parts x 64 lanes x 8 bf16.
+constexpr int kChunkBytes = 3 * 64 * 8 * 2;
 
 // v of lane l % 32 plus v of lane l % 32 + 32, the same bits in both lanes
 // (the swap yields the low half's value in one word and the high half's in the
@@ -70,7 +92,7 @@ __global__ __launch_bounds__(256) void fw_pack_kernel(FwPackArgs a) {
   __shared__ double red[4];
   __shared__ double bsh[128];
   const int k = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
-  const int K = a.K, D = a.D, DP = a.DP, NT = DP / 32, NCH = NT * (NT + 1) / 2;
+  const int K = a.K, D = a.D, DP = a.DP, NT = DP / 32, NCH = NT * (NT + 1);   // 16-deep chunks
   const size_t bk = (size_t)b * K + k;
   // Iteration prelude (torch_fallback.py:2061-2066): w <- max(w, min_weight) / Σ;
   // inference uses the weights as given.
@@ -96,11 +118,22 @@ __global__ __launch_bounds__(256) void fw_pack_kernel(FwPackArgs a) {
     bsh[t] = acc;
   }
   __syncthreads();
+  // -b as the A operand of one 32x32x16 MFMA against ones in k = 0..2: lane
+  // l < 32 of tile tt holds the three parts of -b[32 tt + l] in k = 0..2.
   if (t < 64) {
-    float* aug = a.lpaug + bk * NT * 64;
+    __bf16* aug = reinterpret_cast<__bf16*>(a.lpaug) + (bk * NT) * 512;
     for (int tt = 0; tt < NT; ++tt) {
       const int i = 32 * tt + (t & 31);
-      aug[tt * 64 + t] = (t < 32 && i < D) ? (float)(-bsh[i]) : 0.f;
+      const float v = (t < 32 && i < D) ? (float)(-bsh[i]) : 0.f;
+      const __bf16 p1 = (__bf16)v;
+      const float r1 = v - (float)p1;
+      const __bf16 p2 = (__bf16)r1;
+      const __bf16 p3 = (__bf16)(r1 - (float)p2);
+      __bf16* dst = aug + (tt * 64 + t) * 8;
+      dst[0] = p1;
+      dst[1] = p2;
+      dst[2] = p3;
+      for (int e = 3; e < 8; ++e) dst[e] = (__bf16)0.f;
     }
   }
   if (t == 0) {
@@ -108,16 +141,23 @@ __global__ __launch_bounds__(256) void fw_pack_kernel(FwPackArgs a) {
     const double c2 = (log((double)wk) - 0.5 * ((double)D * kLog2Pi + (double)a.logdet[bk])) * kLog2eD;
     a.cconst[bk] = make_float4((float)c2, 0.f, 0.f, 0.f);
   }
-  // chunk j = (tile tt, column chunk c), j = tt (tt + 1) / 2 + c; lane l, slot u:
-  // L⁻¹[32 tt + l % 32][32 c + 16 (l / 32) + u]
-  float* lp = a.lpack + bk * NCH * 1024;
-  for (int e = t; e < NCH * 1024; e += 256) {
-    const int j = e >> 10, lane = (e >> 4) & 63, u = e & 15;
+  // chunk j = (tile tt, 16-column chunk c <= 2 tt + 1), j = tt (tt + 1) + c;
+  // part p, lane l, slot u: part p of L⁻¹[32 tt + l % 32][16 c + 8 (l / 32) + u]
+  __bf16* lp = reinterpret_cast<__bf16*>(a.lpack) + bk * NCH * (kChunkBytes / 2);
+  for (int e = t; e < NCH * 512; e += 256) {
+    const int j = e >> 9, lane = (e >> 3) & 63, u = e & 7;
     int tt = 0;
-    while ((tt + 1) * (tt + 2) / 2 <= j) ++tt;
-    const int c = j - tt * (tt + 1) / 2;
-    const int i = 32 * tt + (lane & 31), col = 32 * c + 16 * (lane >> 5) + u;
-    lp[e] = (i < D && col < D) ? X[i * D + col] : 0.f;
+    while ((tt + 1) * (tt + 2) <= j) ++tt;
+    const int c = j - tt * (tt + 1);
+    const int i = 32 * tt + (lane & 31), col = 16 * c + 8 * (lane >> 5) + u;
+    const float v = (i < D && col < D) ? X[i * D + col] : 0.f;
+    const __bf16 p1 = (__bf16)v;
+    const float r1 = v - (float)p1;
+    const __bf16 p2 = (__bf16)r1;
+    __bf16* dst = lp + (size_t)j * (kChunkBytes / 2) + lane * 8 + u;
+    dst[0] = p1;
+    dst[512] = p2;
+    dst[1024] = (__bf16)(r1 - (float)p2);
   }
 }
 
@@ -127,7 +167,7 @@ __global__ __launch_bounds__(256) void fw_pack_kernel(FwPackArgs a) {
 
 template <int DP>
 __global__ __launch_bounds__(64 * kFwWaves) void fw_estep_kernel(FwArgs a) {
-  constexpr int NT = DP / 32, NCH = NT * (NT + 1) / 2;
+  constexpr int NT = DP / 32, NCH = NT * (NT + 1), XC = DP / 16;
   __shared__ double llw[kFwWaves];
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane & 31, h = lane >> 5;
   const int b = blockIdx.y;
@@ -137,63 +177,67 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_estep_kernel(FwArgs a) {
   const int64_t n = n0 + lr;
   const bool valid = n < N;
 
-  // x block as the B operand: lane l holds row n, columns 32 c + 16 h + u.
-  float xr[NT][16];
+  // x block as the B operand in three bf16 parts: lane l holds row n, columns
+  // 16 c + 8 h + u (u = 0..7) of 16-column chunk c.
+  bf16x8v x1[XC], x2[XC], x3[XC];
   {
     const float* xrow = a.x + ((size_t)b * N + (valid ? n : 0)) * D;
 #pragma unroll
-    for (int c = 0; c < NT; ++c) {
-      const int col0 = 32 * c + 16 * h;
+    for (int c = 0; c < XC; ++c) {
+      const int col0 = 16 * c + 8 * h;
+      f32x8 v;
       if (a.vec_ok) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 v = valid ? *reinterpret_cast<const f32x4*>(xrow + col0 + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xr[c][4 * q + r] = v[r];
-        }
+        const f32x4 lo = valid ? *reinterpret_cast<const f32x4*>(xrow + col0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 hi = valid ? *reinterpret_cast<const f32x4*>(xrow + col0 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       } else {
 #pragma unroll
-        for (int u = 0; u < 16; ++u) xr[c][u] = (valid && col0 + u < D) ? xrow[col0 + u] : 0.f;
+        for (int u = 0; u < 8; ++u) v[u] = (valid && col0 + u < D) ? xrow[col0 + u] : 0.f;
       }
+      split3v(v, x1[c], x2[c], x3[c]);
     }
   }
-  const float one = h == 0 ? 1.f : 0.f;
+  // B operand of the -b step: ones in k = 0..2.
+  bf16x8v ones;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) ones[u] = (__bf16)((h == 0 && u < 3) ? 1.f : 0.f);
 
   // L⁻¹ chunks stream through a one-chunk prefetch; the buffer holds one spare
   // chunk after the last component, so the final prefetch stays in bounds.
-  const float* lp = a.lpack + (size_t)b * K * NCH * 1024 + lane * 16;
-  f32x4 nx[4];
+  const char* lp = reinterpret_cast<const char*>(a.lpack) + (size_t)b * K * NCH * kChunkBytes + lane * 16;
+  const bf16x8v* augp = reinterpret_cast<const bf16x8v*>(a.lpaug) + (size_t)b * K * NT * 64 + lane;
+  bf16x8v nx[3];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) nx[q] = *reinterpret_cast<const f32x4*>(lp + 4 * q);
+  for (int p = 0; p < 3; ++p) nx[p] = *reinterpret_cast<const bf16x8v*>(lp + p * 1024);
 
   float m = -INFINITY, s = 0.f, best = -INFINITY;
   int bidx = 0;
   for (int k = 0; k < K; ++k) {
     const size_t bk = (size_t)b * K + k;
-    float augv[NT];
+    bf16x8v augv[NT];
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt) augv[tt] = a.lpaug[(bk * NT + tt) * 64 + lane];
+    for (int tt = 0; tt < NT; ++tt) augv[tt] = augp[((size_t)k * NT + tt) * 64];
     float q = 0.f;
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
-      // two accumulators (even and odd k-steps), so consecutive MFMAs do not
-      // depend on each other
-      f32x16 acc = f32x16{}, acc2 = f32x16{};
+      // two accumulators, so consecutive MFMAs do not depend on each other; the
+      // products of a chunk go smallest first
+      f32x16 acc = mfma32b(augv[tt], ones, f32x16{}), acc2 = f32x16{};
 #pragma unroll
-      for (int c = 0; c <= tt; ++c) {
-        f32x4 cur[4];
+      for (int c = 0; c <= 2 * tt + 1; ++c) {
+        bf16x8v cur[3];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cur[r] = nx[r];
-        lp += 1024;
+        for (int p = 0; p < 3; ++p) cur[p] = nx[p];
+        lp += kChunkBytes;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) nx[r] = *reinterpret_cast<const f32x4*>(lp + 4 * r);
-#pragma unroll
-        for (int u = 0; u < 16; u += 2) {
-          acc = mfma32f(cur[u / 4][u % 4], xr[c][u], acc);
-          acc2 = mfma32f(cur[u / 4][u % 4 + 1], xr[c][u + 1], acc2);
-        }
+        for (int p = 0; p < 3; ++p) nx[p] = *reinterpret_cast<const bf16x8v*>(lp + p * 1024);
+        acc2 = mfma32b(cur[0], x3[c], acc2);
+        acc = mfma32b(cur[2], x1[c], acc);
+        acc2 = mfma32b(cur[1], x2[c], acc2);
+        acc = mfma32b(cur[0], x2[c], acc);
+        acc2 = mfma32b(cur[1], x1[c], acc2);
+        acc = mfma32b(cur[0], x1[c], acc);
       }
-      acc2 = mfma32f(augv[tt], one, acc2);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const float y = acc[v] + acc2[v];
@@ -281,6 +325,51 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
     }
     const float* xblk = xb + (size_t)n0 * D;           // the block's rows, 32-bit offsets below
     const int nrows = (int)((r1 - n0) < 32 ? (r1 - n0) : 32);
+    if constexpr (DP <= 64) {
+      // Split bf16 operands, 16 rows per k-step: lane (lr, h) holds rows 8h .. 8h+7
+      // of the step at dims 32c + lr; B = those x values, A = z = r·x, each split
+      // into three parts, and the six products of every lower tile go smallest
+      // first (consecutive MFMAs into different tiles).  (The two steps stay a
+      // loop: unrolled, their operands are live at once.)
+#pragma unroll 1
+      for (int s0 = 0; s0 < 32; s0 += 16) {
+        f32x8 rr, xv[NT];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int src = s0 + 8 * h + e;
+          rr[e] = __shfl(rv, src);
+          const bool rowok = src < nrows;
+#pragma unroll
+          for (int c = 0; c < NT; ++c) {
+            const int col = 32 * c + lr;
+            xv[c][e] = (rowok && col < D) ? xblk[src * D + col] : 0.f;
+          }
+        }
+        bf16x8v x1[NT], x2[NT], x3[NT], z1[NT], z2[NT], z3[NT];
+#pragma unroll
+        for (int c = 0; c < NT; ++c) {
+          split3v(xv[c], x1[c], x2[c], x3[c]);
+          const f32x8 z = xv[c] * rr;
+          sx[c] += ((z[0] + z[1]) + (z[2] + z[3])) + ((z[4] + z[5]) + (z[6] + z[7]));
+          split3v(z, z1[c], z2[c], z3[c]);
+        }
+        sr += ((rr[0] + rr[1]) + (rr[2] + rr[3])) + ((rr[4] + rr[5]) + (rr[6] + rr[7]));
+        auto products = [&](const bf16x8v (&za)[NT], const bf16x8v (&xb_)[NT]) {
+          int ti = 0;
+#pragma unroll
+          for (int I = 0; I < NT; ++I)
+#pragma unroll
+            for (int J = 0; J <= I; ++J, ++ti) acc[ti] = mfma32b(za[I], xb_[J], acc[ti]);
+        };
+        products(z1, x3);
+        products(z3, x1);
+        products(z2, x2);
+        products(z1, x2);
+        products(z2, x1);
+        products(z1, x1);
+      }
+      continue;
+    }
     // (unrolled four k-steps deep: all sixteen measured slower at DP 32 and 64)
 #pragma unroll 4
     for (int st = 0; st < 16; ++st) {
@@ -359,9 +448,9 @@ __global__ __launch_bounds__(256) void fw_proba_kernel(const float* l2, const fl
 // Launchers
 // ---------------------------------------------------------------------------
 
-int64_t fw_lpack_floats(int B, int K, int DP) {
+int64_t fw_lpack_bytes(int B, int K, int DP) {
   const int NT = DP / 32;
-  return ((int64_t)B * K * (NT * (NT + 1) / 2) + 1) * 1024;
+  return ((int64_t)B * K * (NT * (NT + 1)) + 1) * kChunkBytes;
 }
 
 int fw_eblocks(int64_t N) { return (int)((N + 32 * kFwWaves - 1) / (32 * kFwWaves)); }

@@ -105,8 +105,8 @@ struct FwPackArgs {
   const float* weights;        // [B][K]
   const float* linv;           // [B][K][D][D] L^-1 (lower triangular)
   const float* logdet;         // [B][K]
-  float* lpack;                // fw_lpack_floats(B, K, DP): L^-1 as MFMA A-operand chunks
-  float* lpaug;                // [B][K][DP/32][64] -L^-1 μ (lanes 0..31 of each tile)
+  void* lpack;                 // fw_lpack_bytes(B, K, DP): L^-1 as bf16 MFMA A-operand chunks (three parts)
+  void* lpaug;                 // [B][K][DP/32][64][8] bf16: -L^-1 μ in three parts (lanes 0..31 of each tile)
   float4* cconst;              // [B][K] (log2 w - ½ log2(e) (D log 2π + log det), 0, 0, 0)
 };
 struct FwArgs {
@@ -114,8 +114,8 @@ struct FwArgs {
   int vec_ok;                  // D == DP and x 16-byte aligned
   int64_t N;
   int D, K, B;
-  const float* lpack;
-  const float* lpaug;
+  const void* lpack;
+  const void* lpaug;
   const float4* cconst;
   float* l2;                   // [B][K][N] log2 logits (E-step output, statistics input), or null
   float* lse2;                 // [B][N] log2 row log-normalisers
@@ -136,7 +136,7 @@ struct FwArgs {
   const float* thr2;           // [B][N] or null
   const int* thr_idx;          // [B][N]
 };
-int64_t fw_lpack_floats(int B, int K, int DP);
+int64_t fw_lpack_bytes(int B, int K, int DP);
 int fw_eblocks(int64_t N);
 void launch_fw_pack(const FwPackArgs& a, hipStream_t s);
 // phase 0: the E-step over fw_eblocks(N) x B workgroups; 1: the statistics over
