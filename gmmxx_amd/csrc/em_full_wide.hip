@@ -327,17 +327,20 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
     const int nrows = (int)((r1 - n0) < 32 ? (r1 - n0) : 32);
     if constexpr (DP <= 64) {
       // Split bf16 operands, 16 rows per k-step: lane (lr, h) holds rows 8h .. 8h+7
-      // of the step at dims 32c + lr; B = those x values, A = z = r·x, each split
-      // into three parts, and the six products of every lower tile go smallest
-      // first (consecutive MFMAs into different tiles).  (The two steps stay a
-      // loop: unrolled, their operands are live at once.)
+      // of the step at dims 32c + lr.  Σ r x xᵀ = Σ w wᵀ with w = √r·x, so one
+      // three-way split of w is both the A and the B operand (Σ r x = Σ √r·w);
+      // the six products of every lower tile go smallest first (consecutive
+      // MFMAs into different tiles).  (The two steps stay a loop: unrolled, their
+      // operands are live at once.)
 #pragma unroll 1
       for (int s0 = 0; s0 < 32; s0 += 16) {
-        f32x8 rr, xv[NT];
+        f32x8 sq, xv[NT];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int src = s0 + 8 * h + e;
-          rr[e] = __shfl(rv, src);
+          const float r = __shfl(rv, src);
+          sr += r;
+          sq[e] = __builtin_amdgcn_sqrtf(r);
           const bool rowok = src < nrows;
 #pragma unroll
           for (int c = 0; c < NT; ++c) {
@@ -345,28 +348,27 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
             xv[c][e] = (rowok && col < D) ? xblk[src * D + col] : 0.f;
           }
         }
-        bf16x8v x1[NT], x2[NT], x3[NT], z1[NT], z2[NT], z3[NT];
+        bf16x8v w1[NT], w2[NT], w3[NT];
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
-          split3v(xv[c], x1[c], x2[c], x3[c]);
-          const f32x8 z = xv[c] * rr;
-          sx[c] += ((z[0] + z[1]) + (z[2] + z[3])) + ((z[4] + z[5]) + (z[6] + z[7]));
-          split3v(z, z1[c], z2[c], z3[c]);
+          const f32x8 w = xv[c] * sq;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sx[c] = fmaf(sq[e], w[e], sx[c]);
+          split3v(w, w1[c], w2[c], w3[c]);
         }
-        sr += ((rr[0] + rr[1]) + (rr[2] + rr[3])) + ((rr[4] + rr[5]) + (rr[6] + rr[7]));
-        auto products = [&](const bf16x8v (&za)[NT], const bf16x8v (&xb_)[NT]) {
+        auto products = [&](const bf16x8v (&pa)[NT], const bf16x8v (&pb)[NT]) {
           int ti = 0;
 #pragma unroll
           for (int I = 0; I < NT; ++I)
 #pragma unroll
-            for (int J = 0; J <= I; ++J, ++ti) acc[ti] = mfma32b(za[I], xb_[J], acc[ti]);
+            for (int J = 0; J <= I; ++J, ++ti) acc[ti] = mfma32b(pa[I], pb[J], acc[ti]);
         };
-        products(z1, x3);
-        products(z3, x1);
-        products(z2, x2);
-        products(z1, x2);
-        products(z2, x1);
-        products(z1, x1);
+        products(w1, w3);
+        products(w3, w1);
+        products(w2, w2);
+        products(w1, w2);
+        products(w2, w1);
+        products(w1, w1);
       }
       continue;
     }

@@ -96,7 +96,8 @@ int coop_capacity();
 int launch_sph_bf16_coop(int dp, const CoopArgs& a, hipStream_t s);
 
 // Full covariance at 16 < D <= 128 (em_full_wide.hip): whitening E-step and
-// weighted-Gram statistics on the fp32 MFMA, DP in {32, 64, 128}.
+// weighted-Gram statistics on split-bf16 MFMA operands (the statistics at DP = 128
+// on the fp32 MFMA), DP in {32, 64, 128}.
 struct FwPackArgs {
   int B, K, D, DP, prelude;
   int param_round;             // 1 bf16, 2 fp16: the prelude's normalised weights kept in that dtype
