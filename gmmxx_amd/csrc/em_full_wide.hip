@@ -1,6 +1,6 @@
-// Full covariance at 16 < D <= 128: whitening E-step on the bf16 MFMA with
-// split operands (v_mfma_f32_32x32x16_bf16) and weighted-Gram M-step on the fp32
-// MFMA (v_mfma_f32_32x32x2_f32).
+// Full covariance at 16 < D <= 128: whitening E-step and weighted-Gram M-step
+// on the bf16 MFMA with split operands (v_mfma_f32_32x32x16_bf16: every fp32
+// operand as three bf16 parts, six bf16 products per fp32 product).
 //
 // The augmented formulation of em_tile.hip (features = the D(D+1)/2 products
 // x_d x_e, split into bf16 parts) is built for D = 16; at larger D its feature
@@ -27,17 +27,18 @@
 //                    squares of its 16 entries; the partner lane (l ^ 32) holds the
 //                    other 16.  The row's log-normaliser is accumulated online over
 //                    the components; the log2 logits go to a (B, K, N) buffer;
-//   fw_stats_kernel  one wave per component and row slice: Σ_n r_n x_n x_nᵀ as
-//                    the lower tiles of (r ⊙ X)ᵀ X over 2-row k-steps, Σ r x and
-//                    Σ r beside it on the VALU, r = 2^(l2 - lse2) from the
-//                    E-step's buffers;
+//   fw_stats_kernel  one wave per component and row slice (D = 128:
+//                    fw_stats128_kernel, two waves of five tiles each):
+//                    Σ_n r_n x_n x_nᵀ = Σ w wᵀ with w = √r·x as the lower 32 x 32
+//                    tiles over 16-row k-steps, one split of w serving as both
+//                    operands; Σ r x and Σ r beside it on the VALU,
+//                    r = 2^(l2 - lse2) from the E-step's buffers;
 //   fw_proba_kernel  predict_proba: r = 2^(l2 - lse2) transposed to (B, N, K) (or
 //                    the logits themselves, for the top-k selection).
 //
-// 32x32x2 fp32 MFMA operand layout: lane l supplies A[i = l % 32][k = l / 32]
-// and B[k = l / 32][j = l % 32]; 32x32x16 bf16: lane l supplies A[i = l % 32]
-// [k = 8 (l / 32) .. +7] and B[k = 8 (l / 32) .. +7][j = l % 32]; in both,
-// accumulator register v of lane l holds C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+// 32x32x16 bf16 MFMA operand layout: lane l supplies A[i = l % 32]
+// [k = 8 (l / 32) .. +7] and B[k = 8 (l / 32) .. +7][j = l % 32]; accumulator
+// register v of lane l holds C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
 
 #include <math.h>
 
@@ -54,9 +55,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ f32x16 mfma32f(float a, float b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ f32x16 mfma32b(bf16x8v a, bf16x8v b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -286,6 +284,7 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_estep_kernel(FwArgs a) {
 
 template <int DP>
 __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
+  static_assert(DP <= 64, "D = 128 runs fw_stats128_kernel");
   constexpr int NT = DP / 32, NTT = NT * (NT + 1) / 2;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64, lr = lane & 31, h = lane >> 5;
   const int b = blockIdx.z;
@@ -325,73 +324,49 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
     }
     const float* xblk = xb + (size_t)n0 * D;           // the block's rows, 32-bit offsets below
     const int nrows = (int)((r1 - n0) < 32 ? (r1 - n0) : 32);
-    if constexpr (DP <= 64) {
-      // Split bf16 operands, 16 rows per k-step: lane (lr, h) holds rows 8h .. 8h+7
-      // of the step at dims 32c + lr.  Σ r x xᵀ = Σ w wᵀ with w = √r·x, so one
-      // three-way split of w is both the A and the B operand (Σ r x = Σ √r·w);
-      // the six products of every lower tile go smallest first (consecutive
-      // MFMAs into different tiles).  (The two steps stay a loop: unrolled, their
-      // operands are live at once.)
+    // Split bf16 operands, 16 rows per k-step: lane (lr, h) holds rows 8h .. 8h+7
+    // of the step at dims 32c + lr.  Σ r x xᵀ = Σ w wᵀ with w = √r·x, so one
+    // three-way split of w is both the A and the B operand (Σ r x = Σ √r·w);
+    // the six products of every lower tile go smallest first (consecutive
+    // MFMAs into different tiles).  (The two steps stay a loop: unrolled, their
+    // operands are live at once.)
 #pragma unroll 1
-      for (int s0 = 0; s0 < 32; s0 += 16) {
-        f32x8 sq, xv[NT];
+    for (int s0 = 0; s0 < 32; s0 += 16) {
+      f32x8 sq, xv[NT];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int src = s0 + 8 * h + e;
-          const float r = __shfl(rv, src);
-          sr += r;
-          sq[e] = __builtin_amdgcn_sqrtf(r);
-          const bool rowok = src < nrows;
-#pragma unroll
-          for (int c = 0; c < NT; ++c) {
-            const int col = 32 * c + lr;
-            xv[c][e] = (rowok && col < D) ? xblk[src * D + col] : 0.f;
-          }
-        }
-        bf16x8v w1[NT], w2[NT], w3[NT];
+      for (int e = 0; e < 8; ++e) {
+        const int src = s0 + 8 * h + e;
+        const float r = __shfl(rv, src);
+        sr += r;
+        sq[e] = __builtin_amdgcn_sqrtf(r);
+        const bool rowok = src < nrows;
 #pragma unroll
         for (int c = 0; c < NT; ++c) {
-          const f32x8 w = xv[c] * sq;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) sx[c] = fmaf(sq[e], w[e], sx[c]);
-          split3v(w, w1[c], w2[c], w3[c]);
+          const int col = 32 * c + lr;
+          xv[c][e] = (rowok && col < D) ? xblk[src * D + col] : 0.f;
         }
-        auto products = [&](const bf16x8v (&pa)[NT], const bf16x8v (&pb)[NT]) {
-          int ti = 0;
-#pragma unroll
-          for (int I = 0; I < NT; ++I)
-#pragma unroll
-            for (int J = 0; J <= I; ++J, ++ti) acc[ti] = mfma32b(pa[I], pb[J], acc[ti]);
-        };
-        products(w1, w3);
-        products(w3, w1);
-        products(w2, w2);
-        products(w1, w2);
-        products(w2, w1);
-        products(w1, w1);
       }
-      continue;
-    }
-    // (unrolled four k-steps deep: all sixteen measured slower at DP 32 and 64)
-#pragma unroll 4
-    for (int st = 0; st < 16; ++st) {
-      const int src = 2 * st + h;   // row of this k-step for this lane's half
-      const float r = __shfl(rv, src);
-      const bool rowok = src < nrows;
-      float xv[NT], z[NT];
+      bf16x8v w1[NT], w2[NT], w3[NT];
 #pragma unroll
       for (int c = 0; c < NT; ++c) {
-        const int col = 32 * c + lr;
-        xv[c] = (rowok && col < D) ? xblk[src * D + col] : 0.f;
-        z[c] = r * xv[c];
-        sx[c] += z[c];
+        const f32x8 w = xv[c] * sq;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sx[c] = fmaf(sq[e], w[e], sx[c]);
+        split3v(w, w1[c], w2[c], w3[c]);
       }
-      sr += r;
-      int ti = 0;
+      auto products = [&](const bf16x8v (&pa)[NT], const bf16x8v (&pb)[NT]) {
+        int ti = 0;
 #pragma unroll
-      for (int I = 0; I < NT; ++I)
+        for (int I = 0; I < NT; ++I)
 #pragma unroll
-        for (int J = 0; J <= I; ++J, ++ti) acc[ti] = mfma32f(z[I], xv[J], acc[ti]);
+          for (int J = 0; J <= I; ++J, ++ti) acc[ti] = mfma32b(pa[I], pb[J], acc[ti]);
+      };
+      products(w1, w3);
+      products(w3, w1);
+      products(w2, w2);
+      products(w1, w2);
+      products(w2, w1);
+      products(w1, w1);
     }
   }
 
@@ -415,6 +390,121 @@ __global__ __launch_bounds__(64 * kFwWaves) void fw_stats_kernel(FwArgs a) {
   const float nk = half_sum(sr);
   if (lane == 0) out[a.nk_col] = nk;
   if (lane >= 1 && a.nk_col + lane < a.JP) out[a.nk_col + lane] = 0.f;
+}
+
+// D = 128: two waves per component, each with five of the ten lower 32 x 32 tiles
+// (tile rows {0, 3} and {1, 2}), so that the accumulators and the split operands
+// of a wave fit two waves per SIMD; the same k-steps and operands as
+// fw_stats_kernel's D <= 64 path.  Half 0 also forms Σ r x and N_k.
+constexpr int kS128Tiles = 5;
+constexpr int kS128I[2][kS128Tiles] = {{0, 3, 3, 3, 3}, {1, 1, 2, 2, 2}};
+constexpr int kS128J[2][kS128Tiles] = {{0, 0, 1, 2, 3}, {0, 1, 0, 1, 2}};
+
+template <int Q>
+__device__ __forceinline__ void fw_stats128_half(const FwArgs& a, int k, int lane) {
+  constexpr int DP = 128, NT = 4;
+  constexpr int ND = Q == 0 ? 4 : 3;          // dims (32-wide) this half's tiles read
+  const int lr = lane & 31, h = lane >> 5;
+  const int b = blockIdx.z;
+  const int64_t N = a.N;
+  const int D = a.D;
+  const size_t bk = (size_t)b * a.K + k;
+  const int64_t r0 = (int64_t)blockIdx.x * a.rows_per_slice;
+  const int64_t r1 = (r0 + a.rows_per_slice < N) ? r0 + a.rows_per_slice : N;
+  const float* xb = a.x + (size_t)b * N * D;
+  const float* l2 = a.hard ? nullptr : a.l2 + bk * N;
+  const float* lse2 = a.lse2 + (size_t)b * N;
+  const int* hidx = a.hard ? a.hard_idx + (size_t)b * N : nullptr;
+  const float* thr = a.thr2 ? a.thr2 + (size_t)b * N : nullptr;   // top-k mode
+  const int* thri = a.thr2 ? a.thr_idx + (size_t)b * N : nullptr;
+
+  f32x16 acc[kS128Tiles];
+#pragma unroll
+  for (int i = 0; i < kS128Tiles; ++i) acc[i] = f32x16{};
+  float sx[NT];
+#pragma unroll
+  for (int c = 0; c < NT; ++c) sx[c] = 0.f;
+  float sr = 0.f;
+
+  for (int64_t n0 = r0; n0 < r1; n0 += 32) {
+    const int64_t nr = n0 + lr;
+    float rv = 0.f;
+    if (nr < r1) {
+      if (a.hard) {
+        rv = hidx[nr] == k ? 1.f : 0.f;
+      } else {
+        const float l = l2[nr];
+        const bool keep = !thr || l > thr[nr] || (l == thr[nr] && k <= thri[nr]);
+        rv = keep ? fast_exp2(l - lse2[nr]) : 0.f;
+      }
+    }
+    const float* xblk = xb + (size_t)n0 * D;
+    const int nrows = (int)((r1 - n0) < 32 ? (r1 - n0) : 32);
+#pragma unroll 1
+    for (int s0 = 0; s0 < 32; s0 += 16) {
+      f32x8 sq, xv[ND];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int src = s0 + 8 * h + e;
+        const float r = __shfl(rv, src);
+        if (Q == 0) sr += r;
+        sq[e] = __builtin_amdgcn_sqrtf(r);
+        const bool rowok = src < nrows;
+#pragma unroll
+        for (int c = 0; c < ND; ++c) {
+          const int col = 32 * c + lr;
+          xv[c][e] = (rowok && col < D) ? xblk[src * D + col] : 0.f;
+        }
+      }
+      bf16x8v w1[ND], w2[ND], w3[ND];
+#pragma unroll
+      for (int c = 0; c < ND; ++c) {
+        const f32x8 w = xv[c] * sq;
+        if (Q == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sx[c] = fmaf(sq[e], w[e], sx[c]);
+        }
+        split3v(w, w1[c], w2[c], w3[c]);
+      }
+      auto products = [&](const bf16x8v (&pa)[ND], const bf16x8v (&pb)[ND]) {
+#pragma unroll
+        for (int t = 0; t < kS128Tiles; ++t) acc[t] = mfma32b(pa[kS128I[Q][t]], pb[kS128J[Q][t]], acc[t]);
+      };
+      products(w1, w3);
+      products(w3, w1);
+      products(w2, w2);
+      products(w1, w2);
+      products(w2, w1);
+      products(w1, w1);
+    }
+  }
+
+  float* out = a.part_stats + (((size_t)blockIdx.x * a.B + b) * a.K + k) * a.JP;
+  if (Q == 0) {
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+      const float tot = half_sum(sx[c]);
+      if (h == 0) out[32 * c + lr] = tot;
+    }
+    const float nk = half_sum(sr);
+    if (lane == 0) out[a.nk_col] = nk;
+    if (lane >= 1 && a.nk_col + lane < a.JP) out[a.nk_col + lane] = 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < kS128Tiles; ++t)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int gi = 32 * kS128I[Q][t] + 8 * (v / 4) + 4 * h + (v % 4), gj = 32 * kS128J[Q][t] + lr;
+      if (gi >= gj) out[DP + fw_tri(DP, gj, gi)] = acc[t][v];
+    }
+}
+
+__global__ __launch_bounds__(64 * kFwWaves) void fw_stats128_kernel(FwArgs a) {
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int k = blockIdx.y * (kFwWaves / 2) + wave / 2;
+  if (k >= a.K) return;   // whole wave; the kernel has no barrier
+  if (wave % 2 == 0) fw_stats128_half<0>(a, k, lane);
+  else fw_stats128_half<1>(a, k, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -465,6 +555,8 @@ template <int DP>
 static void launch_fw_dp(int phase, const FwArgs& a, int slices, hipStream_t s) {
   if (phase == 0)
     fw_estep_kernel<DP><<<dim3(fw_eblocks(a.N), a.B), 64 * kFwWaves, 0, s>>>(a);
+  else if constexpr (DP == 128)
+    fw_stats128_kernel<<<dim3(slices, (a.K + kFwWaves / 2 - 1) / (kFwWaves / 2), a.B), 64 * kFwWaves, 0, s>>>(a);
   else
     fw_stats_kernel<DP><<<dim3(slices, (a.K + kFwWaves - 1) / kFwWaves, a.B), 64 * kFwWaves, 0, s>>>(a);
 }
