@@ -647,12 +647,12 @@ __global__ __launch_bounds__(64 * chol_waves<DP>()) void chol_one_kernel(const f
 // the same ladder as above: chol128_try finds each matrix's first factorising
 // level and keeps that factor, chol128_finish takes it when the batch level is
 // the matrix's own (else factorises at the batch level) and writes X = L^-1
-// (one thread per column, forward substitution), P = XᵀX and 2 Σ log L_jj.  A
+// (eight lanes per column, forward substitution), P = XᵀX and 2 Σ log L_jj.  A
 // wave per matrix cannot hold a 128-row panel, and these sizes are rare, so
 // simplicity wins over the blocked MFMA path.
 // ---------------------------------------------------------------------------
 
-constexpr int kChol128Threads = 256;
+constexpr int kChol128Threads = 1024;
 constexpr int kChol128RS = 129;   // row stride (floats)
 
 // A = sym(C) + jitter·I (lower triangle) into LDS, then factorised in place;
@@ -679,12 +679,12 @@ __device__ bool chol128_factor(const float* C, int D, float jitter, float* A) {
       colk[i] = v;
     }
     __syncthreads();
-    // trailing update A[i][j] -= L[i][k] L[j][k], k < j <= i: row k + 1 + t/2, columns of
-    // parity t & 1; the column is read from colk, a separate array, so the loads of one
-    // row's updates need not wait for its stores
-    for (int i = k + 1 + (t >> 1); i < D; i += kChol128Threads / 2) {
+    // trailing update A[i][j] -= L[i][k] L[j][k], k < j <= i: row k + 1 + t/8, columns
+    // j ≡ k + 1 + t (mod 8); the column is read from colk, a separate array, so the
+    // loads of one row's updates need not wait for its stores
+    for (int i = k + 1 + (t >> 3); i < D; i += kChol128Threads / 8) {
       const float lik = colk[i];
-      for (int j = k + 1 + (t & 1); j <= i; j += 2) A[i * kChol128RS + j] = fmaf(-lik, colk[j], A[i * kChol128RS + j]);
+      for (int j = k + 1 + (t & 7); j <= i; j += 8) A[i * kChol128RS + j] = fmaf(-lik, colk[j], A[i * kChol128RS + j]);
     }
     __syncthreads();
   }
@@ -749,14 +749,20 @@ __global__ __launch_bounds__(kChol128Threads) void chol128_finish_kernel(const f
     (void)chol128_factor(cov + (size_t)m * D * D, D, jitter_of(lv), A);
   }
   __syncthreads();
-  // X = L^-1, thread c owns column c
-  if (t < D) {
-    const int c = t;
-    for (int r = 0; r < c; ++r) X[r * kChol128RS + c] = 0.f;
+  // X = L^-1 by forward substitution, column c owned by the eight consecutive
+  // lanes 8c .. 8c+7 (one wave): lane s sums k ≡ c + s (mod 8), the eight partial
+  // sums are added by a fixed xor tree, lane 0 stores X[r][c], which the group's
+  // later reads see (LDS operations of one wave execute in order)
+  if (t < 8 * D) {
+    const int c = t >> 3, s = t & 7;
+    for (int r = s; r < c; r += 8) X[r * kChol128RS + c] = 0.f;
     for (int r = c; r < D; ++r) {
       float acc = 0.f;
-      for (int k = c; k < r; ++k) acc = fmaf(A[r * kChol128RS + k], X[k * kChol128RS + c], acc);
-      X[r * kChol128RS + c] = ((r == c) ? 1.f : -acc) / A[r * kChol128RS + r];
+      for (int k = c + s; k < r; k += 8) acc = fmaf(A[r * kChol128RS + k], X[k * kChol128RS + c], acc);
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      acc += __shfl_xor(acc, 4);
+      if (s == 0) X[r * kChol128RS + c] = ((r == c) ? 1.f : -acc) / A[r * kChol128RS + r];
     }
   }
   __syncthreads();
