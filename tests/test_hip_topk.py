@@ -40,6 +40,8 @@ CASES = [
     ("full", 2, 5000, 40, 6, torch.float32, 1),              # D > 16: hard assignment on the whitening kernels
     ("full", 1, 6000, 64, 5, torch.float32, 2),              # D > 16: transposed logits, top-k selection
     ("full", 2, 3000, 24, 9, torch.float32, 8),              # D > 16, top_k = K - 1
+    ("full", 1, 4000, 100, 5, torch.float32, 1),             # 64 < D <= 128: two-wave statistics, hard
+    ("full", 2, 3000, 128, 6, torch.float32, 3),             # D = 128: two-wave statistics, top-k
 ]
 
 
