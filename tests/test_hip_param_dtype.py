@@ -23,8 +23,10 @@ from tests.test_hip_parity import make_problem, to_dev
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
-CASES = [("diag", torch.bfloat16), ("tied", torch.bfloat16), ("full", torch.bfloat16),
-         ("diag", torch.float16), ("tied", torch.float16), ("full", torch.float16)]
+CASES = [("diag", torch.bfloat16, 12), ("tied", torch.bfloat16, 12), ("full", torch.bfloat16, 12),
+         ("diag", torch.float16, 12), ("tied", torch.float16, 12), ("full", torch.float16, 12),
+         # D > 16: the whitening kernels (the prelude's rounding in their packing kernel)
+         ("full", torch.bfloat16, 40), ("full", torch.float16, 40)]
 
 
 def _ulp(t: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
@@ -42,10 +44,10 @@ def _close_half(got, exp, dt, what):
     assert bool((diff <= bar).all()), f"{what}: largest |Δ| {float(diff.max()):.3e}"
 
 
-@pytest.mark.parametrize("cov,dt", CASES, ids=[f"{c}-{str(d).split('.')[-1]}" for c, d in CASES])
-def test_fit_with_half_parameters_matches_oracle(hip, cov, dt):
-    print(f"[param dtype] {cov} {dt}", flush=True)
-    x, means, covs, w = make_problem(cov, 2, 6000, 12, 5, seed=71, dtype=dt)
+@pytest.mark.parametrize("cov,dt,d", CASES, ids=[f"{c}-{str(t).split('.')[-1]}-D{d}" for c, t, d in CASES])
+def test_fit_with_half_parameters_matches_oracle(hip, cov, dt, d):
+    print(f"[param dtype] {cov} {dt} D={d}", flush=True)
+    x, means, covs, w = make_problem(cov, 2, 6000, d, 5, seed=71, dtype=dt)
     _, e_m, e_c, e_w, e_info = torch_ref.fit(x.to(dt), 5, cov, max_iters=5, tol=0.0, init_means=means,
                                              init_covs=covs, init_weights=w, compute_labels=False)
     _, m, c, wt, info = em.fit(to_dev(x), 5, cov, max_iters=5, tol=0.0, init_means=means, init_covs=covs,
