@@ -54,17 +54,40 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x16 mfma32b(bf16x8v a, bf16x8v b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // v = p1 + p2 + p3 exactly (three bf16 parts, each rounded to nearest even).
+// The residuals v - p come from v_dot2_f32_bf16 against (-1, 0) / (0, -1), one
+// instruction per value instead of a widening and a subtraction (the difference
+// is exact, so the bits equal the subtract's for every finite input; a NaN or an
+// infinity also turns its pair partner's lower parts into NaN).  The two
+// constants pass through an empty asm so that they stay register operands: as
+// an inline constant the compiler encodes (-1, 0) as the fp32 -1.0, whose bits
+// the instruction reads as (0, -1).
 __device__ __forceinline__ void split3v(f32x8 v, bf16x8v& p1, bf16x8v& p2, bf16x8v& p3) {
+  uint32_t clo = 0x0000BF80u, chi = 0xBF800000u;
+  asm("" : "+v"(clo), "+v"(chi));
+  const bf16x2 nlo = __builtin_bit_cast(bf16x2, clo), nhi = __builtin_bit_cast(bf16x2, chi);
   p1 = __builtin_convertvector(v, bf16x8v);
-  const f32x8 r1 = v - __builtin_convertvector(p1, f32x8);
+  f32x8 r1, r2;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const bf16x2 q = bf16x2{p1[e], p1[e + 1]};
+    r1[e] = __builtin_amdgcn_fdot2_f32_bf16(q, nlo, v[e], false);
+    r1[e + 1] = __builtin_amdgcn_fdot2_f32_bf16(q, nhi, v[e + 1], false);
+  }
   p2 = __builtin_convertvector(r1, bf16x8v);
-  p3 = __builtin_convertvector(r1 - __builtin_convertvector(p2, f32x8), bf16x8v);
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const bf16x2 q = bf16x2{p2[e], p2[e + 1]};
+    r2[e] = __builtin_amdgcn_fdot2_f32_bf16(q, nlo, r1[e], false);
+    r2[e + 1] = __builtin_amdgcn_fdot2_f32_bf16(q, nhi, r1[e + 1], false);
+  }
+  p3 = __builtin_convertvector(r2, bf16x8v);
 }
 
 // Bytes of one 16-deep L⁻¹ chunk: three parts x 64 lanes x 8 bf16.
