@@ -228,11 +228,15 @@ int plan_problem(const gmmxx_problem* p, Plan* pl) {
   q.gram_slices = (int)((q.N + q.gram_rows - 1) / q.gram_rows);
   q.chol_m = (q.cov == TIED) ? q.B : (q.cov == FULL ? q.B * q.K : 0);
   if (q.fw) {
-    // E-step: one wave per 32-row block.  Statistics: one wave per component,
-    // about 2048 workgroups of four components over row slices.
+    // E-step: one wave per 32-row block.  Statistics: workgroups of four waves
+    // (four components; at D = 128 two components of two waves) over row slices,
+    // as many as one round of resident waves: 8, 4 and 2 waves per SIMD at
+    // DP = 32, 64 and 128 (the kernels' register counts), so 2048, 1024 and 512
+    // workgroups (at D = 64, 2048 measured 5 % slower per EM iteration).
     q.fw_eblk = fw_eblocks(q.N);
-    const int64_t groups = (int64_t)((q.K + 3) / 4) * q.B;
-    int64_t fs = std::max<int64_t>(1, (2048 + groups - 1) / groups);
+    const int64_t groups = (int64_t)(q.DP == 128 ? (q.K + 1) / 2 : (q.K + 3) / 4) * q.B;
+    const int64_t target = q.DP == 32 ? 2048 : (q.DP == 64 ? 1024 : 512);
+    int64_t fs = std::max<int64_t>(1, (target + groups - 1) / groups);
     fs = std::min(fs, std::max<int64_t>(1, row_blocks / kMinBlocksPerSlice));
     q.fw_rows = ((q.N + fs - 1) / fs + kBN - 1) / kBN * kBN;
     q.fw_slices = (int)((q.N + q.fw_rows - 1) / q.fw_rows);
